@@ -1,0 +1,205 @@
+// KV-cache append and interleaved RoPE for gfx950.
+//
+// delta_append_kv replaces mylib::update_kv (hoenza/DELTA utils.py:31-79),
+// which chains FlashInfer get_seq_lens -> get_batch_indices_positions ->
+// append_paged_kv_cache.  One block per appended token; each thread moves 16
+// bytes of K or V into page kv_indices[kv_indptr[b] + pos/16], slot pos % 16.
+//
+// delta_rope replaces mylib::rope (model.py:152-175: FlashInfer apply_rope /
+// apply_llama31_rope with interleave=True).  Published formula: pair
+// (2j, 2j+1) of every head rotates by angle pos * f_j with
+// f_j = theta^(-2j/d) / rope_scale, or for Llama 3.1 the blend
+// (1 - s) f_j/rope_scale + s f_j, s = clamp(f_j * old_ctx / (2 pi (hi - lo)) - 1/(hi/lo - 1), 0, 1).
+// fp32 angle and fp32 sin/cos as the reference's kernel; fp32 rotation, one
+// rounding to the storage dtype.
+#include "delta_common.h"
+
+namespace delta {
+namespace {
+
+// Row of token i under a CSR indptr (uniform binary search).
+__device__ __forceinline__ int find_row(const int32_t *indptr, int batch, int i) {
+  int lo = 0, hi = batch;  // indptr[lo] <= i < indptr[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (indptr[mid] <= i)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+struct AppendArgs {
+  const uint16_t *k;
+  int64_t k_stride;
+  const uint16_t *v;
+  int64_t v_stride;
+  const int32_t *append_indptr;
+  uint16_t *cache;
+  int64_t num_pages;
+  const int32_t *kv_indices;
+  int64_t kv_indices_len;
+  const int32_t *kv_indptr;
+  const int32_t *last_page_len;
+  int batch, hkv;
+};
+
+__global__ void __launch_bounds__(256) append_kv_kernel(AppendArgs a) {
+  const int i = blockIdx.x;
+  const int b = find_row(a.append_indptr, a.batch, i);
+  const int a0 = a.append_indptr[b];
+  const int alen = a.append_indptr[b + 1] - a0;
+  if (i < a0 || i - a0 >= alen) return;
+  int64_t p0 = a.kv_indptr[b], p1 = a.kv_indptr[b + 1];
+  if (p0 < 0 || p1 < p0 || p1 > a.kv_indices_len) return;
+  const int np = (int)(p1 - p0);
+  int lp = a.last_page_len[b];
+  lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+  const int seq = np > 0 ? (np - 1) * kPageSize + lp : lp;
+  const int pos = seq - alen + (i - a0);
+  if (pos < 0 || pos / kPageSize >= np) return;
+  const int pid = a.kv_indices[p0 + pos / kPageSize];
+  if (pid < 0 || (int64_t)pid >= a.num_pages) return;
+  const int slot = pos % kPageSize;
+  const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
+  const int chunks = a.hkv * (kHeadDim / 8);  // 16-byte chunks per token row
+  for (int ch = threadIdx.x; ch < 2 * chunks; ch += blockDim.x) {
+    const int which = ch >= chunks;  // 0 = K, 1 = V
+    const int r = which ? ch - chunks : ch;
+    const uint16_t *src = which ? a.v + (int64_t)i * a.v_stride : a.k + (int64_t)i * a.k_stride;
+    uint16_t *dst = a.cache + (((int64_t)pid * 2 + which) * kPageSize + slot) * row_elems;
+    st128(dst + 8 * r, ld128(src + 8 * r));
+  }
+}
+
+struct RopeArgs {
+  const uint16_t *q;
+  int64_t q_stride;
+  const uint16_t *k;
+  int64_t k_stride;
+  uint16_t *q_out;
+  int64_t q_out_stride;
+  uint16_t *k_out;
+  int64_t k_out_stride;
+  const int32_t *indptr;
+  const int32_t *offsets;
+  int batch, hq, hkv;
+  float rcp_scale, log2_theta, smooth_a, smooth_b;
+};
+
+template <int DT>
+__global__ void __launch_bounds__(256) rope_kernel(RopeArgs a) {
+  using E = Elem<DT>;
+  const int i = blockIdx.x;
+  const int b = find_row(a.indptr, a.batch, i);
+  const float pos = (float)(a.offsets[b] + (i - a.indptr[b]));
+  constexpr int kPairs = kHeadDim / 2;
+  const int total = (a.hq + a.hkv) * kPairs;
+  for (int w = threadIdx.x; w < total; w += blockDim.x) {
+    const int head = w / kPairs;
+    const int j = w % kPairs;
+    float f = exp2f(-(2.0f * (float)j / (float)kHeadDim) * a.log2_theta);  // theta^(-2j/d)
+    float s = fminf(fmaxf(f * a.smooth_a + a.smooth_b, 0.f), 1.f);
+    f = (1.f - s) * (f * a.rcp_scale) + s * f;
+    float sn, cs;
+    sincosf(pos * f, &sn, &cs);
+    const bool is_q = head < a.hq;
+    const uint16_t *src = is_q ? a.q + (int64_t)i * a.q_stride + (int64_t)head * kHeadDim
+                               : a.k + (int64_t)i * a.k_stride + (int64_t)(head - a.hq) * kHeadDim;
+    uint16_t *dst = is_q ? a.q_out + (int64_t)i * a.q_out_stride + (int64_t)head * kHeadDim
+                         : a.k_out + (int64_t)i * a.k_out_stride + (int64_t)(head - a.hq) * kHeadDim;
+    const uint32_t pr = *reinterpret_cast<const uint32_t *>(src + 2 * j);
+    const float x0 = E::lo(pr), x1 = E::hi(pr);
+    const float y0 = x0 * cs - x1 * sn;
+    const float y1 = x1 * cs + x0 * sn;
+    *reinterpret_cast<uint32_t *>(dst + 2 * j) = E::from_float(y0) | (E::from_float(y1) << 16);
+  }
+}
+
+}  // namespace
+}  // namespace delta
+
+extern "C" DELTA_EXPORT int delta_append_kv(const void *k, int64_t k_stride, const void *v, int64_t v_stride,
+                                            const int32_t *kv_append_indptr, void *kv_cache, int64_t num_pages,
+                                            const int32_t *kv_indices, int64_t kv_indices_len,
+                                            const int32_t *kv_indptr, const int32_t *kv_last_page_len, int nnz,
+                                            int batch, int num_kv_heads, int head_dim, int dtype,
+                                            delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_append_kv";
+  if (nnz <= 0 || batch <= 0) return DELTA_OK;
+  if (head_dim != kHeadDim) return set_error(DELTA_ERR_INVALID, "%s: head_dim must be 128", who);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: bad dtype", who);
+  if (!k || !v || !kv_append_indptr || !kv_cache || !kv_indices || !kv_indptr || !kv_last_page_len)
+    return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)kv_cache) & 15u || (k_stride % 8) || (v_stride % 8))
+    return set_error(DELTA_ERR_INVALID, "%s: k/v/cache must be 16-byte aligned with strides in multiples of 8", who);
+  AppendArgs a;
+  a.k = (const uint16_t *)k;
+  a.k_stride = k_stride;
+  a.v = (const uint16_t *)v;
+  a.v_stride = v_stride;
+  a.append_indptr = kv_append_indptr;
+  a.cache = (uint16_t *)kv_cache;
+  a.num_pages = num_pages;
+  a.kv_indices = kv_indices;
+  a.kv_indices_len = kv_indices_len;
+  a.kv_indptr = kv_indptr;
+  a.last_page_len = kv_last_page_len;
+  a.batch = batch;
+  a.hkv = num_kv_heads;
+  const int threads = 2 * num_kv_heads * (kHeadDim / 8) >= 256 ? 256 : 128;
+  hipLaunchKernelGGL(append_kv_kernel, dim3(nnz), dim3(threads), 0, (hipStream_t)stream, a);
+  return check_launch(who);
+}
+
+extern "C" DELTA_EXPORT int delta_rope(const void *q, int64_t q_stride, const void *k, int64_t k_stride, void *q_out,
+                                       int64_t q_out_stride, void *k_out, int64_t k_out_stride, const int32_t *indptr,
+                                       const int32_t *offsets, int nnz, int batch, int num_qo_heads, int num_kv_heads,
+                                       int head_dim, int dtype, float rope_scale, float rope_theta, int llama31,
+                                       float low_freq_factor, float high_freq_factor, float old_context_len,
+                                       delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_rope";
+  if (nnz <= 0 || batch <= 0) return DELTA_OK;
+  if (head_dim != kHeadDim) return set_error(DELTA_ERR_INVALID, "%s: head_dim must be 128", who);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: bad dtype", who);
+  if (!q || !k || !q_out || !k_out || !indptr || !offsets) return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)q_out | (uintptr_t)k_out) & 3u)
+    return set_error(DELTA_ERR_INVALID, "%s: tensors must be 4-byte aligned", who);
+  if (!(rope_scale > 0.f) || !(rope_theta > 0.f)) return set_error(DELTA_ERR_INVALID, "%s: bad rope params", who);
+  RopeArgs a;
+  a.q = (const uint16_t *)q;
+  a.q_stride = q_stride;
+  a.k = (const uint16_t *)k;
+  a.k_stride = k_stride;
+  a.q_out = (uint16_t *)q_out;
+  a.q_out_stride = q_out_stride;
+  a.k_out = (uint16_t *)k_out;
+  a.k_out_stride = k_out_stride;
+  a.indptr = indptr;
+  a.offsets = offsets;
+  a.batch = batch;
+  a.hq = num_qo_heads;
+  a.hkv = num_kv_heads;
+  a.rcp_scale = 1.0f / rope_scale;
+  a.log2_theta = log2f(rope_theta);
+  if (llama31) {
+    if (!(high_freq_factor > low_freq_factor) || !(low_freq_factor > 0.f))
+      return set_error(DELTA_ERR_INVALID, "%s: bad llama3.1 frequency factors", who);
+    const float two_pi = 6.283185307179586f;
+    a.smooth_a = old_context_len / (two_pi * high_freq_factor - two_pi * low_freq_factor);
+    a.smooth_b = -1.0f / (high_freq_factor / low_freq_factor - 1.0f);
+  } else {
+    a.smooth_a = 0.f;
+    a.smooth_b = 0.f;
+  }
+  if (dtype == DELTA_BF16)
+    hipLaunchKernelGGL(rope_kernel<DELTA_BF16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(rope_kernel<DELTA_FP16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch(who);
+}

@@ -1,0 +1,197 @@
+// del3_legacy_softmax page scores for gfx950.
+//
+// Restates hoenza/DELTA backend.py:887-904:
+//   probs  = softmax_t(dump[b, h, :max_pages*16])        (per q head)
+//   score  = sum_{t in page j} max_h probs[b, h, t]
+// The softmax normaliser of each (row, head) is its log-sum-exp: either the
+// lse the decode kernel produced for the same logits, or (lse == NULL) a first
+// pass over the dump.  Positions t >= kv_len_b hold -inf in the reference's
+// buffer (backend.py:384-389); they contribute exp(-inf) = 0 and are not read.
+//
+// Score kernel: grid (ceil(max_pages*16 / 256), batch), 256 threads, one
+// token per thread; per head a fully coalesced 1 KiB read of the dump; the
+// 16-token page sum is a DPP reduction inside each 16-lane row.
+//
+// HBM bytes per launch (algorithmic): the dump rows up to kv_len (read once),
+// lse, page table, scores.
+#include "delta_common.h"
+
+namespace delta {
+
+int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *kv_cache,
+               int64_t num_pages, const int32_t *kv_indptr, const int32_t *kv_indices,
+               int64_t kv_indices_len, const int32_t *kv_last_page_len, void *o,
+               int64_t o_stride_b, int64_t o_stride_h, float *lse, float *dump,
+               int64_t dump_stride_b, int64_t dump_stride_h, int batch, int hq, int hkv,
+               int head_dim, int dtype, float sm_scale, int max_pages, int mode,
+               void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who);
+int decode_num_splits(int batch, int hkv, int max_pages);
+
+namespace {
+
+constexpr int kScoreThreads = 256;
+constexpr int kMaxHeads = 256;
+
+__device__ __forceinline__ int row_kv_len(const int32_t *kv_indptr, const int32_t *last, int b) {
+  int np = kv_indptr[b + 1] - kv_indptr[b];
+  np = np < 0 ? 0 : np;
+  int lp = last[b];
+  lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+  return np > 0 ? (np - 1) * kPageSize + lp : 0;
+}
+
+// lse of one (row, head) dump row over t < kv_len (natural log).
+__global__ void __launch_bounds__(256) dump_lse_kernel(const float *dump, int64_t sdb, int64_t sdh,
+                                                        const int32_t *kv_indptr, const int32_t *last,
+                                                        float *lse, int hq, int cap) {
+  __shared__ float red[4];
+  const int b = blockIdx.x / hq;
+  const int h = blockIdx.x % hq;
+  const int n = min(row_kv_len(kv_indptr, last, b), cap);
+  const float *row = dump + (int64_t)b * sdb + (int64_t)h * sdh;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float mx = -INFINITY;
+  for (int t = threadIdx.x; t < n; t += 256) mx = fmaxf(mx, row[t]);
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, shfl_xor(mx, off));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  const float mref = mx == -INFINITY ? 0.f : mx;
+  float s = 0.f;
+  for (int t = threadIdx.x; t < n; t += 256) s += fast_exp2((row[t] - mref) * kLog2e);
+  for (int off = 32; off > 0; off >>= 1) s += shfl_xor(s, off);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float tot = red[0] + red[1] + red[2] + red[3];
+    lse[(int64_t)b * hq + h] = tot > 0.f ? mref + logf(tot) : -INFINITY;
+  }
+}
+
+__global__ void __launch_bounds__(kScoreThreads)
+    legacy_softmax_score_kernel(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
+                                const int32_t *kv_indptr, const int32_t *last, float *scores,
+                                int64_t score_stride, int hq, int max_pages) {
+  __shared__ float s_lse2[kMaxHeads];
+  const int b = blockIdx.y;
+  for (int h = threadIdx.x; h < hq; h += kScoreThreads) {
+    const float v = lse[(int64_t)b * hq + h];
+    s_lse2[h] = v * kLog2e;
+  }
+  __syncthreads();
+  const int n = min(row_kv_len(kv_indptr, last, b), max_pages * kPageSize);
+  const int tok = blockIdx.x * kScoreThreads + threadIdx.x;
+  const float *col = dump + (int64_t)b * sdb + tok;
+  float best = 0.f;
+  if (tok < n) {
+    int h = 0;
+    for (; h + 4 <= hq; h += 4) {
+      const float x0 = col[(int64_t)(h + 0) * sdh];
+      const float x1 = col[(int64_t)(h + 1) * sdh];
+      const float x2 = col[(int64_t)(h + 2) * sdh];
+      const float x3 = col[(int64_t)(h + 3) * sdh];
+      best = fmaxf(best, fast_exp2(x0 * kLog2e - s_lse2[h + 0]));
+      best = fmaxf(best, fast_exp2(x1 * kLog2e - s_lse2[h + 1]));
+      best = fmaxf(best, fast_exp2(x2 * kLog2e - s_lse2[h + 2]));
+      best = fmaxf(best, fast_exp2(x3 * kLog2e - s_lse2[h + 3]));
+    }
+    for (; h < hq; ++h) best = fmaxf(best, fast_exp2(col[(int64_t)h * sdh] * kLog2e - s_lse2[h]));
+  }
+  const float page_sum = row16_sum(best);
+  const int page = tok >> 4;
+  if ((threadIdx.x & 15) == 0 && page < max_pages) scores[(int64_t)b * score_stride + page] = page_sum;
+}
+
+int launch_scores(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
+                  const int32_t *kv_indptr, const int32_t *last, float *scores, int64_t score_stride,
+                  int batch, int hq, int max_pages, hipStream_t stream, const char *who) {
+  dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
+  hipLaunchKernelGGL(legacy_softmax_score_kernel, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse,
+                     kv_indptr, last, scores, score_stride, hq, max_pages);
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace delta
+
+extern "C" DELTA_EXPORT size_t delta_page_score_workspace_bytes(int batch, int num_qo_heads) {
+  return ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
+}
+
+extern "C" DELTA_EXPORT int delta_page_scores_from_logits(const float *logits_dump, int64_t dump_stride_b,
+                                                          int64_t dump_stride_h, const float *lse,
+                                                          const int32_t *kv_indptr,
+                                                          const int32_t *kv_last_page_len, float *scores,
+                                                          int64_t score_stride, int batch, int num_qo_heads,
+                                                          int max_pages, void *workspace, size_t workspace_bytes,
+                                                          delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_page_scores_from_logits";
+  if (batch <= 0 || max_pages <= 0) return DELTA_OK;
+  if (!logits_dump || !kv_indptr || !kv_last_page_len || !scores)
+    return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (num_qo_heads <= 0 || num_qo_heads > kMaxHeads)
+    return set_error(DELTA_ERR_INVALID, "%s: num_qo_heads must be in [1, %d]", who, kMaxHeads);
+  if (score_stride < max_pages) return set_error(DELTA_ERR_INVALID, "%s: score_stride < max_pages", who);
+  if (dump_stride_h < (int64_t)max_pages * kPageSize)
+    return set_error(DELTA_ERR_INVALID, "%s: dump rows shorter than max_pages*16", who);
+  hipStream_t st = (hipStream_t)stream;
+  if (!lse) {
+    const size_t need = delta_page_score_workspace_bytes(batch, num_qo_heads);
+    if (!workspace || workspace_bytes < need)
+      return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed", who, need);
+    float *lse_ws = (float *)workspace;
+    hipLaunchKernelGGL(dump_lse_kernel, dim3(batch * num_qo_heads), dim3(256), 0, st, logits_dump, dump_stride_b,
+                       dump_stride_h, kv_indptr, kv_last_page_len, lse_ws, num_qo_heads,
+                       max_pages * kPageSize);
+    int rc = check_launch(who);
+    if (rc) return rc;
+    lse = lse_ws;
+  }
+  return launch_scores(logits_dump, dump_stride_b, dump_stride_h, lse, kv_indptr, kv_last_page_len, scores,
+                       score_stride, batch, num_qo_heads, max_pages, st, who);
+}
+
+extern "C" DELTA_EXPORT size_t delta_page_score_kv_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
+                                                                   int max_pages_per_row) {
+  const int ns = delta::decode_num_splits(batch, num_kv_heads, max_pages_per_row);
+  size_t lse_bytes = ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
+  size_t part = ns > 1 ? (size_t)batch * num_qo_heads * ns * 2 * sizeof(float) : 0;
+  return lse_bytes + part;
+}
+
+extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                             const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr,
+                                             const int32_t *kv_indices, int64_t kv_indices_len,
+                                             const int32_t *kv_last_page_len, float *logits_dump,
+                                             int64_t dump_stride_b, int64_t dump_stride_h, float *scores,
+                                             int64_t score_stride, int batch, int num_qo_heads, int num_kv_heads,
+                                             int head_dim, int dtype, float sm_scale, int max_pages,
+                                             void *workspace, size_t workspace_bytes, delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_page_score";
+  if (batch <= 0 || max_pages <= 0) return DELTA_OK;
+  if (!scores || !logits_dump) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
+  if (num_qo_heads > kMaxHeads) return set_error(DELTA_ERR_INVALID, "%s: too many heads", who);
+  if (score_stride < max_pages) return set_error(DELTA_ERR_INVALID, "%s: score_stride < max_pages", who);
+  if (dump_stride_h < (int64_t)max_pages * kPageSize)
+    return set_error(DELTA_ERR_INVALID, "%s: dump rows shorter than max_pages*16", who);
+  const size_t need = delta_page_score_kv_workspace_bytes(batch, num_qo_heads, num_kv_heads, max_pages);
+  if (!workspace || workspace_bytes < need)
+    return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
+  if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
+  hipStream_t st = (hipStream_t)stream;
+  float *lse_ws = (float *)workspace;
+  const size_t lse_bytes = ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
+  void *part = (char *)workspace + lse_bytes;
+  int rc = run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                      kv_last_page_len, nullptr, 0, 0, lse_ws, logits_dump, dump_stride_b, dump_stride_h, batch,
+                      num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale, max_pages, /*kScoreOnly*/ 2, part,
+                      workspace_bytes - lse_bytes, st, who);
+  if (rc) return rc;
+  return launch_scores(logits_dump, dump_stride_b, dump_stride_h, lse_ws, kv_indptr, kv_last_page_len, scores,
+                       score_stride, batch, num_qo_heads, max_pages, st, who);
+}

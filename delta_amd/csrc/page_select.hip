@@ -1,0 +1,259 @@
+// PageSelectorV2 top-k page selection for gfx950.
+//
+// Restates hoenza/DELTA page_selector_v2.py:113-212 for one row per block:
+//   key_j = nan_to_num(score_j, nan=-inf, neginf=-inf) + fp32(-j * bias)   (113-118)
+//   key_j = +inf for j in [max(tp - L, 0), tp)                               (123-126)
+//   pages j >= tp are not candidates (their key is -inf, 128-129)
+//   top-k of key, ties broken by the smaller page index (torch.topk leaves
+//   tie order unspecified; this build fixes it), positions emitted in
+//   ascending j (132-134) as physical ids from the row's block table (147-150).
+//
+// Algorithm per row (256 threads): fp32 keys map to order-preserving uint32
+// (+0/-0 folded); a 4-pass 8-bit radix select finds the k-th largest key T and
+// how many keys equal to T are taken (r); one ordered pass then marks
+// key > T, or key == T among the first r such pages, and compacts the marked
+// pages in ascending j with ballot prefix sums -- the output is sorted by
+// construction, no sort pass.  Keys are recomputed from the fp32 scores in
+// every pass (they stay in L2), so any row length works.
+#include <float.h>
+
+#include "delta_common.h"
+
+namespace delta {
+namespace {
+
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr uint32_t kKeyPosInf = 0xFF800000u;  // order_key(+inf)
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Prepared fp32 score exactly as the reference's sequence of fp32 tensor ops.
+// The product and the sum are two separately rounded fp32 operations, as the
+// reference's `-arange(n) * scale` followed by `scores.add_(bias)`: contraction
+// into an FMA would change the keys, so it is switched off here.
+__device__ __forceinline__ float prepare(float s, int j, float bias_scale) {
+#pragma clang fp contract(off)
+  if (s != s) s = -INFINITY;           // nan -> -inf
+  else if (s == INFINITY) s = FLT_MAX;  // posinf -> largest finite (nan_to_num default)
+  if (bias_scale != 0.f) {
+    const float bj = (-(float)j) * bias_scale;
+    s = s + bj;
+  }
+  return s == 0.f ? 0.f : s;  // -0 and +0 compare equal
+}
+
+struct SelArgs {
+  const float *scores;
+  int64_t score_stride;
+  const int32_t *kv_indptr;
+  const int32_t *block_table;
+  int64_t bt_stride;
+  int batch, max_pages, k;
+  const int32_t *k_per_row;
+  int L;
+  float bias_scale;
+  int fixed_count;
+  const int32_t *use_subset;
+  int32_t *out_indices;
+  int64_t out_len;  // capacity of out_indices
+  int32_t *out_indptr;
+};
+
+// Pages of row b that can be scored (the reference's Nmax is the largest row,
+// so tp <= max_pages there; a larger row is clamped to max_pages columns).
+__device__ __forceinline__ int row_pages(const SelArgs &a, int b) {
+  const int tp = a.kv_indptr[b + 1] - a.kv_indptr[b];
+  return tp < 0 ? 0 : (tp > a.max_pages ? a.max_pages : tp);
+}
+
+__device__ __forceinline__ int row_budget(const SelArgs &a, int b) {
+  int kb = a.k_per_row ? a.k_per_row[b] : a.k;
+  kb = kb < 0 ? 0 : kb;
+  return kb > a.max_pages ? a.max_pages : kb;
+}
+
+// Number of pages row b emits.
+__device__ __forceinline__ int row_count(const SelArgs &a, int b, bool subset) {
+  const int tp = row_pages(a, b);
+  if (!subset) return tp;
+  const int kb = row_budget(a, b);
+  if (a.fixed_count) return kb;
+  return tp < kb ? tp : kb;
+}
+
+// Block-wide sum (all threads receive it).
+__device__ int block_sum(int v, int *scratch) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  int s = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) s += scratch[w];
+  __syncthreads();
+  return s;
+}
+
+// Exclusive block prefix of a 0/1 flag in thread order; *total gets the block total.
+__device__ int block_prefix(bool flag, int *scratch, int *total) {
+  int wtot;
+  const int wpre = wave_prefix_exclusive(flag, &wtot);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) scratch[wave] = wtot;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int x = scratch[w];
+    before += w < wave ? x : 0;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + wpre;
+}
+
+__global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
+  __shared__ int s_scratch[kSelWaves];
+  __shared__ uint32_t s_hist[256];
+  __shared__ int s_digit, s_remaining;
+
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const bool subset = a.use_subset == nullptr || a.use_subset[0] != 0;
+
+  // Output offset of this row: sum of the counts of the rows before it.
+  int before = 0;
+  if (subset && a.fixed_count) {
+    before = b * row_budget(a, 0);
+  } else {
+    int part = 0;
+    for (int i = tid; i < b; i += kSelThreads) part += row_count(a, i, subset);
+    before = block_sum(part, s_scratch);
+  }
+  const int cnt = row_count(a, b, subset);
+  if (tid == 0) {
+    a.out_indptr[b + 1] = before + cnt;
+    if (b == 0) a.out_indptr[0] = 0;
+  }
+
+  const int tp = row_pages(a, b);
+  const int kb = row_budget(a, b);
+  const int32_t *bt = a.block_table + (int64_t)b * a.bt_stride;
+  int32_t *out = a.out_indices + before;
+  // Never write past the caller's buffer (the indptr above still says what was meant).
+  const int64_t room = a.out_len - (int64_t)before;
+  const int lim = room <= 0 ? 0 : (room < cnt ? (int)room : cnt);
+
+  // Every page of the row is taken (no subset, or fewer pages than the
+  // budget): the ascending top-k is 0..cnt-1 (for the fixed path with
+  // tp < k the padding columns tp..k-1 follow, as torch.topk over -inf).
+  if (!subset || tp <= kb) {
+    for (int j = tid; j < lim; j += kSelThreads) out[j] = bt[j];
+    return;
+  }
+
+  const int last_start = tp - a.L > 0 ? tp - a.L : 0;
+  auto key_of = [&](int j) -> uint32_t {
+    if (j >= last_start) return kKeyPosInf;
+    return order_key(prepare(a.scores[(int64_t)b * a.score_stride + j], j, a.bias_scale));
+  };
+
+  // Radix select of the kb-th largest key.
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = kb;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    s_hist[tid] = 0;
+    __syncthreads();
+    for (int j = tid; j < tp; j += kSelThreads) {
+      const uint32_t key = key_of(j);
+      if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    // Suffix sums over the 256 bins: suf[d] = #keys with digit >= d.
+    const int lane = tid & 63, wave = tid >> 6;
+    const int hd = (int)s_hist[tid];
+    int suf = hd;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_down(suf, off);
+      if (lane + off < 64) suf += y;
+    }
+    if (lane == 0) s_scratch[wave] = suf;
+    __syncthreads();
+    for (int w = wave + 1; w < kSelWaves; ++w) suf += s_scratch[w];
+    if (suf >= remaining && suf - hd < remaining) {
+      s_digit = tid;
+      s_remaining = remaining - (suf - hd);
+    }
+    __syncthreads();
+    prefix |= (uint32_t)s_digit << shift;
+    pmask |= 0xFFu << shift;
+    remaining = s_remaining;
+    __syncthreads();
+  }
+  const uint32_t T = prefix;
+  const int take_eq = remaining;  // how many keys == T are selected (smallest j first)
+
+  // Ordered compaction.
+  int eq_seen = 0, written = 0;
+  for (int base = 0; base < tp; base += kSelThreads) {
+    const int j = base + tid;
+    const uint32_t key = j < tp ? key_of(j) : 0u;
+    const bool eq = j < tp && key == T;
+    int eq_tot;
+    const int eq_rank = eq_seen + block_prefix(eq, s_scratch, &eq_tot);
+    const bool sel = j < tp && (key > T || (eq && eq_rank < take_eq));
+    int sel_tot;
+    const int pos = written + block_prefix(sel, s_scratch, &sel_tot);
+    if (sel && pos < lim) out[pos] = bt[j];
+    eq_seen += eq_tot;
+    written += sel_tot;
+  }
+}
+
+}  // namespace
+}  // namespace delta
+
+extern "C" DELTA_EXPORT int delta_select_pages(const float *scores, int64_t score_stride, const int32_t *kv_indptr,
+                                               const int32_t *block_table, int64_t bt_stride, int batch,
+                                               int max_pages, int k, const int32_t *k_per_row, int L,
+                                               float pos_bias_scale, int fixed_count, const int32_t *use_subset,
+                                               int32_t *out_indices, int64_t out_indices_len, int32_t *out_indptr,
+                                               delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_select_pages";
+  if (batch <= 0) return DELTA_OK;
+  if (!scores || !kv_indptr || !block_table || !out_indices || !out_indptr)
+    return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (max_pages <= 0) return set_error(DELTA_ERR_INVALID, "%s: max_pages must be positive", who);
+  if (score_stride < max_pages || bt_stride < max_pages)
+    return set_error(DELTA_ERR_INVALID, "%s: row strides must be >= max_pages", who);
+  if (fixed_count && k_per_row) return set_error(DELTA_ERR_INVALID, "%s: fixed_count needs a global k", who);
+  if (!k_per_row && k > max_pages)
+    return set_error(DELTA_ERR_INVALID, "%s: selected index k out of range (k=%d > %d pages)", who, k, max_pages);
+  if (L < 0) return set_error(DELTA_ERR_INVALID, "%s: L must be >= 0", who);
+  SelArgs a;
+  a.scores = scores;
+  a.score_stride = score_stride;
+  a.kv_indptr = kv_indptr;
+  a.block_table = block_table;
+  a.bt_stride = bt_stride;
+  a.batch = batch;
+  a.max_pages = max_pages;
+  a.k = k;
+  a.k_per_row = k_per_row;
+  a.L = L;
+  a.bias_scale = pos_bias_scale;
+  a.fixed_count = fixed_count;
+  a.use_subset = use_subset;
+  a.out_indices = out_indices;
+  a.out_len = out_indices_len;
+  a.out_indptr = out_indptr;
+  hipLaunchKernelGGL(select_pages_kernel, dim3(batch), dim3(kSelThreads), 0, (hipStream_t)stream, a);
+  return check_launch(who);
+}

@@ -1,0 +1,510 @@
+// Paged decode attention for gfx950 (one query token per row, GQA).
+//
+// Replaces FlashInfer's paged attention run with qo_len = 1
+// (hoenza/DELTA backend.py:461-512, plan at 1091-1105) and the planner layer's
+// BatchDumpAttentionWeights logits side-write (backend.py:175-222, 518-585).
+//
+// Work decomposition
+//   grid  = (num_splits, num_kv_heads, batch); block = 4 waves (256 threads).
+//   A block owns one (row, kv head, split) and its 4 waves take the split's
+//   pages round robin, so a block streams 4 consecutive pages of one head.
+//   Per page and wave:
+//     q.K  : 4 x v_mfma_f32_16x16x32_{bf16,f16}.  A = the G query heads of the
+//            group (rows g = lane%16, zero padded to 16), B = the page's 16 K
+//            rows (cols t = lane%16).  Lane group c = lane/16 supplies
+//            d in [32s + 8c, 32s + 8c + 8) at step s, so each load instruction
+//            covers 16 rows x 64 contiguous bytes.
+//     softmax: online, log2 domain, DPP reductions across the 16-lane rows.
+//     P.V  : VALU fp32 FMA; lane (c, t) owns d in [8t, 8t+8) of V rows
+//            c, c+4, c+8, c+12 (each load instruction covers 4 full rows).
+//   The 4 waves merge in LDS; with num_splits > 1 the block writes an
+//   un-normalised partial (acc, m, l) and a merge kernel combines the splits.
+//
+// HBM bytes per launch (algorithmic): K and V of every attended token once,
+// q and o once, the page indices once (+ the fp32 logits when dumping).
+#include "delta_common.h"
+
+namespace delta {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+struct DecodeArgs {
+  const uint16_t *q;
+  int64_t q_stride_b, q_stride_h;
+  const uint16_t *kv;
+  int64_t num_pages;
+  const int32_t *kv_indptr;
+  const int32_t *kv_indices;
+  int64_t kv_indices_len;
+  const int32_t *last_page_len;
+  uint16_t *o;
+  int64_t o_stride_b, o_stride_h;
+  float *lse;
+  float *dump;
+  int64_t dump_stride_b, dump_stride_h;
+  int dump_cap;     // tokens per dump row the caller guarantees (max_pages_per_row * 16)
+  float *part_acc;  // [batch][hkv][nsplit][G][128]
+  float *part_ml;   // [batch][hkv][nsplit][G][2]  (m in log2 units, l)
+  int batch, hq, hkv, nsplit;
+  float sm_scale;
+};
+
+struct RowInfo {
+  int64_t p0;
+  int np;
+  int kv_len;
+};
+
+__device__ __forceinline__ RowInfo row_info(const DecodeArgs &a, int b) {
+  const int64_t ilen = a.kv_indices_len;
+  int64_t p0 = a.kv_indptr[b];
+  int64_t p1 = a.kv_indptr[b + 1];
+  p0 = p0 < 0 ? 0 : (p0 > ilen ? ilen : p0);
+  p1 = p1 < p0 ? p0 : (p1 > ilen ? ilen : p1);
+  int last = a.last_page_len[b];
+  last = last < 0 ? 0 : (last > kPageSize ? kPageSize : last);
+  RowInfo r;
+  r.p0 = p0;
+  r.np = (int)(p1 - p0);
+  r.kv_len = r.np > 0 ? (r.np - 1) * kPageSize + last : 0;
+  return r;
+}
+
+template <int DT, int G, bool WITH_V, bool WITH_DUMP>
+__global__ void __launch_bounds__(kThreads) decode_split_kernel(DecodeArgs a) {
+  using E = Elem<DT>;
+  extern __shared__ float smem[];
+
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c = lane >> 4;  // 16-lane row of the wave
+  const int t = lane & 15;  // lane within the row
+
+  const RowInfo ri = row_info(a, b);
+  const int pps = (ri.np + a.nsplit - 1) / a.nsplit;
+  const int j0 = split * pps;
+  const int j1 = min(ri.np, j0 + pps);
+
+  // Query fragment (MFMA A operand): row g = t, d = 32s + 8c + [0, 8).
+  u32x4 qf[4];
+  if (t < G) {
+    const uint16_t *qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + t) * a.q_stride_h + 8 * c;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = ld128(qp + 32 * s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
+  const int64_t page_elems = 2 * kPageSize * row_elems;
+  const int64_t k_off = (int64_t)t * row_elems + 8 * c;
+  const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;
+
+  float m[4], l[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+  }
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+
+  const float sm_scale = a.sm_scale;
+  float *dump_row =
+      WITH_DUMP ? a.dump + (int64_t)b * a.dump_stride_b + (int64_t)(h * G) * a.dump_stride_h : nullptr;
+
+  // Page j's base pointer for head h; a page id outside the cache is replaced
+  // by page 0 and all of its tokens are masked.
+  auto page_base = [&](int j, bool &ok) -> const uint16_t * {
+    int pid = a.kv_indices[ri.p0 + j];
+    ok = pid >= 0 && (int64_t)pid < a.num_pages;
+    pid = ok ? pid : 0;
+    return a.kv + (int64_t)pid * page_elems + (int64_t)h * kHeadDim;
+  };
+
+  auto load = [&](const uint16_t *base, u32x4 *kf, u32x4 *vf) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kf[s] = ld128(base + k_off + 32 * s);
+    if (WITH_V) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vf[i] = ld128(base + v_off + (int64_t)(4 * i) * row_elems);
+    }
+  };
+
+  auto process = [&](int j, bool ok, const u32x4 *kf, const u32x4 *vf) {
+    f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) S = E::mfma(qf[s], kf[s], S);
+
+    const int tok = j * kPageSize + t;
+    const bool valid = ok && tok < ri.kv_len;
+    float y[4], p[4], alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = valid ? S[r] * sm_scale : -INFINITY;
+      if (WITH_DUMP) {
+        const int g = 4 * c + r;
+        if (g < G && valid && tok < a.dump_cap) dump_row[(int64_t)g * a.dump_stride_h + tok] = x;
+      }
+      y[r] = x * kLog2e;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float mn = fmaxf(m[r], row16_max(y[r]));
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      alpha[r] = fast_exp2(m[r] - mref);
+      p[r] = fast_exp2(y[r] - mref);
+      l[r] = l[r] * alpha[r] + row16_sum(p[r]);
+      m[r] = mn;
+    }
+    if (WITH_V) {
+      // Rescale the accumulators by each head's alpha (uniform per head).
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float al = readlane(alpha[g & 3], (g >> 2) << 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= al;
+      }
+      const bool tail = (j + 1) * kPageSize > ri.kv_len || !ok;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = c + 4 * i;  // V row handled by this lane
+        float pv[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) pv[g] = shfl(p[g & 3], ((g >> 2) << 4) + tt);
+        float vv[8];
+        const u32x4 w = vf[i];
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          vv[2 * q2] = E::lo(w[q2]);
+          vv[2 * q2 + 1] = E::hi(w[q2]);
+        }
+        if (tail && (!ok || j * kPageSize + tt >= ri.kv_len)) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vv[e] = 0.f;  // stale rows may hold NaN/Inf
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv[g], vv[e], acc[g][e]);
+      }
+    }
+  };
+
+  // Pages j0 + wave, j0 + wave + 4, ...: software pipelined one page ahead.
+  const int first = j0 + wave;
+  const int count = first < j1 ? (j1 - first + kWaves - 1) / kWaves : 0;
+  if (count > 0) {
+    u32x4 kc[4], vc[4], kn[4], vn[4];
+    bool okc, okn;
+    load(page_base(first, okc), kc, vc);
+    int j = first;
+    for (int it = 0; it + 1 < count; ++it) {
+      const int jn = j + kWaves;
+      load(page_base(jn, okn), kn, vn);
+      process(j, okc, kc, vc);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        kc[s] = kn[s];
+        vc[s] = vn[s];
+      }
+      okc = okn;
+      j = jn;
+    }
+    process(j, okc, kc, vc);
+  }
+
+  // Sum the four token subsets of the P.V accumulators (lanes l, l^16, l^32, l^48).
+  if (WITH_V) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[g][e] += shfl_xor(acc[g][e], 16);
+        acc[g][e] += shfl_xor(acc[g][e], 32);
+      }
+  }
+
+  // Merge the block's waves in LDS.
+  float *s_ml = smem;                       // [kWaves][G][2]
+  float *s_acc = smem + kWaves * G * 2;     // [kWaves][G][128]
+  if (t == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int g = 4 * c + r;
+      if (g < G) {
+        s_ml[(wave * G + g) * 2 + 0] = m[r];
+        s_ml[(wave * G + g) * 2 + 1] = l[r];
+      }
+    }
+  }
+  if (WITH_V && c == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float *dst = s_acc + (wave * G + g) * kHeadDim + 8 * t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+
+  const int n_out = WITH_V ? G * kHeadDim : G;
+  for (int idx = threadIdx.x; idx < n_out; idx += kThreads) {
+    const int g = WITH_V ? idx / kHeadDim : idx;
+    const int dd = WITH_V ? idx % kHeadDim : 0;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
+    const float Mr = M == -INFINITY ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = fast_exp2(s_ml[(w * G + g) * 2] - Mr);
+      L = fmaf(s_ml[(w * G + g) * 2 + 1], sc, L);
+      if (WITH_V) A = fmaf(s_acc[(w * G + g) * kHeadDim + dd], sc, A);
+    }
+    const int hq = h * G + g;
+    if (a.nsplit == 1) {
+      if (WITH_V) {
+        const float ov = L > 0.f ? A / L : 0.f;
+        a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(ov);
+      }
+      if (dd == 0 && a.lse != nullptr)
+        a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+    } else {
+      const int64_t pidx = (((int64_t)b * a.hkv + h) * a.nsplit + split) * G + g;
+      if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
+      if (dd == 0) {
+        a.part_ml[pidx * 2 + 0] = M;
+        a.part_ml[pidx * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Combines the split partials of one (row, q head): o = sum A_s 2^(m_s-M) / sum l_s 2^(m_s-M).
+template <int DT>
+__global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
+  using E = Elem<DT>;
+  const int bh = blockIdx.x;
+  const int b = bh / a.hq;
+  const int hq = bh % a.hq;
+  const int h = hq / G;
+  const int g = hq % G;
+  const int dd = threadIdx.x;
+  const int64_t base = (((int64_t)b * a.hkv + h) * a.nsplit) * G + g;
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(base + (int64_t)s * G) * 2]);
+  const float Mr = M == -INFINITY ? 0.f : M;
+  float L = 0.f, A = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const int64_t pidx = base + (int64_t)s * G;
+    const float sc = fast_exp2(a.part_ml[pidx * 2] - Mr);
+    L = fmaf(a.part_ml[pidx * 2 + 1], sc, L);
+    A = fmaf(a.part_acc[pidx * kHeadDim + dd], sc, A);
+  }
+  const float ov = L > 0.f ? A / L : 0.f;
+  a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(ov);
+  if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+}
+
+// lse-only merge (scorer path without V).
+__global__ void decode_merge_lse_kernel(DecodeArgs a, int G) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.batch * a.hq) return;
+  const int b = idx / a.hq;
+  const int hq = idx % a.hq;
+  const int h = hq / G;
+  const int g = hq % G;
+  const int64_t base = (((int64_t)b * a.hkv + h) * a.nsplit) * G + g;
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(base + (int64_t)s * G) * 2]);
+  const float Mr = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const int64_t pidx = base + (int64_t)s * G;
+    L = fmaf(a.part_ml[pidx * 2 + 1], fast_exp2(a.part_ml[pidx * 2] - Mr), L);
+  }
+  a.lse[idx] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+}
+
+enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2 };
+
+template <int DT, int G>
+void launch_split(const DecodeArgs &a, int mode, hipStream_t stream) {
+  dim3 grid(a.nsplit, a.hkv, a.batch);
+  const size_t sm_attn = (size_t)kWaves * G * (2 + kHeadDim) * sizeof(float);
+  const size_t sm_score = (size_t)kWaves * G * 2 * sizeof(float);
+  switch (mode) {
+    case kAttn:
+      hipLaunchKernelGGL((decode_split_kernel<DT, G, true, false>), grid, dim3(kThreads), sm_attn, stream, a);
+      break;
+    case kAttnDump:
+      hipLaunchKernelGGL((decode_split_kernel<DT, G, true, true>), grid, dim3(kThreads), sm_attn, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_split_kernel<DT, G, false, true>), grid, dim3(kThreads), sm_score, stream, a);
+      break;
+  }
+}
+
+template <int DT>
+void launch_split_g(const DecodeArgs &a, int G, int mode, hipStream_t stream) {
+  switch (G) {
+    case 1: launch_split<DT, 1>(a, mode, stream); break;
+    case 2: launch_split<DT, 2>(a, mode, stream); break;
+    case 3: launch_split<DT, 3>(a, mode, stream); break;
+    case 4: launch_split<DT, 4>(a, mode, stream); break;
+    case 5: launch_split<DT, 5>(a, mode, stream); break;
+    case 6: launch_split<DT, 6>(a, mode, stream); break;
+    case 7: launch_split<DT, 7>(a, mode, stream); break;
+    default: launch_split<DT, 8>(a, mode, stream); break;
+  }
+}
+
+}  // namespace
+
+int decode_num_splits(int batch, int hkv, int max_pages) {
+  const int64_t pairs = (int64_t)batch * hkv;
+  if (pairs <= 0 || max_pages <= 0) return 1;
+  const int64_t target_waves = 256 /*CUs*/ * 4 /*SIMDs*/ * 4 /*waves per SIMD*/;
+  int64_t ns = ceil_div(target_waves, pairs * kWaves);
+  int64_t cap = max_pages / (2 * kWaves);  // >= 2 pages per wave
+  if (cap < 1) cap = 1;
+  if (ns > cap) ns = cap;
+  if (ns < 1) ns = 1;
+  if (ns > 256) ns = 256;
+  return (int)ns;
+}
+
+static size_t partial_bytes(int batch, int hq, int nsplit, bool with_acc) {
+  if (nsplit <= 1) return 0;
+  const size_t per = (with_acc ? kHeadDim : 0) + 2;
+  return (size_t)batch * hq * nsplit * per * sizeof(float);
+}
+
+// Shared validation + launch used by the attention and the scorer entry points.
+int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *kv_cache,
+               int64_t num_pages, const int32_t *kv_indptr, const int32_t *kv_indices,
+               int64_t kv_indices_len, const int32_t *kv_last_page_len, void *o,
+               int64_t o_stride_b, int64_t o_stride_h, float *lse, float *dump,
+               int64_t dump_stride_b, int64_t dump_stride_h, int batch, int hq, int hkv,
+               int head_dim, int dtype, float sm_scale, int max_pages, int mode,
+               void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who) {
+  clear_error();
+  if (batch <= 0) return DELTA_OK;
+  if (head_dim != kHeadDim) return set_error(DELTA_ERR_INVALID, "%s: head_dim must be 128 (got %d)", who, head_dim);
+  if (hkv <= 0 || hq <= 0 || hq % hkv != 0)
+    return set_error(DELTA_ERR_INVALID, "%s: num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", who, hq, hkv);
+  const int G = hq / hkv;
+  if (G > kMaxGroup) return set_error(DELTA_ERR_INVALID, "%s: group size %d > %d unsupported", who, G, kMaxGroup);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
+  if (!q || !kv_cache || !kv_indptr || !kv_indices || !kv_last_page_len)
+    return set_error(DELTA_ERR_INVALID, "%s: null input pointer", who);
+  if (mode != kScoreOnly && !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
+  if (mode != kAttn && !dump) return set_error(DELTA_ERR_INVALID, "%s: null logits dump", who);
+  if (((uintptr_t)q | (uintptr_t)kv_cache) & 15u)
+    return set_error(DELTA_ERR_INVALID, "%s: q and kv_cache must be 16-byte aligned", who);
+  if ((q_stride_h % 8) || (q_stride_b % 8))
+    return set_error(DELTA_ERR_INVALID, "%s: q strides must be multiples of 8 elements", who);
+  if (num_pages <= 0 || kv_indices_len < 0) return set_error(DELTA_ERR_INVALID, "%s: empty cache", who);
+  if (max_pages <= 0) max_pages = 1;
+
+  DecodeArgs a;
+  a.q = (const uint16_t *)q;
+  a.q_stride_b = q_stride_b;
+  a.q_stride_h = q_stride_h;
+  a.kv = (const uint16_t *)kv_cache;
+  a.num_pages = num_pages;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.kv_indices_len = kv_indices_len;
+  a.last_page_len = kv_last_page_len;
+  a.o = (uint16_t *)o;
+  a.o_stride_b = o_stride_b;
+  a.o_stride_h = o_stride_h;
+  a.lse = lse;
+  a.dump = dump;
+  a.dump_stride_b = dump_stride_b;
+  a.dump_stride_h = dump_stride_h;
+  a.dump_cap = max_pages * kPageSize;
+  a.batch = batch;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.nsplit = decode_num_splits(batch, hkv, max_pages);
+  a.sm_scale = sm_scale;
+  a.part_acc = nullptr;
+  a.part_ml = nullptr;
+
+  const bool with_acc = mode != kScoreOnly;
+  const size_t need = partial_bytes(batch, hq, a.nsplit, with_acc);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
+    if ((uintptr_t)workspace & 15u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
+    float *ws = (float *)workspace;
+    a.part_ml = ws;
+    a.part_acc = ws + (size_t)batch * hq * a.nsplit * 2;
+  }
+  if (mode == kScoreOnly && !lse && a.nsplit > 1)
+    return set_error(DELTA_ERR_INVALID, "%s: scorer needs an lse buffer", who);
+
+  if (dtype == DELTA_BF16)
+    launch_split_g<DELTA_BF16>(a, G, mode, stream);
+  else
+    launch_split_g<DELTA_FP16>(a, G, mode, stream);
+  int rc = check_launch(who);
+  if (rc) return rc;
+  if (a.nsplit > 1) {
+    if (with_acc) {
+      if (dtype == DELTA_BF16)
+        hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
+      else
+        hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
+    } else {
+      const int n = batch * hq;
+      hipLaunchKernelGGL(decode_merge_lse_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a, G);
+    }
+    rc = check_launch(who);
+  }
+  return rc;
+}
+
+}  // namespace delta
+
+extern "C" DELTA_EXPORT int delta_decode_num_splits(int batch, int num_kv_heads, int max_pages_per_row) {
+  return delta::decode_num_splits(batch, num_kv_heads, max_pages_per_row);
+}
+
+extern "C" DELTA_EXPORT size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
+                                                                  int max_pages_per_row) {
+  const int ns = delta::decode_num_splits(batch, num_kv_heads, max_pages_per_row);
+  return delta::partial_bytes(batch, num_qo_heads, ns, true);
+}
+
+extern "C" DELTA_EXPORT int delta_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                               const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr,
+                                               const int32_t *kv_indices, int64_t kv_indices_len,
+                                               const int32_t *kv_last_page_len, void *o, int64_t o_stride_b,
+                                               int64_t o_stride_h, float *lse, float *logits_dump,
+                                               int64_t dump_stride_b, int64_t dump_stride_h, int batch,
+                                               int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                                               float sm_scale, int max_pages_per_row, void *workspace,
+                                               size_t workspace_bytes, delta_stream_t stream) {
+  const int mode = logits_dump ? delta::kAttnDump : delta::kAttn;
+  return delta::run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                           kv_last_page_len, o, o_stride_b, o_stride_h, lse, logits_dump, dump_stride_b,
+                           dump_stride_h, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
+                           max_pages_per_row, mode, workspace, workspace_bytes, (hipStream_t)stream,
+                           "delta_paged_decode");
+}

@@ -1,0 +1,239 @@
+/*
+ * delta_hip.h -- C ABI of the MI355X (gfx950) selective-KV decode hot path.
+ *
+ * The library (delta_amd/_delta_hip.so) replaces the device work behind the
+ * reference's torch.library ops and planner helpers (hoenza/DELTA):
+ *
+ *   FlashInfer BatchPrefillWithPagedKVCacheWrapper.run  (backend.py:461-512)
+ *   FlashInfer JIT BatchDumpAttentionWeights + run      (backend.py:175-222, 518-585)
+ *   _compute_page_scores_from_attention_buffer_legacy_softmax (backend.py:887-904)
+ *   PageSelectorV2.select / _prepare_scores             (page_selector_v2.py:113-212)
+ *   Triton _pack_page_indices_kernel                    (page_metadata.py:6-70)
+ *   _collect_decode_page_info_fast (device half)        (backend.py:2040-2172)
+ *   FlashInfer append_paged_kv_cache (mylib::update_kv) (utils.py:31-79)
+ *   FlashInfer apply_rope / apply_llama31_rope          (model.py:152-175)
+ *
+ * Conventions shared by every entry point:
+ *   - all pointers are device pointers unless stated; sizes and strides are in
+ *     ELEMENTS of the pointed-to type;
+ *   - the paged KV cache is [num_pages, 2, page_size=16, num_kv_heads, head_dim=128]
+ *     (model.py:102), K at [:,0], V at [:,1]; dtype bf16 (DELTA_BF16) or fp16
+ *     (DELTA_FP16);
+ *   - page tables are CSR: kv_indptr [batch+1], kv_indices [kv_indices_len],
+ *     kv_last_page_len [batch] in [0,16]; row b holds
+ *     (pages_b - 1) * 16 + last_page_len_b tokens;
+ *   - kernels never allocate, never synchronise and never read host memory, so
+ *     every call can be recorded in a hipGraph; caller-provided workspaces are
+ *     sized by the *_workspace_bytes queries;
+ *   - out-of-range page ids / indptr entries are masked (the kernel never
+ *     faults on a bad table, it drops the offending pages);
+ *   - return 0 on success; otherwise a non-zero code and delta_last_error()
+ *     (thread local) describes the failure.
+ */
+#ifndef DELTA_HIP_H_
+#define DELTA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *delta_stream_t; /* a hipStream_t (0 = the null stream) */
+
+enum {
+  DELTA_BF16 = 0,
+  DELTA_FP16 = 1,
+};
+
+enum {
+  DELTA_OK = 0,
+  DELTA_ERR_INVALID = 1,   /* bad argument (shape, dtype, null pointer, size) */
+  DELTA_ERR_WORKSPACE = 2, /* workspace too small */
+  DELTA_ERR_HIP = 3,       /* a HIP runtime call failed */
+};
+
+/* Last error message of the calling thread ("" when none). */
+const char *delta_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+int delta_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Paged decode attention (one query token per row)                          */
+/* ------------------------------------------------------------------------ */
+
+/* Number of split-K work units per (row, kv head) the decode kernels use for
+ * this shape.  Depends only on its arguments, so a value computed at graph
+ * capture stays valid for every replay.  max_pages_per_row is an upper bound
+ * of pages_b over the rows. */
+int delta_decode_num_splits(int batch, int num_kv_heads, int max_pages_per_row);
+
+/* Bytes of workspace delta_paged_decode needs (split-K partials). */
+size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
+                                          int max_pages_per_row);
+
+/* o[b,h,:] = softmax(q[b,h,:] . K_b[:, h/G, :] * sm_scale) @ V_b[:, h/G, :].
+ *
+ * Replaces BatchPrefillWithPagedKVCacheWrapper.run with causal=True and
+ * qo_len=1 per row (backend.py:461-484 target_decode over the full CSR,
+ * backend.py:486-512 target_subset_decode over the subset CSR; plan at
+ * backend.py:1091-1105).
+ *
+ *   q   [batch, num_qo_heads, 128] with row stride q_stride_b, head stride q_stride_h
+ *   o   [batch, num_qo_heads, 128] with strides o_stride_b / o_stride_h (same dtype)
+ *   lse [batch, num_qo_heads] fp32 natural-log log-sum-exp of the scaled logits
+ *       (-inf for an empty row), or NULL
+ *   logits_dump (planner layer, or NULL): fp32, receives
+ *       dump[b*dump_stride_b + h*dump_stride_h + t] = (q.k_t) * sm_scale for t < kv_len_b,
+ *       exactly the BatchDumpAttentionWeights side write (backend.py:207-219);
+ *       positions t >= kv_len_b are left untouched.
+ *   num_qo_heads % num_kv_heads == 0 and num_qo_heads / num_kv_heads <= 8.
+ */
+int delta_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                       const void *kv_cache, int64_t num_pages,
+                       const int32_t *kv_indptr, const int32_t *kv_indices,
+                       int64_t kv_indices_len, const int32_t *kv_last_page_len,
+                       void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                       float *logits_dump, int64_t dump_stride_b, int64_t dump_stride_h,
+                       int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+                       int dtype, float sm_scale, int max_pages_per_row,
+                       void *workspace, size_t workspace_bytes, delta_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Page scoring (del3_legacy_softmax)                                         */
+/* ------------------------------------------------------------------------ */
+
+/* scores[b, j] = sum_{t in page j} max_h softmax_t(dump[b, h, :max_pages*16])
+ * for b < batch, j < max_pages (backend.py:887-904).
+ *
+ * dump is the planner logits buffer (layout as in delta_paged_decode);
+ * positions t >= kv_len_b are treated as -inf (the reference's -inf fill,
+ * backend.py:384-389) and never read.  kv_indptr/kv_last_page_len give
+ * kv_len_b.  lse (natural log, [batch, num_qo_heads], as written by
+ * delta_paged_decode for the same dump) may be NULL, in which case the
+ * softmax normaliser is computed from the dump in a first pass (then
+ * workspace must hold delta_page_score_workspace_bytes).  scores has row
+ * stride score_stride (>= max_pages). */
+size_t delta_page_score_workspace_bytes(int batch, int num_qo_heads);
+int delta_page_scores_from_logits(const float *logits_dump, int64_t dump_stride_b,
+                                  int64_t dump_stride_h, const float *lse,
+                                  const int32_t *kv_indptr, const int32_t *kv_last_page_len,
+                                  float *scores, int64_t score_stride, int batch,
+                                  int num_qo_heads, int max_pages, void *workspace,
+                                  size_t workspace_bytes, delta_stream_t stream);
+
+/* Standalone scorer: reads the paged K cache once (no V), writes the fp32
+ * logits into logits_dump (caller-provided, layout as above, >= max_pages*16
+ * per (b,h) row) and the page scores.  Replaces the dump attention kernel +
+ * legacy-softmax torch ops for a caller that only needs scores
+ * (backend.py:561-577 + 887-904). */
+size_t delta_page_score_kv_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
+                                           int max_pages_per_row);
+int delta_page_score(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr,
+                     const int32_t *kv_indices, int64_t kv_indices_len,
+                     const int32_t *kv_last_page_len, float *logits_dump,
+                     int64_t dump_stride_b, int64_t dump_stride_h, float *scores,
+                     int64_t score_stride, int batch, int num_qo_heads, int num_kv_heads,
+                     int head_dim, int dtype, float sm_scale, int max_pages,
+                     void *workspace, size_t workspace_bytes, delta_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* PageSelectorV2 (top-k page selection)                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Selects pages per row exactly as PageSelectorV2.select
+ * (page_selector_v2.py:113-212) with ties broken by the smaller page index:
+ *
+ *   key_j = nan_to_num(score_j, nan=-inf, neginf=-inf) + fp32(-j * pos_bias_scale)
+ *   key_j = +inf for j in [max(tp-L,0), tp);  pages j >= tp are not candidates
+ *   top-k of key (key desc, j asc), emitted in ascending j as
+ *   block_table[b * bt_stride + j].
+ *
+ * tp_b = kv_indptr[b+1] - kv_indptr[b].  k_b = k, or k_per_row[b] when
+ * k_per_row != NULL (extension: per-row budgets).
+ *   fixed_count = 0 (general path, 136-164): row b emits min(tp_b, k_b) pages
+ *                 and out_indptr = cumsum.
+ *   fixed_count = 1 (fixed path, 166-188): row b emits k_b pages and
+ *                 out_indptr[b] = b * k (requires k_per_row == NULL).
+ * use_subset (optional, device int): when non-NULL and *use_subset == 0 the
+ * row's full page list block_table[b, :tp_b] is emitted (the engine's
+ * "subset == full" step).  out_indices holds out_indices_len entries (sum of
+ * the row counts is needed; writes past it are dropped).  max_pages (Nmax)
+ * bounds the columns: tp_b is clamped to it (the reference's Nmax is the
+ * largest tp_b, so this never binds there). */
+int delta_select_pages(const float *scores, int64_t score_stride, const int32_t *kv_indptr,
+                       const int32_t *block_table, int64_t bt_stride, int batch,
+                       int max_pages, int k, const int32_t *k_per_row, int L,
+                       float pos_bias_scale, int fixed_count, const int32_t *use_subset,
+                       int32_t *out_indices, int64_t out_indices_len, int32_t *out_indptr,
+                       delta_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Page-table metadata                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* In-place pack of page lists (page_metadata.py:6-70): row r copies
+ * slot_block_table[active_slots[r] * pages_per_slot + start_cols[r] + c] for
+ * c < counts[r] to out_indices[indptr[r] + c] and, when write_row_block, to
+ * row_block_table[r * pages_per_slot + c].  slot_block_table has num_slots
+ * rows; a row whose slot, columns or destination fall outside the tables
+ * (num_slots, pages_per_slot, out_indices_len) is skipped. */
+int delta_pack_page_indices(const int32_t *slot_block_table, int num_slots,
+                            const int32_t *active_slots, const int32_t *start_cols,
+                            const int32_t *counts, const int32_t *indptr,
+                            int32_t *out_indices, int64_t out_indices_len,
+                            int32_t *row_block_table, int n_rows, int pages_per_slot,
+                            int max_count, int write_row_block, delta_stream_t stream);
+
+/* Device-side decode page info for rows 0..batch-1 of a slot block table
+ * (backend.py:2040-2172 with scheduler.py:60-66), so a decode step needs no
+ * host work: for each row, kv_len = cachelens[b] + 1, pages = kv_len/16 + 1,
+ * last = kv_len % 16.  Writes kv_indptr (cumsum), kv_indices (packed from
+ * slot_block_table), kv_last_page_len, row_block_table [batch, pages_per_slot]
+ * (optional), the default subset CSR of the last min(pages, k) pages
+ * (subset_indices/subset_indptr, optional), and use_subset[0] =
+ * (selective && subset_total > 0 && full_total / subset_total > compression_ratio)
+ * (optional).  Rows whose page count would exceed pages_per_slot are clamped. */
+int delta_decode_page_info(const int32_t *cachelens, const int32_t *slot_block_table,
+                           int batch, int pages_per_slot, int k, double compression_ratio,
+                           int selective, int32_t *kv_indptr, int32_t *kv_indices,
+                           int32_t *kv_last_page_len, int32_t *row_block_table,
+                           int32_t *subset_indices, int32_t *subset_indptr,
+                           int32_t *use_subset, delta_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* KV append and RoPE                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* mylib::update_kv (utils.py:31-79, FlashInfer append_paged_kv_cache):
+ * appended token i of row b (rows from kv_append_indptr) is written at
+ * position seq_len_b - append_len_b + i, page kv_indices[kv_indptr[b] + pos/16],
+ * slot pos % 16, where seq_len_b comes from kv_indptr/kv_last_page_len.
+ * k, v: [nnz, num_kv_heads, 128] with token strides k_stride / v_stride. */
+int delta_append_kv(const void *k, int64_t k_stride, const void *v, int64_t v_stride,
+                    const int32_t *kv_append_indptr, void *kv_cache, int64_t num_pages,
+                    const int32_t *kv_indices, int64_t kv_indices_len,
+                    const int32_t *kv_indptr, const int32_t *kv_last_page_len, int nnz,
+                    int batch, int num_kv_heads, int head_dim, int dtype,
+                    delta_stream_t stream);
+
+/* mylib::rope (model.py:152-175; FlashInfer apply_rope / apply_llama31_rope
+ * with interleave=True): token i of row b is at offsets[b] + i - indptr[b];
+ * pair (2j, 2j+1) rotates by pos * f_j, f_j = theta^(-2j/d) / rope_scale, or
+ * the Llama-3.1 blend when llama31 != 0.  q [nnz, Hq, 128] -> q_out,
+ * k [nnz, Hkv, 128] -> k_out (out may alias in). */
+int delta_rope(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+               void *q_out, int64_t q_out_stride, void *k_out, int64_t k_out_stride,
+               const int32_t *indptr, const int32_t *offsets, int nnz, int batch,
+               int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+               float rope_scale, float rope_theta, int llama31, float low_freq_factor,
+               float high_freq_factor, float old_context_len, delta_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DELTA_HIP_H_ */

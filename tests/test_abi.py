@@ -1,0 +1,79 @@
+"""The C-ABI library builds, loads without a GPU and exports what include/delta_hip.h declares."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "delta_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"\b(delta_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from delta_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from delta_amd import build
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for must in ("delta_paged_decode", "delta_page_score", "delta_page_scores_from_logits",
+                 "delta_select_pages", "delta_pack_page_indices", "delta_decode_page_info",
+                 "delta_append_kv", "delta_rope", "delta_last_error"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from delta_amd import _lib
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_no_undeclared_exports(lib):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ROOT / "delta_amd" / "_delta_hip.so")],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l and l.split()[-1].startswith("delta_")}
+    assert exported == set(declared_functions())
+
+
+def test_queries_without_gpu(lib):
+    assert lib.delta_abi_version() == 100
+    assert lib.delta_last_error() == b""
+    # split heuristic: deterministic, >= 1, and >= 2 pages per wave
+    assert lib.delta_decode_num_splits(32, 8, 128) == 4
+    assert lib.delta_decode_num_splits(1024, 8, 2048) == 1
+    assert lib.delta_decode_num_splits(4, 4, 4096) >= 16
+    assert lib.delta_decode_num_splits(1, 8, 4) == 1
+    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 128) == 32 * 32 * 4 * 130 * 4
+    assert lib.delta_paged_decode_workspace_bytes(1024, 32, 8, 2048) == 0
+
+
+def test_argument_errors_reported_without_launch(lib):
+    from delta_amd import _lib
+    # head_dim 64 is rejected before any launch; the message is kept per thread
+    with pytest.raises(_lib.DeltaHipError, match="head_dim"):
+        _lib.call("delta_paged_decode", 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, None, None, 0, 0,
+                  1, 8, 8, 64, 0, 1.0, 1, None, 0, None)
+    with pytest.raises(_lib.DeltaHipError, match="k out of range"):
+        _lib.call("delta_select_pages", 8, 4, 8, 8, 4, 1, 4, 5, None, 1, 1e-7, 0, None, 8, 4, 8, None)
+
+
+def test_wrappers_reject_cpu_tensors():
+    from delta_amd import kernels
+    q = torch.zeros(1, 8, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(2, 2, 16, 8, 128, dtype=torch.bfloat16)
+    i32 = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        kernels.paged_decode(q, cache, i32, i32, i32, max_pages_per_row=1)

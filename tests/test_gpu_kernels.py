@@ -1,0 +1,340 @@
+"""GPU parity: every HIP kernel against the CPU oracle on the same seeded inputs.
+
+Tolerances (north star): selected page sets bit-exact; page scores within 1e-4
+relative (fp32); attention outputs within 2e-2 absolute with cosine > 0.999
+(bf16/fp16).  Logits dump within 1e-4 * (1 + |x|) (fp32 accumulation order).
+"""
+import math
+
+import pytest
+import torch
+
+from delta_amd import kernels as K
+from delta_amd.workloads import config_case, make_case
+from oracle import delta_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def cases():
+    return {
+        "cfg1_bf16": lambda: config_case(1, dtype=torch.bfloat16),
+        "cfg2_fp16_small": lambda: config_case(2, scale=0.125),
+        "cfg3_bf16_small": lambda: config_case(3, scale=0.125, batch=6),
+        "cfg4_g7_small": lambda: config_case(4, scale=1 / 64),
+        "cfg5_g5_ragged_small": lambda: config_case(5, scale=1 / 32, batch=12),
+        "ragged_g1": lambda: make_case(batch=5, hq=8, hkv=8, kv_lens=[1, 15, 16, 17, 300], seed=3, k=4, L=2),
+        "ragged_g8_trailing": lambda: make_case(batch=4, hq=16, hkv=2, kv_lens=[32, 48, 7, 129], seed=4,
+                                                k=3, L=1, trailing_empty_page=True, dtype=torch.float16),
+    }
+
+
+CASES = cases()
+
+
+def assert_attn_close(got, want, what=""):
+    got = got.float().cpu()
+    want = want.float().cpu()
+    err = (got - want).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0).item()
+    assert err <= 2e-2, f"{what}: max abs err {err}"
+    assert cos > 0.999, f"{what}: cosine {cos}"
+
+
+def gpu(c):
+    return c.to(DEV)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_decode_attention_and_dump(name):
+    c = CASES[name]()
+    g = gpu(c)
+    B, hq = c.q.shape[:2]
+    mp = c.max_pages
+    dump = torch.full((B, hq, mp * 16 + 5), 12345.0, device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    o = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                       max_pages_per_row=mp, lse=lse, logits_dump=dump)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                              c.kv_last_page_len, c.sm_scale)
+    assert_attn_close(o, o_ref, name)
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
+    x_ref = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                          c.sm_scale, mp * 16 + 5)
+    d = dump.cpu()
+    valid = torch.isfinite(x_ref)
+    assert torch.all(d[~valid] == 12345.0), "dump wrote past kv_len"
+    err = (d[valid] - x_ref[valid]).abs() / (1 + x_ref[valid].abs())
+    assert err.max().item() < 1e-4
+    # without the dump the attention result is bit-identical
+    o2 = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
+    assert torch.equal(o, o2)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_page_scores(name):
+    c = CASES[name]()
+    g = gpu(c)
+    B, hq = c.q.shape[:2]
+    mp = c.max_pages
+    dump = torch.empty((B, hq, mp * 16), device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                   max_pages_per_row=mp, lse=lse, logits_dump=dump)
+    s_lse = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
+    s_2pass = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp)
+    s_kv = K.page_score(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, mp)
+    torch.cuda.synchronize()
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, c.sm_scale, mp * 16)
+    ref = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
+    for what, s in (("planner", s_lse), ("two-pass", s_2pass), ("kv-only", s_kv)):
+        s = s.cpu().double()
+        rel = ((s - ref).abs() / ref.abs().clamp_min(1e-30))
+        rel[ref == 0] = s[ref == 0].abs()
+        assert rel.max().item() < 1e-4, f"{name}/{what}: rel err {rel.max().item()}"
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_selection_bit_exact_on_gpu_scores(name):
+    c = CASES[name]()
+    g = gpu(c)
+    mp = c.max_pages
+    s = K.page_score(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, mp)
+    counts = (c.kv_indptr[1:] - c.kv_indptr[:-1])
+    k = min(c.k, mp)
+    kpr = c.k_per_row
+    if kpr is not None:
+        kpr = torch.clamp(kpr, max=mp)
+    idx, indptr = K.select_pages(s, g.kv_indptr, g.block_table, k, c.L,
+                                 k_per_row=None if kpr is None else kpr.to(DEV))
+    torch.cuda.synchronize()
+    sc = s.cpu()
+    if kpr is None:
+        want_i, want_p = O.select_pages(sc, counts, c.block_table, k, c.L)
+    else:  # per-row budgets: the oracle row by row
+        wi, wp = [], [0]
+        for b in range(c.batch):
+            ii, _ = O.select_pages(sc[b:b + 1], counts[b:b + 1], c.block_table[b:b + 1], int(kpr[b]), c.L)
+            wi.append(ii)
+            wp.append(wp[-1] + ii.numel())
+        want_i, want_p = torch.cat(wi), torch.tensor(wp, dtype=torch.int32)
+    assert indptr.cpu().tolist() == want_p.tolist()
+    assert idx[:int(want_p[-1])].cpu().tolist() == want_i.tolist()
+
+
+def test_selection_adversarial_scores():
+    gen = torch.Generator().manual_seed(5)
+    B, n = 6, 300
+    s = torch.round(torch.rand(B, n, generator=gen) * 4) / 4  # heavy ties
+    s[0, :50] = float("nan")
+    s[1, 10:20] = float("inf")
+    s[2, ::3] = float("-inf")
+    s[3] = 0.0
+    s[3, ::2] = -0.0
+    s[4, 5] = 3.4e38
+    counts = torch.tensor([300, 299, 200, 300, 17, 64])
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(counts, 0)
+    bt = torch.randperm(B * n, generator=gen).reshape(B, n).to(torch.int32)
+    for k, L, bias in ((40, 8, 1e-7), (40, 8, 0.0), (64, 0, 1e-7), (1, 1, 1e-7), (300, 3, 1e-7)):
+        idx, ip = K.select_pages(s.to(DEV), indptr.to(DEV), bt.to(DEV), k, L, pos_bias_scale=bias)
+        wi, wp = O.select_pages(s, counts, bt, k, L, bias)
+        assert ip.cpu().tolist() == wp.tolist(), (k, L, bias)
+        assert idx[:int(wp[-1])].cpu().tolist() == wi.tolist(), (k, L, bias)
+
+
+def test_selection_fixed_and_use_subset():
+    gen = torch.Generator().manual_seed(6)
+    B, n, k = 4, 50, 16
+    s = torch.rand(B, n, generator=gen)
+    counts = torch.tensor([50, 50, 40, 30])
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(counts, 0)
+    bt = torch.randperm(B * n, generator=gen).reshape(B, n).to(torch.int32)
+    idx, ip = K.select_pages(s.to(DEV), indptr.to(DEV), bt.to(DEV), k, 4, fixed_count=True)
+    wi, wp = O.select_pages(s, counts, bt, k, 4, fixed_count=True)
+    assert ip.cpu().tolist() == wp.tolist() and idx.cpu().tolist() == wi.tolist()
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    idx, ip = K.select_pages(s.to(DEV), indptr.to(DEV), bt.to(DEV), k, 4, use_subset=flag)
+    assert ip.cpu().tolist() == indptr.tolist()
+    full = torch.cat([bt[b, :int(counts[b])] for b in range(B)])
+    assert idx[:int(indptr[-1])].cpu().tolist() == full.tolist()
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_selective_step_end_to_end(name):
+    """Planner score -> selection -> sparse attention, against the oracle's own chain."""
+    c = CASES[name]()
+    if c.k_per_row is not None:
+        pytest.skip("per-row budgets checked in test_selection_bit_exact_on_gpu_scores")
+    g = gpu(c)
+    B, hq = c.q.shape[:2]
+    mp = c.max_pages
+    k = min(c.k, mp)
+    dump = torch.empty((B, hq, mp * 16), device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    o_full = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                            max_pages_per_row=mp, lse=lse, logits_dump=dump)
+    s = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
+    idx, ip = K.select_pages(s, g.kv_indptr, g.block_table, k, c.L)
+    o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=k)
+    torch.cuda.synchronize()
+    ref = O.selective_step(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, k=k, L=c.L)
+    assert_attn_close(o_full, ref["o_full"], name + "/full")
+    got = idx[:int(ip[-1])].cpu()
+    counts = (c.kv_indptr[1:] - c.kv_indptr[:-1])
+    # Exact equality unless two pages straddle the threshold closer than the score error.
+    keys = O.prepare_scores(ref["scores"], counts, c.L)
+    mism = 0
+    for b in range(B):
+        a = set(got[int(ip[b]):int(ip[b + 1])].tolist())
+        r = set(ref["indices"][int(ref["indptr"][b]):int(ref["indptr"][b + 1])].tolist())
+        if a == r:
+            continue
+        mism += 1
+        kb = sorted(keys[b].tolist(), reverse=True)
+        thr = kb[k - 1]
+        bt = c.block_table[b].tolist()
+        for p in a ^ r:
+            j = bt.index(p)
+            assert abs(float(keys[b, j]) - thr) <= 2e-4 * abs(thr), f"{name}: row {b} page {j} far from threshold"
+    if mism == 0:
+        assert_attn_close(o_sp, ref["o_sparse"], name + "/sparse")
+    if c.planted is not None:
+        for b in range(B):
+            sel = set(got[int(ip[b]):int(ip[b + 1])].tolist())
+            planted_phys = {int(c.block_table[b, int(j)]) for j in c.planted[b]}
+            assert planted_phys <= sel, f"row {b}: planted-page recall < 100%"
+
+
+def test_sparse_equals_full_when_budget_covers_all():
+    c = config_case(3, scale=0.25, batch=4)
+    g = gpu(c)
+    mp = c.max_pages
+    dump = torch.empty((4, 32, mp * 16), device=DEV)
+    lse = torch.empty(4, 32, device=DEV)
+    o_full = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                            max_pages_per_row=mp, lse=lse, logits_dump=dump)
+    s = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
+    idx, ip = K.select_pages(s, g.kv_indptr, g.block_table, mp, 8)
+    assert torch.equal(ip, g.kv_indptr) and torch.equal(idx[:int(ip[-1])], g.kv_indices)
+    o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=mp)
+    assert torch.equal(o_sp, o_full)
+
+
+def test_pack_page_indices():
+    gen = torch.Generator().manual_seed(7)
+    pps = 40
+    slot_bt = torch.randint(0, 10000, (6, pps), generator=gen, dtype=torch.int32)
+    active = torch.tensor([5, 1, 2, 0], dtype=torch.int32)
+    starts = torch.tensor([0, 10, 3, 39], dtype=torch.int32)
+    counts = torch.tensor([40, 30, 0, 1], dtype=torch.int32)
+    indptr = torch.tensor([0, 40, 70, 70, 71], dtype=torch.int32)
+    out = torch.full((71,), -1, dtype=torch.int32)
+    row = torch.full((4, pps), -1, dtype=torch.int32)
+    out_g, row_g = out.to(DEV), row.to(DEV)
+    K.pack_page_indices(slot_bt.to(DEV), active.to(DEV), starts.to(DEV), counts.to(DEV), indptr.to(DEV),
+                        out_g, row_g, 4, 40, write_row_block=True)
+    O.pack_page_indices(slot_bt, active, starts, counts, indptr, out, row, 4, True)
+    assert torch.equal(out_g.cpu(), out) and torch.equal(row_g.cpu(), row)
+
+
+def test_decode_page_info():
+    gen = torch.Generator().manual_seed(8)
+    B, pps, k = 7, 64, 9
+    cachelens = torch.tensor([0, 14, 15, 16, 31, 200, 1100], dtype=torch.int32)  # last row overflows
+    slot_bt = torch.randint(0, 99999, (B, pps), generator=gen, dtype=torch.int32)
+    ind = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    ip = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    last = torch.zeros(B, dtype=torch.int32, device=DEV)
+    rbt = torch.full((B, pps), -7, dtype=torch.int32, device=DEV)
+    sub_i = torch.zeros(B * k, dtype=torch.int32, device=DEV)
+    sub_p = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    flag = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, k, 1.0, True, ip, ind, last, rbt, sub_i, sub_p, flag)
+    torch.cuda.synchronize()
+    pc, lp, sc, ss = O.decode_page_info(cachelens[:-1], pps, k)
+    pc = torch.cat([pc, torch.tensor([pps])])     # the overflowing row is clamped to a full table
+    lp = torch.cat([lp, torch.tensor([16])])
+    sc = torch.clamp(pc, max=k)
+    ss = pc - sc
+    assert last.cpu().tolist() == lp.tolist()
+    want_ip = [0] + torch.cumsum(pc, 0).tolist()
+    assert ip.cpu().tolist() == want_ip
+    for b in range(B):
+        row = slot_bt[b, :int(pc[b])]
+        assert ind[want_ip[b]:want_ip[b + 1]].cpu().tolist() == row.tolist()
+        assert rbt[b, :int(pc[b])].cpu().tolist() == row.tolist()
+        assert rbt[b, int(pc[b]):].cpu().eq(0).all()
+    sp = [0] + torch.cumsum(sc, 0).tolist()
+    assert sub_p.cpu().tolist() == sp
+    for b in range(B):
+        assert sub_i[sp[b]:sp[b + 1]].cpu().tolist() == slot_bt[b, int(ss[b]):int(pc[b])].tolist()
+    assert int(flag) == int(O.use_subset_decision(int(pc.sum()), int(sc.sum()), 1.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_append_kv(dtype):
+    c = make_case(batch=3, hq=8, hkv=4, kv_lens=[17, 32, 50], seed=9, dtype=dtype, trailing_empty_page=True)
+    gen = torch.Generator().manual_seed(1)
+    nnz = 6
+    app = torch.tensor([0, 1, 1, 6], dtype=torch.int32)  # row 1 appends nothing; row 2 appends 5 (prefill-like)
+    qkv = torch.randn(nnz, 16, 128, generator=gen).to(dtype)  # strided k/v views like wqkv(x).split
+    k, v = qkv[:, 8:12], qkv[:, 12:16]
+    cache = c.kv_cache.clone()
+    O.append_kv(k.float(), v.float(), app, cache, c.kv_indices, c.kv_indptr, c.kv_last_page_len)
+    gcache = c.kv_cache.to(DEV)
+    K.append_kv(k.to(DEV), v.to(DEV), app.to(DEV), gcache, c.kv_indices.to(DEV), c.kv_indptr.to(DEV),
+                c.kv_last_page_len.to(DEV))
+    assert torch.equal(gcache.cpu(), cache)
+
+
+@pytest.mark.parametrize("llama31", [False, True])
+def test_rope(llama31):
+    gen = torch.Generator().manual_seed(2)
+    nnz, hq, hkv = 7, 32, 8
+    q = torch.randn(nnz, hq, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(nnz, hkv, 128, generator=gen).to(torch.bfloat16)
+    indptr = torch.tensor([0, 1, 5, 7], dtype=torch.int32)
+    offsets = torch.tensor([8191, 0, 123], dtype=torch.int32)
+    kw = dict(rope_scale=8.0 if llama31 else 1.0, rope_theta=5e5)
+    if llama31:
+        kw.update(low_freq_factor=1.0, high_freq_factor=4.0, old_context_len=8192)
+    qo, ko = K.rope(q.to(DEV), k.to(DEV), indptr.to(DEV), offsets.to(DEV), **kw)
+    f = O.rope_frequencies(128, kw["rope_scale"], kw["rope_theta"], kw.get("low_freq_factor"),
+                           kw.get("high_freq_factor"), kw.get("old_context_len"))
+    qr = O.apply_rope(q.float(), indptr, offsets, f)
+    kr = O.apply_rope(k.float(), indptr, offsets, f)
+    # fp32 angles at positions ~8k are good to ~1e-3 rad; bf16 output rounding ~4e-3 relative
+    assert (qo.float().cpu() - qr).abs().max().item() < 3e-2
+    assert (ko.float().cpu() - kr).abs().max().item() < 3e-2
+
+
+def test_decode_is_deterministic_full_size():
+    """Config 3 at full size: two runs are bit-identical; score sums lie in [1, Hq]."""
+    c = config_case(3, device=DEV)
+    mp = c.max_pages
+    B, hq = c.q.shape[:2]
+    dump = torch.empty((B, hq, mp * 16), device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    o1 = K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                        max_pages_per_row=mp, lse=lse, logits_dump=dump)
+    o2 = K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                        max_pages_per_row=mp)
+    s = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+    idx, ip = K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L)
+    idx2, ip2 = K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    tot = s.sum(1)
+    assert bool((tot > 1 - 1e-3).all()) and bool((tot < hq + 1e-3).all())
+    assert torch.equal(idx, idx2) and torch.equal(ip, ip2)
+    assert ip.cpu().tolist() == [c.k * b for b in range(B + 1)]
+    # ascending logical order, forced last L pages
+    inv = torch.empty(c.kv_cache.shape[0], dtype=torch.int64, device=DEV)
+    inv[c.block_table.flatten().long()] = torch.arange(mp, device=DEV).repeat(B)
+    pos = inv[idx.long()].view(B, c.k)
+    assert bool((pos[:, 1:] > pos[:, :-1]).all())
+    assert bool((pos[:, -c.L:] == torch.arange(mp - c.L, mp, device=DEV)).all())

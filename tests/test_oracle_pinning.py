@@ -1,0 +1,373 @@
+"""Pins the CPU oracle (oracle/delta_oracle.py) to brute force, closed forms and invariants.
+
+The reference ships no golden vectors for this path (its tests are end-to-end
+runners), so each oracle function is pinned here by an independent route:
+pure-Python loops on tiny inputs, closed forms the math fixes, and invariants a
+plausible mistake (wrong head map, missing bias, wrong tie order, off-by-one
+in kv_len, transposed operand) would break.
+"""
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import delta_oracle as O
+
+F32_MAX = float(np.finfo(np.float32).max)
+
+
+def tiny_case(seed=0, B=3, hq=4, hkv=2, lens=(20, 33, 16), dtype=torch.float64, trailing=False):
+    from delta_amd.workloads import make_case
+    return make_case(batch=B, hq=hq, hkv=hkv, kv_lens=list(lens), dtype=dtype, seed=seed,
+                     page_order="randperm", k=2, L=1, trailing_empty_page=trailing)
+
+
+# ---------------------------------------------------------------- page tables
+
+def test_kv_lengths_flashinfer_convention():
+    indptr = torch.tensor([0, 3, 3, 5, 6], dtype=torch.int32)
+    last = torch.tensor([16, 0, 1, 0], dtype=torch.int32)
+    assert O.kv_lengths(indptr, last).tolist() == [48, 0, 17, 0]
+
+
+def _request_plan_sim(n_tokens_per_step):
+    """scheduler.py:60-74 restated as a loop: pages/last after each plan()."""
+    pages, last = 1, 0  # initialize_pages
+    out = []
+    for q in n_tokens_per_step:
+        last += q
+        while last >= 16:
+            pages += 1
+            last -= 16
+        out.append((pages, last))
+    return out
+
+
+def test_decode_page_info_matches_request_plan():
+    steps = [4] + [1] * 60  # dummy4tok prompt, then decode steps
+    sim = _request_plan_sim(steps)
+    # before decode step i the row holds cachelens = 4 + (i - 1) tokens
+    for i in range(1, len(steps)):
+        cl = torch.tensor([4 + i - 1], dtype=torch.int32)
+        pc, last, sc, ss = O.decode_page_info(cl, 100, k=3)
+        assert (int(pc[0]), int(last[0])) == sim[i]
+        assert int(sc[0]) == min(sim[i][0], 3) and int(ss[0]) == sim[i][0] - int(sc[0])
+
+
+def test_use_subset_gate():
+    assert O.use_subset_decision(100, 20, 1.0)
+    assert not O.use_subset_decision(20, 20, 1.0)       # ratio 1 is not > 1
+    assert not O.use_subset_decision(100, 20, 5.0)
+    assert not O.use_subset_decision(100, 0, 1.0)
+    assert not O.use_subset_decision(100, 20, 1.0, enable_selective_cache=False)
+
+
+# ---------------------------------------------------------------- dump logits
+
+def test_dump_logits_bruteforce():
+    c = tiny_case(seed=3)
+    d = 128
+    scale = 1.0 / math.sqrt(d)
+    S = 48
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, scale, S)
+    G = c.q.shape[1] // c.kv_cache.shape[3]
+    for b in range(c.batch):
+        pages = c.kv_indices[int(c.kv_indptr[b]):int(c.kv_indptr[b + 1])].tolist()
+        n = c.kv_lens[b]
+        for h in range(c.q.shape[1]):
+            for t in range(S):
+                if t >= n:
+                    assert x[b, h, t] == float("-inf")
+                    continue
+                page, slot = pages[t // 16], t % 16
+                krow = c.kv_cache[page, 0, slot, h // G].tolist()
+                want = math.fsum(a * bb for a, bb in zip(c.q[b, h].tolist(), krow)) * scale
+                assert abs(float(x[b, h, t]) - want) <= 1e-6 * max(1.0, abs(want))
+
+
+def test_dump_uses_gqa_head_map():
+    # A map h % Hkv instead of h // G would pair head 1 with kv head 1: make them differ.
+    c = tiny_case(seed=4, B=1, hq=4, hkv=2, lens=(16,))
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 1.0, 16)
+    page = int(c.kv_indices[0])
+    k0 = c.kv_cache[page, 0, 0, 0]
+    assert torch.allclose(x[0, 1, 0].double(), (c.q[0, 1] @ k0).double(), rtol=1e-6)
+
+
+# ---------------------------------------------------------------- page scores
+
+def _scores_bruteforce(x, B, max_pages):
+    hq = x.shape[1]
+    out = [[0.0] * max_pages for _ in range(B)]
+    for b in range(B):
+        probs = []
+        for h in range(hq):
+            row = x[b, h, :max_pages * 16].tolist()
+            m = max(row)
+            e = [0.0 if v == float("-inf") else math.exp(v - m) for v in row]
+            s = math.fsum(e)
+            probs.append([v / s for v in e])
+        for j in range(max_pages):
+            out[b][j] = math.fsum(max(probs[h][t] for h in range(hq)) for t in range(16 * j, 16 * j + 16))
+    return torch.tensor(out, dtype=torch.float64)
+
+
+def test_page_scores_bruteforce():
+    torch.manual_seed(0)
+    B, hq, S = 2, 5, 80
+    x = torch.randn(B, hq, S, dtype=torch.float32) * 3
+    x[0, :, 70:] = float("-inf")
+    x[1, :, 41:] = float("-inf")
+    want = _scores_bruteforce(x.double(), B, 5)
+    got64 = O.legacy_softmax_page_scores(x, B, 5, compute_dtype=torch.float64)
+    got32 = O.legacy_softmax_page_scores(x, B, 5)
+    assert torch.allclose(got64.double(), want, rtol=1e-6, atol=0)
+    assert torch.allclose(got32.double(), want, rtol=1e-5, atol=1e-9)
+
+
+def test_page_scores_closed_forms():
+    c = tiny_case(seed=5, B=2, hq=4, hkv=2, lens=(37, 64))
+    mp = 4
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.1, mp * 16)
+    s = O.legacy_softmax_page_scores(x, 2, mp, compute_dtype=torch.float64).double()
+    # every head's softmax sums to 1: the head-max sum lies in [1, Hq]
+    assert (s.sum(1) >= 1 - 1e-6).all() and (s.sum(1) <= 4 + 1e-6).all()
+    # row 0 holds 37 tokens = 3 pages: page 3 scores exactly 0
+    assert s[0, 3] == 0.0
+    # one head: sum of scores == 1
+    s1 = O.legacy_softmax_page_scores(x[:, :1], 2, mp, compute_dtype=torch.float64).double()
+    assert torch.allclose(s1.sum(1), torch.ones(2, dtype=torch.float64), atol=1e-12)
+    # identical heads: head-max == that head
+    xr = x[:, :1].repeat(1, 3, 1)
+    s3 = O.legacy_softmax_page_scores(xr, 2, mp, compute_dtype=torch.float64).double()
+    assert torch.allclose(s3, s1, atol=1e-15)
+
+
+def test_scores_invariant_to_page_permutation_and_v():
+    c = tiny_case(seed=6, B=2, lens=(40, 60))
+    mp = 4
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.2, mp * 16)
+    # move every page to a new physical slot; same logical content
+    n = c.kv_cache.shape[0]
+    perm = torch.randperm(n, generator=torch.Generator().manual_seed(1))
+    cache2 = torch.empty_like(c.kv_cache)
+    cache2[perm] = c.kv_cache
+    idx2 = perm[c.kv_indices.long()].to(torch.int32)
+    cache2[:, 1] = torch.randn_like(cache2[:, 1])  # V must not matter
+    x2 = O.dump_logits(c.q, cache2, c.kv_indptr, idx2, c.kv_last_page_len, 0.2, mp * 16)
+    assert torch.equal(x, x2)
+
+
+# ---------------------------------------------------------------- selector
+
+def _select_bruteforce(scores, counts, bt, k, L, bias):
+    B, n = scores.shape
+    idx, indptr = [], [0]
+    for b in range(B):
+        tp = int(counts[b])
+        keyed = []
+        for j in range(n):
+            s = float(scores[b, j])
+            if s != s:
+                s = float("-inf")
+            elif s == float("inf"):
+                s = F32_MAX
+            if bias:
+                bj = float(np.float32(float(j) * float(np.float32(bias))))  # exact product, one rounding
+                s = float(np.float32(-bj + s)) if s not in (float("-inf"), F32_MAX) else s
+            if max(tp - L, 0) <= j < tp:
+                s = float("inf")
+            if j >= tp:
+                s = float("-inf")
+            keyed.append((-s, j))
+        chosen = sorted(sorted(keyed)[:k], key=lambda p: p[1])
+        keep = [j for _, j in chosen][:min(tp, k)]
+        idx.extend(int(bt[b, j]) for j in keep)
+        indptr.append(indptr[-1] + len(keep))
+    return idx, indptr
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_selector_bruteforce(seed):
+    rng = np.random.default_rng(seed)
+    B, n, k, L = 4, 24, 6, 2
+    scores = torch.tensor(rng.random((B, n)), dtype=torch.float32)
+    # quantised values so exact ties (and bias-broken ties) happen often
+    scores = torch.round(scores * 8) / 8
+    scores[0, 3] = float("nan")
+    scores[1, 5] = float("inf")
+    scores[2, 7] = float("-inf")
+    counts = torch.tensor([24, 10, 5, 17])
+    bt = torch.tensor(rng.permutation(B * n).reshape(B, n), dtype=torch.int32)
+    for bias in (1e-7, 0.0):
+        got_i, got_p = O.select_pages(scores, counts, bt, k, L, bias)
+        want_i, want_p = _select_bruteforce(scores, counts, bt, k, L, bias)
+        assert got_i.tolist() == want_i and got_p.tolist() == want_p
+
+
+def test_selector_bias_rounding_is_fp32():
+    b = O.position_bias(1000, 1e-7)
+    for j in (1, 3, 7, 999):
+        assert b[j] == np.float32(-(np.float64(j) * np.float64(np.float32(1e-7))))
+    # bias breaks exact ties toward the lower page index
+    scores = torch.ones(1, 10)
+    counts = torch.tensor([10])
+    bt = torch.arange(10, dtype=torch.int32)[None]
+    idx, _ = O.select_pages(scores, counts, bt, 4, 1, 1e-7)
+    assert idx.tolist() == [0, 1, 2, 9]
+
+
+def test_selector_invariants():
+    rng = np.random.default_rng(7)
+    B, n, k, L = 5, 40, 12, 4
+    scores = torch.tensor(rng.random((B, n)), dtype=torch.float32)
+    counts = torch.tensor([40, 13, 12, 3, 31])
+    bt = torch.tensor(rng.permutation(B * n).reshape(B, n), dtype=torch.int32)
+    idx, indptr = O.select_pages(scores, counts, bt, k, L)
+    for b in range(B):
+        tp = int(counts[b])
+        row = idx[indptr[b]:indptr[b + 1]].tolist()
+        assert len(row) == min(tp, k)
+        pos = [list(bt[b]).index(v) for v in row]
+        assert pos == sorted(pos) and all(p < tp for p in pos)
+        assert set(range(max(tp - L, 0), tp)) <= set(pos)
+    # fixed path == general path when every row has >= k pages
+    full = torch.full((B,), n)
+    fi, fp = O.select_pages(scores, full, bt, k, L, fixed_count=True)
+    gi, gp = O.select_pages(scores, full, bt, k, L)
+    assert torch.equal(fi, gi) and torch.equal(fp, gp)
+    assert fp.tolist() == [k * b for b in range(B + 1)]
+
+
+def test_selector_monotone():
+    rng = np.random.default_rng(8)
+    scores = torch.tensor(rng.random((1, 30)), dtype=torch.float32)
+    counts = torch.tensor([30])
+    bt = torch.arange(30, dtype=torch.int32)[None]
+    idx, _ = O.select_pages(scores, counts, bt, 8, 2)
+    sel = set(idx.tolist())
+    s2 = scores.clone()
+    j_in = min(sel)
+    s2[0, j_in] += 10.0            # raising a selected page keeps it
+    j_out = next(j for j in range(30) if j not in sel)
+    s2[0, j_out] -= 10.0           # lowering an unselected page keeps it out
+    idx2, _ = O.select_pages(s2, counts, bt, 8, 2)
+    assert set(idx2.tolist()) == sel
+
+
+def test_selector_k_out_of_range_raises():
+    with pytest.raises(RuntimeError):
+        O.select_pages(torch.zeros(1, 4), torch.tensor([4]), torch.zeros(1, 4, dtype=torch.int32), 5, 1)
+
+
+# ---------------------------------------------------------------- attention
+
+def test_attention_matches_sdpa():
+    c = tiny_case(seed=9, B=3, hq=8, hkv=2, lens=(19, 48, 5))
+    o, lse = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.09)
+    G = 4
+    for b in range(3):
+        k, v = O.gather_row_kv(c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, b)
+        kk = k.double().repeat_interleave(G, 1).transpose(0, 1)  # [Hq, n, d]
+        vv = v.double().repeat_interleave(G, 1).transpose(0, 1)
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            c.q[b].double()[:, None, :], kk, vv, scale=0.09)[:, 0]
+        assert torch.allclose(o[b].double(), ref, atol=1e-6)
+        s = (c.q[b].double()[:, None, :] * kk).sum(-1) * 0.09
+        assert torch.allclose(lse[b].double(), torch.logsumexp(s, -1), atol=1e-5)
+
+
+def test_sparse_equals_full_when_all_pages_selected():
+    c = tiny_case(seed=10, B=2, lens=(40, 70))
+    res = O.selective_step(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, k=5, L=2)
+    assert torch.equal(res["indices"], c.kv_indices) and torch.equal(res["indptr"], c.kv_indptr)
+    assert torch.allclose(res["o_full"], res["o_sparse"], atol=0)
+
+
+def test_attention_empty_row_and_permutation():
+    c = tiny_case(seed=11, B=2, lens=(33, 20))
+    last = c.kv_last_page_len.clone()
+    indptr = c.kv_indptr.clone()
+    indptr[2] = indptr[1]  # row 1 has no pages
+    last[1] = 0
+    o, lse = O.paged_decode_attention(c.q, c.kv_cache, indptr, c.kv_indices, last, 0.1)
+    assert torch.all(o[1] == 0) and torch.all(torch.isinf(lse[1]))
+    n = c.kv_cache.shape[0]
+    perm = torch.randperm(n, generator=torch.Generator().manual_seed(2))
+    cache2 = torch.empty_like(c.kv_cache)
+    cache2[perm] = c.kv_cache
+    o2, _ = O.paged_decode_attention(c.q, cache2, c.kv_indptr, perm[c.kv_indices.long()].int(),
+                                     c.kv_last_page_len, 0.1)
+    o1, _ = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.1)
+    assert torch.allclose(o1, o2, atol=1e-7)
+
+
+def test_trailing_empty_page_contributes_nothing():
+    c = tiny_case(seed=12, B=1, lens=(32,), trailing=True)
+    assert c.kv_last_page_len.tolist() == [0] and int(c.kv_indptr[1]) == 3
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.1, 48)
+    s = O.legacy_softmax_page_scores(x, 1, 3)
+    assert s[0, 2] == 0
+    idx, _ = O.select_pages(s, torch.tensor([3]), c.block_table, 2, 1)
+    assert int(idx[-1]) == int(c.kv_indices[2])  # the empty last page is forced in
+
+
+# ---------------------------------------------------------------- metadata, append, rope
+
+def test_pack_page_indices_bruteforce():
+    rng = random.Random(0)
+    pps = 9
+    slot_bt = torch.tensor([[rng.randrange(1000) for _ in range(pps)] for _ in range(5)], dtype=torch.int32)
+    active = torch.tensor([3, 0, 4], dtype=torch.int32)
+    starts = torch.tensor([2, 0, 5], dtype=torch.int32)
+    counts = torch.tensor([4, 9, 0], dtype=torch.int32)
+    indptr = torch.tensor([0, 4, 13, 13], dtype=torch.int32)
+    out = torch.full((13,), -1, dtype=torch.int32)
+    row_bt = torch.full((3, pps), -1, dtype=torch.int32)
+    O.pack_page_indices(slot_bt, active, starts, counts, indptr, out, row_bt, 3, True)
+    want = slot_bt[3, 2:6].tolist() + slot_bt[0, :9].tolist()
+    assert out.tolist() == want
+    assert row_bt[0, :4].tolist() == slot_bt[3, 2:6].tolist() and row_bt[0, 4:].tolist() == [-1] * 5
+    assert row_bt[2].tolist() == [-1] * pps
+
+
+def test_append_then_gather_round_trip():
+    c = tiny_case(seed=13, B=2, lens=(17, 40))
+    cache = c.kv_cache.clone()
+    k = torch.randn(3, 2, 128, dtype=torch.float64)
+    v = torch.randn(3, 2, 128, dtype=torch.float64)
+    app = torch.tensor([0, 1, 3], dtype=torch.int32)  # 1 token for row 0, 2 for row 1
+    O.append_kv(k, v, app, cache, c.kv_indices, c.kv_indptr, c.kv_last_page_len)
+    k0, v0 = O.gather_row_kv(cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0)
+    k1, v1 = O.gather_row_kv(cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 1)
+    assert torch.equal(k0[-1], k[0]) and torch.equal(v0[-1], v[0])
+    assert torch.equal(k1[-2:], k[1:]) and torch.equal(v1[-2:], v[1:])
+    # nothing else moved
+    ka, _ = O.gather_row_kv(c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 1)
+    assert torch.equal(k1[:-2], ka[:-2])
+
+
+def test_rope_closed_forms():
+    torch.manual_seed(1)
+    x = torch.randn(4, 3, 128, dtype=torch.float64)
+    f = O.rope_frequencies(128, 1.0, 1e4)
+    assert f[0] == 1.0 and abs(float(f[1]) - 1e4 ** (-2 / 128)) < 1e-15
+    indptr = torch.tensor([0, 4], dtype=torch.int32)
+    # position 0 is the identity
+    y0 = O.apply_rope(x[:1], torch.tensor([0, 1], dtype=torch.int32), torch.tensor([0], dtype=torch.int32), f)
+    assert torch.allclose(y0.double(), x[:1], atol=1e-6)
+    # rotation preserves every pair's norm
+    y = O.apply_rope(x, indptr, torch.tensor([100], dtype=torch.int32), f).double()
+    n0 = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
+    n1 = y[..., 0::2] ** 2 + y[..., 1::2] ** 2
+    assert torch.allclose(n0, n1, rtol=1e-5)
+    # token i of the row sits at offset + i: pair 0 of token 1 turned by (offset+1) * f0
+    a = 101.0
+    want0 = x[1, 0, 0] * math.cos(a) - x[1, 0, 1] * math.sin(a)
+    assert abs(float(y[1, 0, 0]) - float(want0)) < 1e-5
+    # rope_scale divides the frequencies; llama3.1 keeps high frequencies unscaled
+    f2 = O.rope_frequencies(128, 8.0, 5e5, 1.0, 4.0, 8192)
+    assert abs(float(f2[0]) - 1.0) < 1e-12
+    assert abs(float(f2[-1]) - float(O.rope_frequencies(128, 8.0, 5e5)[-1])) < 1e-18

@@ -1,0 +1,299 @@
+#!/usr/bin/env python
+"""Selective-KV decode benchmark on one MI355X.
+
+Workload: a random-init Llama-3-8B-shaped model
+(32 layers, dim 4096, 32 q / 8 kv heads, d 128, bf16), batch 32, 8192-token
+context per row in 16-token pages drawn from a shuffled pool, layers 0-1 full
+(layer 1 is the planner), a 2048-token budget (128 pages, L = 8) for layers
+2-31, every decode step one hipGraph replay.  A "step" is one decode step of
+the whole batch; ``value`` = batch / step time (tokens/s).
+
+Also measured, in the same process:
+  * the same engine with the selective cache off (full-cache decode);
+  * per-kernel HBM roofline: the subset attention kernel (dominant: 30 launches
+    per step), the planner kernel, the full-cache kernel and the standalone
+    K-only scorer, each timed with HIP events on its launch stream; achieved
+    GB/s from algorithmic bytes (K/V of the attended tokens once, q, o, the
+    page indices, + the logits for the scorers);
+  * a CPU baseline: the oracle's PyTorch-CPU restatement of the same math,
+    composed per step from per-op timings on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "selective decode tokens/s (bs×ctx) + page-score/attn HBM GB/s vs peak"
+
+# config 3
+MODEL = "llama-3-8b"
+BATCH = 32
+CONTEXT = 8192
+BUDGET_PAGES = 128
+L_LAST = 8
+FULL_LAYERS = [0, 1]
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_engine(torch, steps_budget: int):
+    from delta_amd.backend import LMBackend
+    eng = LMBackend(dtype=torch.bfloat16, device="cuda:0", cuda_graph_decode=True)
+    eng.load_model(f"random:{MODEL}", seed=0)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = list(FULL_LAYERS)
+    cfg.subset_cache_size = BUDGET_PAGES
+    cfg.compression_ratio = 1.0
+    cfg.L = L_LAST
+    eng.setup_caches(max_batch_size=BATCH, max_seq_length=CONTEXT + steps_budget + 16)
+    eng.prepare_synthetic_decode(CONTEXT, decode_budget=steps_budget, seed=0)
+    return eng
+
+
+def time_steps(torch, eng, warmup: int, steps: int) -> float:
+    """ms per decode step over ``steps`` graph replays (after ``warmup`` replays)."""
+    eng.decode_steps(warmup)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    eng.decode_steps(steps)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_roofline(torch, reps: int = 50):
+    """Time each hot-path kernel at the config-3 layer shape with HIP events on its stream."""
+    from delta_amd import kernels as K
+    from delta_amd.workloads import config_case
+    c = config_case(3, device="cuda:0")
+    B, hq = c.q.shape[:2]
+    hkv = c.kv_cache.shape[3]
+    mp = c.max_pages
+    esz = c.kv_cache.element_size()
+    dump = torch.empty((B, hq, mp * 16), device="cuda:0")
+    lse = torch.empty((B, hq), device="cuda:0")
+    K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
+                   lse=lse, logits_dump=dump)
+    scores = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+    idx, ip = K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L)
+    torch.cuda.synchronize()
+    last = c.kv_last_page_len.cpu()
+    ntok_full = sum(c.kv_lens)
+    ntok_sub = sum((c.k - 1) * 16 + int(l) for l in last)
+    qo = 2 * B * hq * 128 * esz
+    row_kv = hkv * 128 * esz  # one token of K (or V) for all kv heads
+
+    def timed(fn):
+        stream = torch.cuda.current_stream()
+        for _ in range(3):
+            fn()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / reps  # us
+
+    res = {}
+
+    def add(name, us, nbytes, note):
+        res[name] = {"us": round(us, 2), "bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "what": note}
+
+    add("paged_decode_subset_kernel",
+        timed(lambda: K.paged_decode(c.q, c.kv_cache, ip, idx, c.kv_last_page_len, max_pages_per_row=c.k,
+                                     subset=True)),
+        ntok_sub * 2 * row_kv + qo + B * c.k * 4, "K+V of the 128 selected pages/row, q, o, page ids")
+    add("paged_decode_full_kernel",
+        timed(lambda: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                                     max_pages_per_row=mp)),
+        ntok_full * 2 * row_kv + qo + B * mp * 4, "K+V of all 512 pages/row, q, o, page ids")
+    add("paged_decode_plan_kernel",
+        timed(lambda: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                                     max_pages_per_row=mp, lse=lse, logits_dump=dump)),
+        ntok_full * 2 * row_kv + qo + B * mp * 4 + ntok_full * hq * 4,
+        "planner: full attention + fp32 logits dump")
+    add("legacy_softmax_score_kernel",
+        timed(lambda: K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse,
+                                                scores=scores)),
+        ntok_full * hq * 4 + B * mp * 4, "reads the logits dump once, writes page scores")
+    sc_dump = torch.empty_like(dump)
+    add("page_score_kv (standalone scorer)",
+        timed(lambda: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, mp,
+                                   logits_dump=sc_dump, scores=scores)),
+        ntok_full * row_kv + B * hq * 128 * esz + B * mp * 4 + B * mp * 4,
+        "K read once + q + page table + scores (logit spill not counted)")
+    add("select_pages_kernel",
+        timed(lambda: K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L, out_indices=idx, out_indptr=ip)),
+        B * mp * 4 * 2 + B * c.k * 4, "latency-bound selection (reported in us)")
+    del c, dump, sc_dump
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(torch, sample_rows: int = 2):
+    """Oracle (PyTorch CPU, fp32) timing of the same step, composed from per-op timings.
+
+    Attention ops run on ``sample_rows`` rows of the config-3 layer and are scaled to the
+    batch; the dense decoder layer (GEMMs, norms) and lm_head run at the full batch with
+    random fp32 weights.  Step = 2 full layers (one of them the planner with dump, score,
+    selection) + 30 subset layers + 32 dense layers + lm_head."""
+    from delta_amd.workloads import make_case
+    from oracle import delta_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+
+    def med(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    c = make_case(batch=sample_rows, hq=32, hkv=8, kv_lens=CONTEXT, dtype=torch.float32, seed=0,
+                  page_order="shuffle", k=BUDGET_PAGES, L=L_LAST)
+    scale = 1 / math.sqrt(128)
+    mp = c.max_pages
+    f32 = torch.float32
+    t_full = med(lambda: O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                  c.kv_last_page_len, scale, compute_dtype=f32))
+
+    def plan():
+        x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, scale, mp * 16,
+                          compute_dtype=f32)
+        s = O.legacy_softmax_page_scores(x, sample_rows, mp)
+        return O.select_pages(s, c.kv_indptr[1:] - c.kv_indptr[:-1], c.block_table, c.k, c.L)
+
+    t_plan = med(plan)
+    idx, ip = plan()
+    t_sub = med(lambda: O.paged_decode_attention(c.q, c.kv_cache, ip, idx, c.kv_last_page_len, scale,
+                                                 compute_dtype=f32))
+    per_row = (t_full + (t_full + t_plan) + 30 * t_sub) / sample_rows
+    dim, inter, vocab = 4096, 14336, 128256
+    g = torch.Generator().manual_seed(0)
+    w = {n: torch.randn(shape, generator=g) * 0.02 for n, shape in
+         (("wqkv", (6144, dim)), ("wo", (dim, dim)), ("w1", (inter, dim)), ("w3", (inter, dim)),
+          ("w2", (dim, inter)))}
+    x = torch.randn(BATCH, dim, generator=g)
+
+    def dense():
+        h = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-5)
+        qkv = h @ w["wqkv"].T
+        y = x + qkv[:, :dim] @ w["wo"].T
+        hn = y * torch.rsqrt((y * y).mean(-1, keepdim=True) + 1e-5)
+        return y + (torch.nn.functional.silu(hn @ w["w1"].T) * (hn @ w["w3"].T)) @ w["w2"].T
+
+    t_dense = med(dense)
+    del w
+    lm = torch.randn(vocab, dim, generator=g) * 0.02
+    t_head = med(lambda: (x @ lm.T).argmax(-1))
+    del lm
+    step = BATCH * per_row + 32 * t_dense + t_head
+    return {"value": round(BATCH / step, 3), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"oracle fp32 on {sample_rows} of {BATCH} rows of the config-3 layer (8192 tokens, "
+                       f"128-page budget), scaled to the batch: full {t_full * 1e3:.1f} ms, planner extra "
+                       f"{t_plan * 1e3:.1f} ms, subset {t_sub * 1e3:.1f} ms per {sample_rows} rows; dense layer "
+                       f"{t_dense * 1e3:.1f} ms and lm_head {t_head * 1e3:.1f} ms at batch {BATCH}; "
+                       f"composed step {step:.2f} s")}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-full-compare", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "The selective decode shards by batch with no cross-GPU exchange; run --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    torch.manual_seed(0)
+    budget = args.warmup + args.steps + 16
+    if not args.no_full_compare:
+        budget += args.warmup + args.steps
+    log(f"building engine ({MODEL}, B={BATCH}, ctx={CONTEXT})")
+    eng = build_engine(torch, budget)
+    log("selective decode (hipGraph)")
+    ms = time_steps(torch, eng, args.warmup, args.steps)
+    tok_s = BATCH / ms * 1e3
+    log(f"selective: {ms:.3f} ms/step, {tok_s:.1f} tokens/s")
+    full = None
+    if not args.no_full_compare:
+        eng.enable_selective_cache = False
+        eng._decode_graph = None
+        ms_full = time_steps(torch, eng, args.warmup, args.steps)
+        full = {"ms_per_step": round(ms_full, 4), "tokens_per_s": round(BATCH / ms_full * 1e3, 2)}
+        log(f"full cache: {ms_full:.3f} ms/step")
+    from delta_amd import ops
+    ops.set_active_backend(None)
+    del eng
+    torch.cuda.empty_cache()
+    log("kernel roofline")
+    kern = kernel_roofline(torch, args.kernel_reps)
+    for k, v in kern.items():
+        log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s ({100 * v['frac']:.1f}% of peak)")
+    dom = kern["paged_decode_subset_kernel"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle)")
+        cpu = cpu_baseline(torch)
+        log(f"  cpu: {cpu['value']} tokens/s on {cpu['cores']} cores")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights, N(0,1) K/V, random current tokens",
+        "config": {"workload": "config3: Llama-3-8B-shaped decode step, B=32, 8192-token context, "
+                               "2048-token budget (128 pages, L=8), full layers [0,1], one hipGraph per step",
+                   "batch": BATCH, "context": CONTEXT, "budget_pages": BUDGET_PAGES, "page_size": 16},
+        "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": dom["frac"], "traffic": None, "kernel": "paged_decode_subset_kernel"},
+        "cpu_baseline": cpu,
+        "full_cache": full,
+        "speedup_vs_full_cache": round(tok_s / full["tokens_per_s"], 3) if full else None,
+        "kernels": kern,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -29,6 +29,9 @@ SIGNATURES = {
         c_int, c_int, c_int, c_int, c_int,    # batch, hq, hkv, head_dim, dtype
         c_float, c_int,                       # sm_scale, max_pages_per_row
         _P, c_size_t, _P]),                   # workspace, bytes, stream
+    "delta_paged_decode_subset": (c_int, [
+        _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P,
+        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),
     "delta_page_score_workspace_bytes": (c_size_t, [c_int, c_int]),
     "delta_page_scores_from_logits": (c_int, [
         _P, c_int64, c_int64, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, _P, c_size_t, _P]),
@@ -47,6 +50,7 @@ SIGNATURES = {
     "delta_append_kv": (c_int, [
         _P, c_int64, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int,
         c_int, c_int, _P]),
+    "delta_argmax_rows": (c_int, [_P, c_int64, c_int, c_int, c_int, _P, c_int64, _P]),
     "delta_rope": (c_int, [
         _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_float, c_int, c_float, c_float, c_float, _P]),

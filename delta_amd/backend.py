@@ -1,0 +1,555 @@
+"""LMBackend: DELTA's engine surface, with the selective decode step on gfx950.
+
+Public surface mirrors DELTA/Engine/DELTA/backend.py: the constructor and its
+validation (29-168), ``load_model`` (227), ``setup_caches`` (247-593),
+``add_requests`` (1480), ``run_scheduler_loop`` (1486-1553) and the
+``mylib::target_*`` attention ops bound per layer.  What differs is where the
+work runs:
+
+* Decode metadata is derived on the device (``delta_decode_page_info``) from
+  ``cachelens`` and a slot block table that holds every page a slot owns, so
+  a decode step needs no host planning (the reference rebuilds it on the host
+  each step, backend.py:2040-2172).
+* The planner layer's attention writes the logits dump and lse, then page
+  scores and the v2 selection run on the device straight into the subset CSR
+  (the reference runs them eagerly between graph segments, 1432-1447), so the
+  *whole* decode step -- metadata, every layer, argmax, the token feedback and
+  the ``cachelens`` advance -- is one hipGraph.
+* Idle slots point at a private scratch page with ``cachelens = 0`` so the
+  graph also covers partial batches.
+* Prefill / mixed steps run eagerly: each prompt token becomes a virtual
+  decode row over its causal prefix, on the same attention kernel.
+
+Out of scope on this build (raise): tensor parallelism, ``torch.compile``
+(no Triton), the v1 selector, the ``delta_lse`` scorer and an fp16 dump.
+"""
+from __future__ import annotations
+
+import json
+import math
+import os
+import time
+from collections import defaultdict
+from pathlib import Path
+from typing import List, Optional
+
+import torch
+
+from . import kernels as K
+from . import ops
+from .model import Transformer, build_random_model
+from .page_selector_v2 import PageSelectorV2
+from .public_config import FINAL_PUBLIC_DELTA_BACKEND_CONFIG as _CFG
+from .scheduler import BatchScheduler, PageManager, Request
+
+PAGE_SIZE = 16
+
+
+class _StepCSR:
+    """Page tables the attention ops read during one forward."""
+
+    __slots__ = ("mode", "kv_indptr", "kv_indices", "kv_last", "max_pages")
+
+    def __init__(self, mode, kv_indptr, kv_indices, kv_last, max_pages):
+        self.mode = mode
+        self.kv_indptr = kv_indptr
+        self.kv_indices = kv_indices
+        self.kv_last = kv_last
+        self.max_pages = max_pages
+
+
+class LMBackend:
+    def __init__(
+        self,
+        dtype=torch.bfloat16,
+        device: str = "cuda:0",
+        dec_len: int = 1,
+        draft_dec_len: int = None,
+        cuda_graph_decode: bool = False,
+        cuda_graph_delta_subset_segments: bool = _CFG["cuda_graph_delta_subset_segments"],
+        delta_impl_profile: bool = _CFG["delta_impl_profile"],
+        delta_fused_page_scores: bool = _CFG["delta_fused_page_scores"],
+        delta_fixed_selector: bool = _CFG["delta_fixed_selector"],
+        delta_fast_decode_page_info: bool = _CFG["delta_fast_decode_page_info"],
+        delta_v2_position_bias: bool = _CFG["delta_v2_position_bias"],
+        delta_debug_page_selection_parity: bool = False,
+        delta_debug_fast_decode_page_info_parity: bool = False,
+        delta_subset_plan_reuse: bool = _CFG["delta_subset_plan_reuse"],
+        delta_dump_buffer_dtype: str = _CFG["delta_dump_buffer_dtype"],
+        delta_page_score_impl: str = _CFG["delta_page_score_impl"],
+        page_selector_version: str = _CFG["page_selector_version"],
+    ) -> None:
+        # Same validation and messages as backend.py:49-64.
+        page_selector_version = str(page_selector_version).lower()
+        if page_selector_version not in {"v1", "v2"}:
+            raise ValueError(f"Unsupported page_selector_version={page_selector_version!r}; expected 'v1' or 'v2'")
+        delta_dump_buffer_dtype = str(delta_dump_buffer_dtype).lower()
+        if delta_dump_buffer_dtype not in {"fp16", "fp32"}:
+            raise ValueError(
+                f"Unsupported delta_dump_buffer_dtype={delta_dump_buffer_dtype!r}; expected 'fp16' or 'fp32'")
+        delta_page_score_impl = str(delta_page_score_impl).lower()
+        if delta_page_score_impl not in {"delta_lse", "del3_legacy_softmax"}:
+            raise ValueError("Unsupported delta_page_score_impl="
+                             f"{delta_page_score_impl!r}; expected 'delta_lse' or 'del3_legacy_softmax'")
+        # The public release path is the only one built for gfx950.
+        if page_selector_version != "v2":
+            raise NotImplementedError("page_selector_version='v1' is not built on this path (v2 only)")
+        if delta_dump_buffer_dtype != "fp32":
+            raise NotImplementedError("delta_dump_buffer_dtype='fp16' is not built on this path (fp32 only)")
+        if delta_page_score_impl != "del3_legacy_softmax":
+            raise NotImplementedError("delta_page_score_impl='delta_lse' is not built on this path")
+        if dec_len != 1 or draft_dec_len is not None:
+            raise NotImplementedError("speculative decoding (dec_len != 1) is not part of this path")
+
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.dec_len = dec_len
+        self.enable_cuda_graph_decode = bool(cuda_graph_decode)
+        self.enable_cuda_graph_delta_subset_segments = cuda_graph_delta_subset_segments
+        self.enable_delta_impl_profile = delta_impl_profile
+        self.enable_delta_fused_page_scores = delta_fused_page_scores
+        self.enable_delta_fixed_selector = delta_fixed_selector
+        self.enable_delta_fast_decode_page_info = delta_fast_decode_page_info
+        self.enable_delta_v2_position_bias = delta_v2_position_bias
+        self.enable_delta_debug_page_selection_parity = delta_debug_page_selection_parity
+        self.enable_delta_debug_fast_decode_page_info_parity = delta_debug_fast_decode_page_info_parity
+        self.enable_delta_subset_plan_reuse = delta_subset_plan_reuse
+        self.delta_dump_buffer_dtype = delta_dump_buffer_dtype
+        self.delta_page_score_impl = delta_page_score_impl
+        self.page_selector_version = page_selector_version
+
+        self.model: Optional[Transformer] = None
+        self.cachelens = None
+        self.is_main_process = True
+        self.tokenizer = None
+        self.scheduler = None
+        self.throughput_mode = False
+        self.timer = None
+        self._compiled = False
+        self._step: Optional[_StepCSR] = None
+        self._decode_graph: Optional[torch.cuda.CUDAGraph] = None
+        self._decode_graph_failed: Optional[str] = None
+        self._decode_graph_stats = defaultdict(int)
+        self._decode_graph_fallback_reasons = defaultdict(int)
+        self._pending_events = []
+        self._step_records = []
+        self._using_subset_cache_this_step = False
+
+    # ------------------------------------------------------------------ setup
+    def set_tokenizer(self, tokenizer):
+        self.tokenizer = tokenizer
+
+    def load_model(self, checkpoints, use_tp: bool = False, rank_group=None, group=None, seed: int = 0):
+        """Load a model (backend.py:227-228 -> utils.py:209-231).
+
+        ``checkpoints`` is either a ``model.pth`` state dict (loaded with
+        ``weights_only=True``; its parent directory names the shape, as in the
+        reference) or ``"random:<shape>"`` for a seeded random-init model.
+        """
+        if use_tp:
+            raise NotImplementedError("tensor parallelism is out of scope for this one-GPU path")
+        ck = str(checkpoints)
+        if ck.startswith("random:"):
+            self.model = build_random_model(ck[len("random:"):], self.device, self.dtype, seed=seed)
+            return
+        path = Path(ck)
+        model = build_random_model(path.parent.name, self.device, self.dtype, seed=seed)
+        state = torch.load(str(path), mmap=True, weights_only=True)
+        model.load_state_dict(state, assign=False, strict=False)
+        self.model = model.to(self.dtype)
+
+    def compile(self):
+        """torch.compile is not used on this path (it would need Triton); graphs replace it."""
+        self.enable_cuda_graph_decode = True
+
+    @torch.inference_mode()
+    def setup_caches(self, max_batch_size: int = 1, max_seq_length: int = 2048):
+        if self.model is None:
+            raise RuntimeError("load_model() first")
+        cfg = self.model.config
+        dev = self.device
+        self.max_length = max_seq_length
+        self.batch_size = max_batch_size
+        self.page_size = PAGE_SIZE
+        self.pages_per_slot = (max_seq_length + PAGE_SIZE - 1) // PAGE_SIZE + 1  # +1: trailing empty page
+        self.max_num_pages = self.pages_per_slot * max_batch_size
+        # one private scratch page per slot: idle slots append/read only there
+        self.num_pages = self.max_num_pages + max_batch_size
+        self.scratch_pages = torch.arange(self.max_num_pages, self.num_pages, dtype=torch.int32)
+        self.page_manager = PageManager(self.max_num_pages, seed=0)
+        self.scheduler = BatchScheduler(max_batch_size, dev, self.is_main_process, self.pages_per_slot,
+                                        PAGE_SIZE, self.page_manager)
+
+        self.enable_selective_cache = bool(getattr(cfg, "enable_selective_cache", False))
+        self.subset_cache_size = int(getattr(cfg, "subset_cache_size", 64))
+        self.compression_ratio = float(getattr(cfg, "compression_ratio", 1.0))
+        self.L = int(getattr(cfg, "L", 8))
+        self.k_eff = max(1, min(self.subset_cache_size, self.pages_per_slot))
+
+        i32 = dict(dtype=torch.int32, device=dev)
+        B = max_batch_size
+        self.cachelens = torch.zeros(B, **i32)
+        self.active = torch.zeros(B, **i32)
+        self.slot_block_table = self.scratch_pages.to(dev)[:, None].repeat(1, self.pages_per_slot).contiguous()
+        self.page_selector = PageSelectorV2(B, self.pages_per_slot, True, self.k_eff,
+                                           self.compression_ratio, self.L, dev,
+                                           position_bias_scale=1e-7 if self.enable_delta_v2_position_bias else 0.0)
+        self.use_subset_flag = torch.zeros(1, **i32)
+        self.qo_indptr = torch.arange(B + 1, **i32)
+        self.static_tokens = torch.zeros((1, B), dtype=torch.long, device=dev)
+        hq = cfg.n_head
+        hkv = cfg.n_local_heads
+        self.dump = torch.full((B, hq, self.pages_per_slot * PAGE_SIZE), float("-inf"), dtype=torch.float32,
+                               device=dev)
+        self.lse = torch.zeros((B, hq), dtype=torch.float32, device=dev)
+        self.page_scores = torch.zeros((B, self.pages_per_slot), dtype=torch.float32, device=dev)
+        ws = max(K.decode_workspace_bytes(B, hq, hkv, self.pages_per_slot),
+                 K.decode_workspace_bytes(B, hq, hkv, self.k_eff), 256)
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
+        self._pinned_tokens = torch.zeros(B, dtype=torch.long).pin_memory()
+        with torch.device(dev):
+            self.model.setup_caches(num_pages=self.num_pages, page_size=PAGE_SIZE)
+        self.layer_roles = list(self.model.layer_roles)
+        ops.set_active_backend(self)
+        self._decode_graph = None
+
+    # ----------------------------------------------------------- op bodies
+    def rope_params(self) -> dict:
+        c = self.model.config
+        p = dict(rope_scale=float(c.scaling_factor), rope_theta=float(c.rope_base))
+        if c.high_freq_factor is not None and c.low_freq_factor is not None:
+            p.update(low_freq_factor=float(c.low_freq_factor), high_freq_factor=float(c.high_freq_factor),
+                     old_context_len=float(c.original_max_position_embeddings))
+        return p
+
+    def _decode_mode(self) -> bool:
+        return self._step is not None and self._step.mode == "decode"
+
+    def attn_full(self, q, kv_cache):
+        st = self._step
+        return K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
+                              max_pages_per_row=st.max_pages, workspace=self.workspace)
+
+    def attn_subset(self, q, kv_cache):
+        if not (self.enable_selective_cache and self._decode_mode()):
+            return self.attn_full(q, kv_cache)
+        sel = self.page_selector
+        return K.paged_decode(q, kv_cache, sel.paged_subset_kv_indptr, sel.paged_subset_kv_indices,
+                              self._step.kv_last, max_pages_per_row=self.k_eff, workspace=self.workspace,
+                              subset=True)
+
+    def attn_plan(self, q, kv_cache):
+        """Planner layer: full attention + logits dump, page scores, v2 selection into the subset CSR."""
+        if not (self.enable_selective_cache and self._decode_mode()):
+            return self.attn_full(q, kv_cache)
+        st = self._step
+        sel = self.page_selector
+        B = q.shape[0]
+        o = K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
+                           max_pages_per_row=st.max_pages, lse=self.lse, logits_dump=self.dump,
+                           workspace=self.workspace)
+        K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
+                                  scores=self.page_scores, batch=B, workspace=self.workspace)
+        K.select_pages(self.page_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,
+                       pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
+                       use_subset=self.use_subset_flag, out_indices=sel.paged_subset_kv_indices,
+                       out_indptr=sel.paged_subset_kv_indptr)
+        if self.enable_delta_debug_page_selection_parity and not torch.cuda.is_current_stream_capturing():
+            self._debug_check_selection(st, B)
+        return o
+
+    def _debug_check_selection(self, st, B):
+        """Selection from the two-pass (dump-only) scores must equal the planner's (backend.py:812-819)."""
+        ref_scores = K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot,
+                                               batch=B)
+        sel = self.page_selector
+        ri, rp = K.select_pages(ref_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,
+                                pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
+                                use_subset=self.use_subset_flag,
+                                out_indices=torch.empty_like(sel.paged_subset_kv_indices))
+        n = int(rp[B])
+        if not torch.equal(rp[:B + 1], sel.paged_subset_kv_indptr[:B + 1]) or \
+                not torch.equal(ri[:n], sel.paged_subset_kv_indices[:n]):
+            raise RuntimeError("DELTA page selection mismatch against torch-score reference path")
+
+    # ------------------------------------------------------------ decode step
+    def _decode_csr(self) -> _StepCSR:
+        sel = self.page_selector
+        return _StepCSR("decode", sel.paged_kv_indptr, sel.paged_kv_indices, sel.paged_kv_last_page_len,
+                        self.pages_per_slot)
+
+    def _decode_body(self, advance: bool):
+        """One decode step for all slots; only device work (capturable)."""
+        B = self.batch_size
+        sel = self.page_selector
+        K.decode_page_info(self.cachelens, self.slot_block_table, B, self.k_eff, self.compression_ratio,
+                           self.enable_selective_cache, sel.paged_kv_indptr, sel.paged_kv_indices,
+                           sel.paged_kv_last_page_len, row_block_table=sel._block_table,
+                           subset_indices=sel.paged_subset_kv_indices, subset_indptr=sel.paged_subset_kv_indptr,
+                           use_subset=self.use_subset_flag)
+        self._step = self._decode_csr()
+        try:
+            tokens = self.model(self.static_tokens, self.cachelens, self.qo_indptr, sel.paged_kv_indices,
+                                sel.paged_kv_indptr, sel.paged_kv_last_page_len)
+        finally:
+            self._step = None
+        self.static_tokens.copy_(tokens)
+        if advance:
+            self.cachelens.add_(self.active)
+        return tokens
+
+    def _capture_decode_graph(self):
+        stream = torch.cuda.Stream(device=self.device)
+        saved_tokens = self.static_tokens.clone()
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(stream):
+            for _ in range(2):  # warm-up (workspaces, BLAS handles); no cachelens advance
+                self._decode_body(advance=False)
+                self.static_tokens.copy_(saved_tokens)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._decode_body(advance=True)
+        self._decode_graph = graph
+        self._decode_graph_stats["captures"] += 1
+
+    @torch.inference_mode()
+    def decode_steps(self, n: int = 1, use_graph: Optional[bool] = None):
+        """Run ``n`` decode steps for every slot, feeding tokens back on the device."""
+        use_graph = self.enable_cuda_graph_decode if use_graph is None else use_graph
+        if use_graph and self._decode_graph is None and self._decode_graph_failed is None:
+            try:
+                self._capture_decode_graph()
+            except Exception as exc:  # capture failure -> eager fallback (backend.py:1138-1150)
+                self._decode_graph_failed = repr(exc)
+                self._decode_graph_stats["capture_failures"] += 1
+                self._decode_graph_fallback_reasons["capture_failed"] += 1
+                if self.is_main_process:
+                    print(f"[hip graph decode] capture failed, running eagerly: {exc}")
+        for _ in range(n):
+            if use_graph and self._decode_graph is not None:
+                self._decode_graph.replay()
+                self._decode_graph_stats["replays"] += 1
+            else:
+                self._decode_body(advance=True)
+        return self.static_tokens
+
+    # --------------------------------------------------- synthetic contexts
+    @torch.inference_mode()
+    def prepare_synthetic_decode(self, kv_len, decode_budget: int = 256, seed: int = 0,
+                                 fill_std: float = 1.0):
+        """Put every slot in the state "``kv_len`` tokens cached, decoding" (``kv_len`` an int
+        or one length per slot): pages for ``kv_len + decode_budget`` tokens from the page
+        pool, seeded N(0, fill_std) K/V in every layer, random current tokens.  Used by the
+        benchmark and tests (no prompts, no prefill)."""
+        B = self.batch_size
+        lens = [int(kv_len)] * B if isinstance(kv_len, int) else [int(x) for x in kv_len]
+        if len(lens) != B:
+            raise ValueError(f"need {B} context lengths, got {len(lens)}")
+        bt = self.slot_block_table.cpu()
+        for b, n in enumerate(lens):
+            need = (n + decode_budget) // PAGE_SIZE + 1
+            if need > self.pages_per_slot:
+                raise ValueError(f"{n} + {decode_budget} tokens need {need} pages > {self.pages_per_slot}")
+            bt[b, :need] = torch.tensor(self.page_manager.alloc(need), dtype=torch.int32)
+        self.slot_block_table.copy_(bt)
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        for layer in self.model.layers:
+            cache = layer.attention.kv_cache.kv_cache
+            cache.normal_(0.0, fill_std, generator=gen)
+        self.cachelens.copy_(torch.tensor(lens, dtype=torch.int32))
+        self.active.fill_(1)
+        vocab = self.model.config.vocab_size
+        self.static_tokens.copy_(torch.randint(0, vocab, (1, B), generator=gen, device=self.device))
+        self._decode_graph = None
+
+    # ------------------------------------------------------ request serving
+    def add_requests(self, input_ids_list: list, max_lengths: list, eot_token_ids: list):
+        if self.scheduler is None:
+            raise RuntimeError("Backend not initialized. Call setup_caches first.")
+        self.scheduler.add_requests(input_ids_list, max_lengths, eot_token_ids)
+
+    @torch.inference_mode()
+    def _sync_slot_block_table(self, slot_id: int, request: Request, old_page_count: int):
+        new = len(request.page_indices)
+        if new > old_page_count:
+            self.slot_block_table[slot_id, old_page_count:new].copy_(
+                torch.tensor(request.page_indices[old_page_count:new], dtype=torch.int32))
+
+    @torch.inference_mode()
+    def _release_slot(self, slot_id: int):
+        self.cachelens[slot_id].fill_(0)
+        self.active[slot_id].fill_(0)
+        self.slot_block_table[slot_id].fill_(int(self.scratch_pages[slot_id]))
+
+    @torch.inference_mode()
+    def run_scheduler_loop(self):
+        """Serve queued requests until done (backend.py:1486-1553)."""
+        torch.cuda.synchronize(self.device)
+        self.scheduler.stats["start_time"] = time.perf_counter()
+        self._step_records = []
+        i = 0
+        while True:
+            i += 1
+            finished = self.scheduler.check_finished_requests()
+            if finished and self.throughput_mode:
+                if self.is_main_process:
+                    print(f"\n[throughput_mode] {len(finished)} request(s) finished -- stopping all")
+                self._force_finish_all_requests()
+                break
+            for slot_id in finished:
+                self._release_slot(slot_id)
+            new_slots, new_reqs = self.scheduler.schedule_requests()
+            for slot_id, req in zip(new_slots, new_reqs):
+                req.initialize_pages(slot_id, self.pages_per_slot)
+                self.slot_block_table[slot_id].fill_(int(self.scratch_pages[slot_id]))
+                self._sync_slot_block_table(slot_id, req, 0)
+            if not self.scheduler.has_active_requests():
+                break
+            self._forward(i)
+        if self.is_main_process:
+            self._print_final_stats()
+        return self.get_detailed_results()
+
+    def _force_finish_all_requests(self):
+        for slot_id in range(self.batch_size):
+            rid = int(self.scheduler.runner_slots[slot_id])
+            if rid != -1:
+                req = self.scheduler.request_queue[rid]
+                if not req.is_finished():
+                    req.status = "finished"
+                self.scheduler.runner_slots[slot_id] = -1
+                self._release_slot(slot_id)
+
+    def _active_slots(self) -> List[int]:
+        return [s for s in range(self.batch_size) if int(self.scheduler.runner_slots[s]) != -1]
+
+    def _record_event(self):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
+    def _forward(self, step_index: int):
+        slots = self._active_slots()
+        if not slots:
+            return
+        reqs = [self.scheduler.request_queue[int(self.scheduler.runner_slots[s])] for s in slots]
+        ev0 = self._record_event()
+        decode_only = all(len(r.output_ids) > 0 for r in reqs)
+        if decode_only:
+            self._using_subset_cache_this_step = self.enable_selective_cache
+            for s, r in zip(slots, reqs):
+                old = len(r.page_indices)
+                r.plan(1, PAGE_SIZE)
+                self._sync_slot_block_table(s, r, old)
+                self._pinned_tokens[s] = r.output_ids[-1]
+            mask = torch.zeros(self.batch_size, dtype=torch.int32)
+            mask[slots] = 1
+            self.active.copy_(mask)
+            self.static_tokens[0].copy_(self._pinned_tokens, non_blocking=True)
+            ev1 = self._record_event()
+            tokens = self.decode_steps(1)
+            ev2 = self._record_event()
+            nxt = tokens[0].cpu().tolist()
+            next_tokens = [nxt[s] for s in slots]
+            qo_lengths = [1] * len(slots)
+        else:
+            self._using_subset_cache_this_step = False
+            ev1 = self._record_event()
+            next_tokens, qo_lengths = self._prefill_forward(slots, reqs)
+            ev2 = self._record_event()
+        for r, t in zip(reqs, next_tokens):
+            r.append_output(int(t))
+        self.scheduler.stats["total_tokens_generated"] += sum(qo_lengths)
+        ev3 = self._record_event()
+        self._pending_events.append((step_index, ev0, ev1, ev2, ev3, len(slots)))
+
+    @torch.inference_mode()
+    def _prefill_forward(self, slots, reqs):
+        """Eager step for rows with several query tokens: each query token is a virtual
+        decode row over its causal prefix (same attention kernel)."""
+        dev = self.device
+        toks, qo_lens, rows_pages, rows_last, offsets = [], [], [], [], []
+        for s, r in zip(slots, reqs):
+            q_tokens = r.get_qo_tokens()
+            old = len(r.page_indices)
+            start = r.kv_len(PAGE_SIZE)
+            r.plan(len(q_tokens), PAGE_SIZE)
+            self._sync_slot_block_table(s, r, old)
+            toks.append(q_tokens.to(torch.long))
+            qo_lens.append(len(q_tokens))
+            rows_pages.append(list(r.page_indices))
+            rows_last.append(r.page_lastlen)
+            offsets.append(start)
+        # row CSR (KV append) and virtual rows (attention)
+        kv_indptr, kv_indices = [0], []
+        v_indptr, v_indices, v_last = [0], [], []
+        for pages, q_len, start in zip(rows_pages, qo_lens, offsets):
+            kv_indices.extend(pages)
+            kv_indptr.append(len(kv_indices))
+            for i in range(q_len):
+                pos = start + i
+                n = pos // PAGE_SIZE + 1
+                v_indices.extend(pages[:n])
+                v_indptr.append(len(v_indices))
+                v_last.append(pos % PAGE_SIZE + 1)
+        i32 = dict(dtype=torch.int32, device=dev)
+        tokens = torch.cat(toks).view(1, -1).to(dev)
+        qo_indptr = torch.tensor([0] + list(torch.cumsum(torch.tensor(qo_lens), 0).tolist()), **i32)
+        self._step = _StepCSR("prefill", torch.tensor(v_indptr, **i32), torch.tensor(v_indices, **i32),
+                              torch.tensor(v_last, **i32), max(v_indptr[i + 1] - v_indptr[i] for i in range(len(v_last))))
+        try:
+            out = self.model(tokens, torch.tensor(offsets, **i32), qo_indptr, torch.tensor(kv_indices, **i32),
+                             torch.tensor(kv_indptr, **i32), torch.tensor(rows_last, **i32))
+        finally:
+            self._step = None
+        for s, q_len, start in zip(slots, qo_lens, offsets):
+            self.cachelens[s].fill_(start + q_len)
+            self.active[s].fill_(1)
+        last_pos = (qo_indptr[1:] - 1).long()
+        next_tokens = out[0].index_select(0, last_pos).cpu().tolist()
+        return next_tokens, qo_lens
+
+    # ------------------------------------------------------------- reporting
+    def _print_final_stats(self):
+        torch.cuda.synchronize(self.device)
+        total_time = time.perf_counter() - self.scheduler.stats["start_time"]
+        total_tokens = self.scheduler.stats["total_tokens_generated"]
+        for step, e0, e1, e2, e3, bsz in self._pending_events:
+            self._step_records.append({"step": step, "collect_pages_ms": e0.elapsed_time(e1),
+                                       "model_forward_ms": e1.elapsed_time(e2),
+                                       "postprocess_ms": e2.elapsed_time(e3), "step_total_ms": e0.elapsed_time(e3),
+                                       "active_bsz": bsz})
+        self._pending_events.clear()
+        print(f"\n{'=' * 60}\nSCHEDULER PERFORMANCE SUMMARY\n{'=' * 60}")
+        print(f"Total time: {total_time:.2f}s")
+        print(f"Total requests: {len(self.scheduler.request_queue)}")
+        print(f"Total tokens: {total_tokens:,}")
+        print(f"Tokens per second: {total_tokens / max(total_time, 1e-9):.2f}")
+        if self.enable_cuda_graph_decode:
+            print(f"HIP graph decode: {dict(self._decode_graph_stats)}"
+                  + (f" (capture failed: {self._decode_graph_failed})" if self._decode_graph_failed else ""))
+        if self._step_records:
+            n = len(self._step_records)
+            for key in ("collect_pages_ms", "model_forward_ms", "postprocess_ms", "step_total_ms"):
+                avg = sum(r[key] for r in self._step_records) / n
+                print(f"  {key[:-3]:<20s} avg {avg:8.3f} ms  ({n} steps)")
+            log_dir = os.environ.get("DELTA_STEP_LOG_DIR")
+            if log_dir:
+                path = Path(log_dir) / f"step_timings_{time.strftime('%Y%m%d_%H%M%S')}.json"
+                path.parent.mkdir(parents=True, exist_ok=True)
+                meta = {"total_time_s": total_time, "total_tokens": total_tokens,
+                        "tokens_per_second": total_tokens / max(total_time, 1e-9), "batch_size": self.batch_size,
+                        "max_length": self.max_length, "page_size": PAGE_SIZE,
+                        "selective_cache": self.enable_selective_cache, "num_steps": n,
+                        "cuda_graph_decode": self.enable_cuda_graph_decode,
+                        "cuda_graph_decode_stats": dict(self._decode_graph_stats)}
+                path.write_text(json.dumps({"meta": meta, "steps": self._step_records}, indent=2))
+                print(f"  Step timings saved to: {path}")
+        print("=" * 60)
+
+    def get_detailed_results(self):
+        if self.scheduler is None:
+            return []
+        return self.scheduler.get_detailed_results(self.tokenizer)

@@ -98,16 +98,18 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
 
   int np, lp;
   row_pages(a, b, &np, &lp);
-  const int sc = np < a.k ? np : a.k;
+  // use_subset gate (backend.py:2104-2109); when it is off the subset CSR is the full CSR.
+  const bool gate = a.selective && sub_tot > 0 && ((double)full_tot / (double)sub_tot) > a.compression_ratio;
+  const int sc = gate ? (np < a.k ? np : a.k) : np;
+  const long long sb = gate ? sub_before : full_before;
   if (tid == 0) {
     a.kv_indptr[b + 1] = (int32_t)(full_before + np);
     a.last_page_len[b] = lp;
-    if (a.subset_indptr) a.subset_indptr[b + 1] = (int32_t)(sub_before + sc);
+    if (a.subset_indptr) a.subset_indptr[b + 1] = (int32_t)(sb + sc);
     if (b == 0) {
       a.kv_indptr[0] = 0;
       if (a.subset_indptr) a.subset_indptr[0] = 0;
-      if (a.use_subset)
-        a.use_subset[0] = (a.selective && sub_tot > 0 && ((double)full_tot / (double)sub_tot) > a.compression_ratio) ? 1 : 0;
+      if (a.use_subset) a.use_subset[0] = gate ? 1 : 0;
     }
   }
   const int32_t *src = a.slot_bt + (int64_t)b * a.pages_per_slot;
@@ -117,7 +119,7 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
       const int32_t v = src[c];
       a.kv_indices[full_before + c] = v;
       if (a.row_bt) a.row_bt[(int64_t)b * a.pages_per_slot + c] = v;
-      if (a.subset_indices && c >= sub_start) a.subset_indices[sub_before + c - sub_start] = v;
+      if (a.subset_indices && c >= sub_start) a.subset_indices[sb + c - sub_start] = v;
     } else if (a.row_bt) {
       a.row_bt[(int64_t)b * a.pages_per_slot + c] = 0;  // no stale ids past the row (backend.py:2080-2086)
     }

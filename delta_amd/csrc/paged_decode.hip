@@ -74,9 +74,8 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs &a, int b) {
 }
 
 template <int DT, int G, bool WITH_V, bool WITH_DUMP>
-__global__ void __launch_bounds__(kThreads) decode_split_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
   using E = Elem<DT>;
-  extern __shared__ float smem[];
 
   const int split = blockIdx.x;
   const int h = blockIdx.y;
@@ -292,6 +291,31 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(DecodeArgs a) {
   }
 }
 
+// Named entry kernels, one per reference op, so profiles separate them:
+//   full  = target_decode (full CSR), subset = target_subset_decode (selected
+//   pages), plan = target_decode_plan (full CSR + logits dump),
+//   score = the standalone K-only scorer.
+template <int DT, int G>
+__global__ void __launch_bounds__(kThreads) paged_decode_full_kernel(DecodeArgs a) {
+  extern __shared__ float smem[];
+  decode_split_body<DT, G, true, false>(a, smem);
+}
+template <int DT, int G>
+__global__ void __launch_bounds__(kThreads) paged_decode_subset_kernel(DecodeArgs a) {
+  extern __shared__ float smem[];
+  decode_split_body<DT, G, true, false>(a, smem);
+}
+template <int DT, int G>
+__global__ void __launch_bounds__(kThreads) paged_decode_plan_kernel(DecodeArgs a) {
+  extern __shared__ float smem[];
+  decode_split_body<DT, G, true, true>(a, smem);
+}
+template <int DT, int G>
+__global__ void __launch_bounds__(kThreads) page_score_kv_kernel(DecodeArgs a) {
+  extern __shared__ float smem[];
+  decode_split_body<DT, G, false, true>(a, smem);
+}
+
 // Combines the split partials of one (row, q head): o = sum A_s 2^(m_s-M) / sum l_s 2^(m_s-M).
 template <int DT>
 __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
@@ -338,7 +362,7 @@ __global__ void decode_merge_lse_kernel(DecodeArgs a, int G) {
   a.lse[idx] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
 }
 
-enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2 };
+enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
 
 template <int DT, int G>
 void launch_split(const DecodeArgs &a, int mode, hipStream_t stream) {
@@ -347,13 +371,16 @@ void launch_split(const DecodeArgs &a, int mode, hipStream_t stream) {
   const size_t sm_score = (size_t)kWaves * G * 2 * sizeof(float);
   switch (mode) {
     case kAttn:
-      hipLaunchKernelGGL((decode_split_kernel<DT, G, true, false>), grid, dim3(kThreads), sm_attn, stream, a);
+      hipLaunchKernelGGL((paged_decode_full_kernel<DT, G>), grid, dim3(kThreads), sm_attn, stream, a);
+      break;
+    case kAttnSubset:
+      hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G>), grid, dim3(kThreads), sm_attn, stream, a);
       break;
     case kAttnDump:
-      hipLaunchKernelGGL((decode_split_kernel<DT, G, true, true>), grid, dim3(kThreads), sm_attn, stream, a);
+      hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G>), grid, dim3(kThreads), sm_attn, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((decode_split_kernel<DT, G, false, true>), grid, dim3(kThreads), sm_score, stream, a);
+      hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, dim3(kThreads), sm_score, stream, a);
       break;
   }
 }
@@ -412,7 +439,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   if (!q || !kv_cache || !kv_indptr || !kv_indices || !kv_last_page_len)
     return set_error(DELTA_ERR_INVALID, "%s: null input pointer", who);
   if (mode != kScoreOnly && !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
-  if (mode != kAttn && !dump) return set_error(DELTA_ERR_INVALID, "%s: null logits dump", who);
+  if ((mode == kAttnDump || mode == kScoreOnly) && !dump)
+    return set_error(DELTA_ERR_INVALID, "%s: null logits dump", who);
   if (((uintptr_t)q | (uintptr_t)kv_cache) & 15u)
     return set_error(DELTA_ERR_INVALID, "%s: q and kv_cache must be 16-byte aligned", who);
   if ((q_stride_h % 8) || (q_stride_b % 8))
@@ -507,4 +535,18 @@ extern "C" DELTA_EXPORT int delta_paged_decode(const void *q, int64_t q_stride_b
                            dump_stride_h, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
                            max_pages_per_row, mode, workspace, workspace_bytes, (hipStream_t)stream,
                            "delta_paged_decode");
+}
+
+extern "C" DELTA_EXPORT int delta_paged_decode_subset(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                                      const void *kv_cache, int64_t num_pages,
+                                                      const int32_t *kv_indptr, const int32_t *kv_indices,
+                                                      int64_t kv_indices_len, const int32_t *kv_last_page_len, void *o,
+                                                      int64_t o_stride_b, int64_t o_stride_h, float *lse, int batch,
+                                                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                                                      float sm_scale, int max_pages_per_row, void *workspace,
+                                                      size_t workspace_bytes, delta_stream_t stream) {
+  return delta::run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                           kv_last_page_len, o, o_stride_b, o_stride_h, lse, nullptr, 0, 0, batch, num_qo_heads,
+                           num_kv_heads, head_dim, dtype, sm_scale, max_pages_per_row, delta::kAttnSubset, workspace,
+                           workspace_bytes, (hipStream_t)stream, "delta_paged_decode_subset");
 }

@@ -110,12 +110,16 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tenso
                  max_pages_per_row: int, sm_scale: Optional[float] = None,
                  out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                  logits_dump: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 workspace: Optional[torch.Tensor] = None, subset: bool = False) -> torch.Tensor:
     """Paged decode attention (``delta_paged_decode``); returns ``out`` [B, Hq, 128].
 
     ``logits_dump`` (fp32, [B_max, Hq, S] or any view with unit last stride)
-    receives the planner-layer logits for ``t < kv_len``.
+    receives the planner-layer logits for ``t < kv_len``.  ``subset=True``
+    runs the same attention through ``delta_paged_decode_subset`` (selected
+    pages; no dump).
     """
+    if subset and logits_dump is not None:
+        raise ValueError("the subset attention writes no logits dump")
     dev = _check_cuda(q, kv_cache, kv_indptr, kv_indices, kv_last_page_len, out, lse, logits_dump)
     _check_cache(kv_cache)
     hq, hkv = _check_heads(q, kv_cache)
@@ -146,15 +150,15 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tenso
         workspace = _default_ws.get(need, dev)
     elif workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace too small: {need} bytes needed")
-    _lib.call("delta_paged_decode",
-              q.data_ptr(), q.stride(0), q.stride(1),
-              kv_cache.data_ptr(), kv_cache.shape[0],
-              kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_indices.numel(),
-              kv_last_page_len.data_ptr(),
-              out.data_ptr(), out.stride(0), out.stride(1), _ptr(lse),
-              _ptr(logits_dump), dsb, dsh,
-              B, hq, hkv, HEAD_DIM, _dtype_code(q), float(sm_scale), int(max_pages_per_row),
-              workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
+    common_head = (q.data_ptr(), q.stride(0), q.stride(1), kv_cache.data_ptr(), kv_cache.shape[0],
+                   kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_indices.numel(), kv_last_page_len.data_ptr(),
+                   out.data_ptr(), out.stride(0), out.stride(1), _ptr(lse))
+    common_tail = (B, hq, hkv, HEAD_DIM, _dtype_code(q), float(sm_scale), int(max_pages_per_row),
+                   workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
+    if subset:
+        _lib.call("delta_paged_decode_subset", *common_head, *common_tail)
+    else:
+        _lib.call("delta_paged_decode", *common_head, _ptr(logits_dump), dsb, dsh, *common_tail)
     return out
 
 
@@ -326,7 +330,7 @@ def decode_page_info(cachelens: torch.Tensor, slot_block_table: torch.Tensor, ba
         if row_block_table.shape[-1] != pps:
             raise ValueError("row_block_table must have pages_per_slot columns")
     if subset_indices is not None:
-        _check_i32("subset_indices", subset_indices, batch * min(k, pps))
+        _check_i32("subset_indices", subset_indices, batch * pps)
         _check_i32("subset_indptr", subset_indptr, batch + 1)
     if use_subset is not None:
         _check_i32("use_subset", use_subset, 1)
@@ -394,3 +398,18 @@ def rope(q: torch.Tensor, k: torch.Tensor, indptr: torch.Tensor, offsets: torch.
               float(low_freq_factor or 0.0), float(high_freq_factor or 0.0),
               float(old_context_len or 0.0), _stream(dev))
     return q_out, k_out
+
+
+def argmax_rows(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """First index of each row's maximum (``delta_argmax_rows``); logits [rows, cols]."""
+    dev = _check_cuda(logits, out)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [rows, cols] with unit inner stride")
+    rows, cols = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=dev)
+    if out.dtype != torch.int64 or out.dim() != 1 or out.shape[0] < rows:
+        raise ValueError("out must be int64 [>=rows]")
+    _lib.call("delta_argmax_rows", logits.data_ptr(), logits.stride(0), int(rows), int(cols),
+              _dtype_code(logits), out.data_ptr(), out.stride(0), _stream(dev))
+    return out

@@ -1,0 +1,276 @@
+"""gpt-fast style decoder whose attention runs through the ``mylib::*`` ops on gfx950.
+
+Mirrors DELTA/Engine/DELTA/model.py: ``ModelArgs`` and the model-shape table
+(20-97), the paged ``KVCache`` buffer ``[pages, 2, 16, Hkv, d]`` (99-127), the
+per-layer binding of ``attn_decode`` to ``target_decode`` /
+``target_decode_plan`` (last full layer before a non-full one) /
+``target_subset_decode`` (146-196), and the block structure (330-532).  The
+dense parts (GEMMs, RMSNorm, SiLU) stay torch ops (hipBLASLt on ROCm); the
+final argmax is the HIP ``delta_argmax_rows`` kernel so a captured decode step
+records no torch multi-block reduction.
+
+No checkpoints ship with this build: ``init_random_weights`` gives every
+parameter seeded N(0, std) values of the named architecture.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+from torch.nn import functional as F
+
+from . import kernels as K
+from . import ops  # noqa: F401  (registers the mylib:: ops)
+
+
+def find_multiple(n: int, k: int) -> int:
+    return n if n % k == 0 else n + k - (n % k)
+
+
+@dataclass
+class ModelArgs:
+    block_size: int = 2048
+    vocab_size: int = 32000
+    n_layer: int = 32
+    n_head: int = 32
+    dim: int = 4096
+    intermediate_size: Optional[int] = None
+    n_local_heads: int = -1
+    head_dim: int = 64
+    rope_base: float = 10000
+    norm_eps: float = 1e-5
+    scaling_factor: float = 1.0
+    low_freq_factor: Optional[int] = None
+    high_freq_factor: Optional[int] = None
+    original_max_position_embeddings: Optional[int] = None
+    qkv_bias: bool = False
+    full_cache_layers: Optional[List[int]] = None
+    subset_cache_ratio: float = 0.5
+    subset_cache_size: int = 0
+    L: int = 8
+
+    def __post_init__(self):
+        if self.n_local_heads == -1:
+            self.n_local_heads = self.n_head
+        if self.intermediate_size is None:
+            self.intermediate_size = find_multiple(int(2 * (4 * self.dim) / 3), 256)
+        self.head_dim = self.dim // self.n_head
+        if self.full_cache_layers is None:
+            self.full_cache_layers = []
+
+    @classmethod
+    def from_name(cls, name: str):
+        if name in transformer_configs:
+            return cls(**transformer_configs[name])
+        hits = [c for c in transformer_configs if c.lower() in str(name).lower()]
+        if not hits:
+            raise ValueError(f"unknown model shape {name!r}")
+        hits.sort(key=len, reverse=True)
+        return cls(**transformer_configs[hits[0]])
+
+
+# Architecture shapes used by the benchmarks and the reference's recipes (model.py:72-97).
+transformer_configs = {
+    "llama-3-8b": dict(block_size=8192, n_layer=32, n_head=32, n_local_heads=8, dim=4096,
+                       intermediate_size=14336, vocab_size=128256, rope_base=500000),
+    "llama-3.1-8b": dict(block_size=131072, n_layer=32, n_head=32, n_local_heads=8, dim=4096,
+                         intermediate_size=14336, vocab_size=128256, rope_base=500000.0, scaling_factor=8,
+                         high_freq_factor=4, low_freq_factor=1, original_max_position_embeddings=8192),
+    "Qwen2.5-7b": dict(block_size=131072, n_layer=28, n_head=28, n_local_heads=4, dim=3584,
+                       intermediate_size=18944, vocab_size=152064, rope_base=1000000.0, qkv_bias=True,
+                       norm_eps=1e-6),
+    "Qwen2.5-14b": dict(block_size=131072, n_layer=48, n_head=40, n_local_heads=8, dim=5120,
+                        intermediate_size=13824, vocab_size=152064, rope_base=1000000.0, qkv_bias=True,
+                        norm_eps=1e-6),
+    "DeepSeek-R1-Distill-Qwen-1.5B": dict(block_size=131072, n_layer=28, n_head=12, n_local_heads=2, dim=1536,
+                                          intermediate_size=8960, vocab_size=151936, rope_base=10000.0,
+                                          qkv_bias=True, norm_eps=1e-6),
+    "DeepSeek-R1-Distill-Qwen-7B": dict(block_size=131072, n_layer=28, n_head=28, n_local_heads=4, dim=3584,
+                                        intermediate_size=18944, vocab_size=152064, rope_base=10000.0,
+                                        qkv_bias=True, norm_eps=1e-6),
+    "DeepSeek-R1-Distill-Llama-8B": dict(block_size=131072, n_layer=32, n_head=32, n_local_heads=8, dim=4096,
+                                         intermediate_size=14336, vocab_size=128256, rope_base=500000.0,
+                                         scaling_factor=8, high_freq_factor=4, low_freq_factor=1,
+                                         original_max_position_embeddings=8192),
+    # small shape for tests: head_dim 128, GQA group 2
+    "tiny-test": dict(block_size=4096, n_layer=4, n_head=4, n_local_heads=2, dim=512, intermediate_size=1024,
+                      vocab_size=1000, rope_base=10000.0),
+}
+
+
+class KVCache(nn.Module):
+    """One layer's paged cache ``[num_pages, 2, page_size, n_heads, head_dim]``."""
+
+    def __init__(self, max_num_pages, page_size, n_heads, head_dim, dtype=torch.bfloat16):
+        super().__init__()
+        self.register_buffer("kv_cache", torch.zeros((max_num_pages, 2, page_size, n_heads, head_dim),
+                                                     dtype=dtype), persistent=False)
+
+    def update_target(self, k, v, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen):
+        torch.ops.mylib.update_kv(k, v, kv_append_indptr, self.kv_cache, kv_page_indices, kv_page_indptr,
+                                  kv_page_lastlen)
+        return self.kv_cache
+
+
+class Transformer(nn.Module):
+    def __init__(self, config: ModelArgs) -> None:
+        super().__init__()
+        self.config = config
+        self.tok_embeddings = nn.Embedding(config.vocab_size, config.dim)
+        self.layers = nn.ModuleList(TransformerBlock(config) for _ in range(config.n_layer))
+        self.norm = RMSNorm(config.dim, eps=config.norm_eps)
+        self.output = nn.Linear(config.dim, config.vocab_size, bias=False)
+        self.layer_roles: List[str] = []
+        self._argmax_out: Optional[Tensor] = None
+
+    def setup_caches(self, num_pages: int, page_size: int):
+        """Allocate per-layer caches and bind each layer's attention op (model.py:146-196)."""
+        cfg = self.config
+        head_dim = cfg.dim // cfg.n_head
+        dtype = self.output.weight.dtype if self.output.weight.dtype == torch.float16 else torch.bfloat16
+        full = set(cfg.full_cache_layers or [])
+        self.layer_roles = []
+        for i, b in enumerate(self.layers):
+            if full:
+                use_full = i in full
+                next_full = (i + 1) in full if (i + 1) < cfg.n_layer else True
+            else:
+                use_full = next_full = True
+            b.attention.kv_cache = KVCache(num_pages, page_size, cfg.n_local_heads, head_dim, dtype)
+            if use_full:
+                if next_full:
+                    b.attention.attn_decode = torch.ops.mylib.target_decode
+                    self.layer_roles.append("full")
+                else:
+                    b.attention.attn_decode = torch.ops.mylib.target_decode_plan
+                    self.layer_roles.append("plan")
+            else:
+                b.attention.attn_decode = torch.ops.mylib.target_subset_decode
+                self.layer_roles.append("subset")
+            b.attention.rope = torch.ops.mylib.rope
+
+    def forward(self, idx: Tensor, input_pos: Tensor, kv_append_indptr: Tensor, kv_page_indices: Tensor,
+                kv_page_indptr: Tensor, kv_page_lastlen: Tensor) -> Tensor:
+        logits = self.forward_logits(idx, input_pos, kv_append_indptr, kv_page_indices, kv_page_indptr,
+                                     kv_page_lastlen)
+        return self._finalize_logits(logits)
+
+    def forward_logits(self, idx, input_pos, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen):
+        x = self.tok_embeddings(idx)
+        for layer in self.layers:
+            x = layer(x, input_pos, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen)
+        return self.output(self.norm(x))
+
+    def _finalize_logits(self, logits: Tensor) -> Tensor:
+        """argmax over the vocabulary on the HIP kernel; returns int64 [bsz, seqlen]."""
+        bsz, seqlen, vocab = logits.shape
+        flat = logits.reshape(bsz * seqlen, vocab)
+        out = torch.empty(bsz * seqlen, dtype=torch.int64, device=logits.device)
+        K.argmax_rows(flat, out)
+        return out.view(bsz, seqlen)
+
+    @classmethod
+    def from_name(cls, name: str):
+        return cls(ModelArgs.from_name(name))
+
+
+class TransformerBlock(nn.Module):
+    def __init__(self, config: ModelArgs) -> None:
+        super().__init__()
+        self.attention = Attention(config)
+        self.feed_forward = FeedForward(config)
+        self.ffn_norm = RMSNorm(config.dim, config.norm_eps)
+        self.attention_norm = RMSNorm(config.dim, config.norm_eps)
+
+    def forward(self, x, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen):
+        h = x + self.attention(self.attention_norm(x), offsets, kv_append_indptr, kv_page_indices,
+                               kv_page_indptr, kv_page_lastlen)
+        return h + self.feed_forward(self.ffn_norm(h))
+
+
+class Attention(nn.Module):
+    def __init__(self, config: ModelArgs):
+        super().__init__()
+        assert config.dim % config.n_head == 0
+        total_head_dim = (config.n_head + 2 * config.n_local_heads) * config.head_dim
+        self.wqkv = nn.Linear(config.dim, total_head_dim, bias=config.qkv_bias)
+        self.wo = nn.Linear(config.dim, config.dim, bias=False)
+        self.kv_cache: Optional[KVCache] = None
+        self.attn_decode = None
+        self.rope = None
+        self.n_head = config.n_head
+        self.head_dim = config.head_dim
+        self.n_local_heads = config.n_local_heads
+        self.dim = config.n_head * config.head_dim
+        # debug capture (tests): when a list, each call appends (q, o)
+        self.record: Optional[list] = None
+
+    def forward(self, x, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen):
+        bsz, seqlen, _ = x.shape
+        q_size = self.n_head * self.head_dim
+        kv_size = self.n_local_heads * self.head_dim
+        q, k, v = self.wqkv(x).split([q_size, kv_size, kv_size], dim=-1)
+        q = q.view(bsz * seqlen, self.n_head, self.head_dim)
+        k = k.view(bsz * seqlen, self.n_local_heads, self.head_dim)
+        v = v.view(bsz * seqlen, self.n_local_heads, self.head_dim)
+        q, k = self.rope(q, k, kv_append_indptr, offsets)
+        kv_cache = self.kv_cache.update_target(k, v, kv_append_indptr, kv_page_indices, kv_page_indptr,
+                                               kv_page_lastlen)
+        y = self.attn_decode(q, kv_cache)
+        if self.record is not None:
+            self.record.append((q.detach().clone(), y.detach().clone()))
+        y = y.contiguous().view(bsz, seqlen, self.dim)
+        return self.wo(y)
+
+
+class FeedForward(nn.Module):
+    def __init__(self, config: ModelArgs) -> None:
+        super().__init__()
+        self.w1 = nn.Linear(config.dim, config.intermediate_size, bias=False)
+        self.w3 = nn.Linear(config.dim, config.intermediate_size, bias=False)
+        self.w2 = nn.Linear(config.intermediate_size, config.dim, bias=False)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: Tensor) -> Tensor:
+        xf = x.float()
+        out = xf * torch.rsqrt(torch.mean(xf * xf, dim=-1, keepdim=True) + self.eps)
+        return out.type_as(x) * self.weight
+
+
+@torch.no_grad()
+def init_random_weights(model: Transformer, std: float = 0.02, seed: int = 0) -> Transformer:
+    """Seeded N(0, std) linear/embedding weights, zero biases, unit norms (random-init checkpoint)."""
+    gen = torch.Generator(device=next(model.parameters()).device)
+    gen.manual_seed(seed)
+    for name, p in model.named_parameters():
+        if name.endswith("norm.weight") or ".attention_norm." in name or ".ffn_norm." in name:
+            p.fill_(1.0)
+        elif name.endswith(".bias"):
+            p.zero_()
+        else:
+            p.normal_(0.0, std, generator=gen)
+    return model
+
+
+def build_random_model(name: str, device, dtype=torch.bfloat16, seed: int = 0, std: float = 0.02,
+                       **overrides) -> Transformer:
+    """Random-init model of the named shape, materialised directly on ``device``."""
+    cfg = ModelArgs.from_name(name)
+    for k, v in overrides.items():
+        setattr(cfg, k, v)
+    with torch.device("meta"):
+        model = Transformer(cfg)
+    model = model.to_empty(device=device).to(dtype)
+    return init_random_weights(model, std=std, seed=seed).eval()

@@ -101,6 +101,19 @@ int delta_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                        int dtype, float sm_scale, int max_pages_per_row,
                        void *workspace, size_t workspace_bytes, delta_stream_t stream);
 
+/* The same attention over a *selected* page subset (the subset CSR built by
+ * delta_select_pages, sharing kv_last_page_len with the full CSR):
+ * target_subset_decode (backend.py:486-512).  Separate entry point (and
+ * kernel name) so profiles tell the selective layers from the full ones. */
+int delta_paged_decode_subset(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                              const void *kv_cache, int64_t num_pages,
+                              const int32_t *kv_indptr, const int32_t *kv_indices,
+                              int64_t kv_indices_len, const int32_t *kv_last_page_len,
+                              void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                              int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+                              int dtype, float sm_scale, int max_pages_per_row,
+                              void *workspace, size_t workspace_bytes, delta_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Page scoring (del3_legacy_softmax)                                         */
 /* ------------------------------------------------------------------------ */
@@ -193,10 +206,13 @@ int delta_pack_page_indices(const int32_t *slot_block_table, int num_slots,
  * host work: for each row, kv_len = cachelens[b] + 1, pages = kv_len/16 + 1,
  * last = kv_len % 16.  Writes kv_indptr (cumsum), kv_indices (packed from
  * slot_block_table), kv_last_page_len, row_block_table [batch, pages_per_slot]
- * (optional), the default subset CSR of the last min(pages, k) pages
- * (subset_indices/subset_indptr, optional), and use_subset[0] =
- * (selective && subset_total > 0 && full_total / subset_total > compression_ratio)
- * (optional).  Rows whose page count would exceed pages_per_slot are clamped. */
+ * (optional), the subset CSR (subset_indices/subset_indptr, optional) and
+ * use_subset[0] = (selective && subset_total > 0 &&
+ * full_total / subset_total > compression_ratio) (optional).  The subset CSR
+ * holds each row's last min(pages, k) pages when the gate is on and the full
+ * CSR when it is off (the reference rebinds the subset lists to the full ones,
+ * backend.py:2111-2150), so subset_indices needs batch * pages_per_slot
+ * entries.  Rows whose page count would exceed pages_per_slot are clamped. */
 int delta_decode_page_info(const int32_t *cachelens, const int32_t *slot_block_table,
                            int batch, int pages_per_slot, int k, double compression_ratio,
                            int selective, int32_t *kv_indptr, int32_t *kv_indices,
@@ -231,6 +247,17 @@ int delta_rope(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
                int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
                float rope_scale, float rope_theta, int llama31, float low_freq_factor,
                float high_freq_factor, float old_context_len, delta_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Decode-step helper                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* out[r * out_stride] = first index of the maximum of logits[r, :cols]
+ * (bf16/fp16 rows with stride row_stride; NaN ranks highest), as torch.argmax
+ * in _finalize_logits (model.py:320-323).  Used inside the captured decode
+ * step in place of torch's multi-block reduction. */
+int delta_argmax_rows(const void *logits, int64_t row_stride, int rows, int cols, int dtype,
+                      int64_t *out, int64_t out_stride, delta_stream_t stream);
 
 #ifdef __cplusplus
 }

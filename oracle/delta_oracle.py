@@ -91,7 +91,8 @@ def gather_row_kv(kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
 
 def dump_logits(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
                 kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
-                sm_scale: float, max_len: int) -> torch.Tensor:
+                sm_scale: float, max_len: int,
+                compute_dtype: torch.dtype = torch.float64) -> torch.Tensor:
     """fp32 ``x[b, h, t] = (q[b,h] . K[b, t, h // G]) * sm_scale``; -inf past kv_len.
 
     Restates the ``BatchDumpAttentionWeights`` logits transform
@@ -99,7 +100,7 @@ def dump_logits(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor
     at ``b*H*S + h*S + t`` for ``t < kv_len``; the buffer is -inf filled
     (backend.py:384-389), so every other position reads -inf.  ``sm_scale`` is
     ``1/sqrt(head_dim)`` at the call site (backend.py:542).  The dot product is
-    taken in float64 and rounded once to fp32.
+    taken in ``compute_dtype`` (float64 by default) and rounded once to fp32.
     """
     B, Hq, d = q.shape
     Hkv = kv_cache.shape[3]
@@ -110,8 +111,8 @@ def dump_logits(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor
         n = k.shape[0]
         if n == 0:
             continue
-        kk = k.to(torch.float64).repeat_interleave(G, dim=1)          # [n, Hq, d]
-        s = torch.einsum("hd,nhd->hn", q[b].to(torch.float64), kk) * float(sm_scale)
+        kk = k.to(compute_dtype).repeat_interleave(G, dim=1)          # [n, Hq, d]
+        s = torch.einsum("hd,nhd->hn", q[b].to(compute_dtype), kk) * float(sm_scale)
         out[b, :, :n] = s.to(torch.float32)
     return out
 

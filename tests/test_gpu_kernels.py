@@ -46,6 +46,14 @@ def gpu(c):
     return c.to(DEV)
 
 
+def assert_ulp_close(a, b):
+    """Two kernel variants (with / without the logits dump) round the same math
+    differently in the last bit at most."""
+    ulp = torch.finfo(a.dtype).eps
+    a, b = a.float(), b.float()
+    assert ((a - b).abs() <= ulp * b.abs() + 1e-6).all()
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_decode_attention_and_dump(name):
     c = CASES[name]()
@@ -68,9 +76,11 @@ def test_decode_attention_and_dump(name):
     assert torch.all(d[~valid] == 12345.0), "dump wrote past kv_len"
     err = (d[valid] - x_ref[valid]).abs() / (1 + x_ref[valid].abs())
     assert err.max().item() < 1e-4
-    # without the dump the attention result is bit-identical
+    # the no-dump variant agrees to an ulp and each variant is deterministic
     o2 = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
-    assert torch.equal(o, o2)
+    o3 = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
+    assert torch.equal(o2, o3)
+    assert_ulp_close(o, o2)
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -179,7 +189,7 @@ def test_selective_step_end_to_end(name):
                             max_pages_per_row=mp, lse=lse, logits_dump=dump)
     s = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
     idx, ip = K.select_pages(s, g.kv_indptr, g.block_table, k, c.L)
-    o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=k)
+    o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=k, subset=True)
     torch.cuda.synchronize()
     ref = O.selective_step(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, k=k, L=c.L)
     assert_attn_close(o_full, ref["o_full"], name + "/full")
@@ -220,8 +230,10 @@ def test_sparse_equals_full_when_budget_covers_all():
     s = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
     idx, ip = K.select_pages(s, g.kv_indptr, g.block_table, mp, 8)
     assert torch.equal(ip, g.kv_indptr) and torch.equal(idx[:int(ip[-1])], g.kv_indices)
-    o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=mp)
-    assert torch.equal(o_sp, o_full)
+    o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=mp, subset=True)
+    o_nd = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
+    assert torch.equal(o_sp, o_nd)
+    assert_ulp_close(o_sp, o_full)
 
 
 def test_pack_page_indices():
@@ -250,7 +262,7 @@ def test_decode_page_info():
     ip = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
     last = torch.zeros(B, dtype=torch.int32, device=DEV)
     rbt = torch.full((B, pps), -7, dtype=torch.int32, device=DEV)
-    sub_i = torch.zeros(B * k, dtype=torch.int32, device=DEV)
+    sub_i = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
     sub_p = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
     flag = torch.full((1,), -1, dtype=torch.int32, device=DEV)
     K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, k, 1.0, True, ip, ind, last, rbt, sub_i, sub_p, flag)
@@ -272,7 +284,13 @@ def test_decode_page_info():
     assert sub_p.cpu().tolist() == sp
     for b in range(B):
         assert sub_i[sp[b]:sp[b + 1]].cpu().tolist() == slot_bt[b, int(ss[b]):int(pc[b])].tolist()
-    assert int(flag) == int(O.use_subset_decision(int(pc.sum()), int(sc.sum()), 1.0))
+    assert int(flag) == int(O.use_subset_decision(int(pc.sum()), int(sc.sum()), 1.0)) == 1
+    # gate off (ratio too high): the subset CSR is the full CSR
+    K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, k, 1e9, True, ip, ind, last, rbt, sub_i, sub_p, flag)
+    torch.cuda.synchronize()
+    assert int(flag) == 0
+    assert sub_p.cpu().tolist() == want_ip
+    assert torch.equal(sub_i[:want_ip[-1]], ind[:want_ip[-1]])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -322,7 +340,7 @@ def test_decode_is_deterministic_full_size():
     o1 = K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
                         max_pages_per_row=mp, lse=lse, logits_dump=dump)
     o2 = K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
-                        max_pages_per_row=mp)
+                        max_pages_per_row=mp, lse=lse, logits_dump=dump)
     s = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
     idx, ip = K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L)
     idx2, ip2 = K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L)

@@ -78,37 +78,48 @@ def time_steps(torch, eng, warmup: int, steps: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def kernel_roofline(torch, reps: int = 50):
-    """Time each hot-path kernel at the config-3 layer shape with HIP events on its stream."""
+def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
+    """Time each hot-path kernel at the config-3 layer shape with HIP events on its stream.
+
+    Launches rotate over ``n_rot`` independent layers (own KV cache, q and selection), as
+    the 30 selective layers of a step do, so no launch re-reads a working set left in the
+    256 MB MALL by the previous one."""
     from delta_amd import kernels as K
-    from delta_amd.workloads import config_case
-    c = config_case(3, device="cuda:0")
+    from delta_amd.workloads import make_case
+    layers = []
+    for seed in range(n_rot):
+        c = make_case(batch=BATCH, hq=32, hkv=8, kv_lens=CONTEXT, dtype=torch.bfloat16, seed=seed,
+                      page_order="shuffle", k=BUDGET_PAGES, L=L_LAST, device="cuda:0")
+        B, hq = c.q.shape[:2]
+        mp = c.max_pages
+        dump = torch.empty((B, hq, mp * 16), device="cuda:0")
+        lse = torch.empty((B, hq), device="cuda:0")
+        K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
+                       lse=lse, logits_dump=dump)
+        scores = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+        idx, ip = K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L)
+        layers.append((c, dump, lse, scores, idx, ip))
+    torch.cuda.synchronize()
+    c = layers[0][0]
     B, hq = c.q.shape[:2]
     hkv = c.kv_cache.shape[3]
     mp = c.max_pages
     esz = c.kv_cache.element_size()
-    dump = torch.empty((B, hq, mp * 16), device="cuda:0")
-    lse = torch.empty((B, hq), device="cuda:0")
-    K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
-                   lse=lse, logits_dump=dump)
-    scores = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
-    idx, ip = K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L)
-    torch.cuda.synchronize()
     last = c.kv_last_page_len.cpu()
     ntok_full = sum(c.kv_lens)
-    ntok_sub = sum((c.k - 1) * 16 + int(l) for l in last)
+    ntok_sub = sum((c.k - 1) * 16 + int(x) for x in last)
     qo = 2 * B * hq * 128 * esz
     row_kv = hkv * 128 * esz  # one token of K (or V) for all kv heads
 
     def timed(fn):
         stream = torch.cuda.current_stream()
-        for _ in range(3):
-            fn()
+        for i in range(n_rot):
+            fn(*layers[i])
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record(stream)
-        for _ in range(reps):
-            fn()
+        for i in range(reps):
+            fn(*layers[i % n_rot])
         e.record(stream)
         torch.cuda.synchronize()
         return s.elapsed_time(e) * 1e3 / reps  # us
@@ -120,32 +131,33 @@ def kernel_roofline(torch, reps: int = 50):
                      "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "what": note}
 
     add("paged_decode_subset_kernel",
-        timed(lambda: K.paged_decode(c.q, c.kv_cache, ip, idx, c.kv_last_page_len, max_pages_per_row=c.k,
-                                     subset=True)),
+        timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
+                                                       max_pages_per_row=c.k, subset=True)),
         ntok_sub * 2 * row_kv + qo + B * c.k * 4, "K+V of the 128 selected pages/row, q, o, page ids")
     add("paged_decode_full_kernel",
-        timed(lambda: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
-                                     max_pages_per_row=mp)),
+        timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                       c.kv_last_page_len, max_pages_per_row=mp)),
         ntok_full * 2 * row_kv + qo + B * mp * 4, "K+V of all 512 pages/row, q, o, page ids")
     add("paged_decode_plan_kernel",
-        timed(lambda: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
-                                     max_pages_per_row=mp, lse=lse, logits_dump=dump)),
+        timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                       c.kv_last_page_len, max_pages_per_row=mp, lse=l,
+                                                       logits_dump=d)),
         ntok_full * 2 * row_kv + qo + B * mp * 4 + ntok_full * hq * 4,
         "planner: full attention + fp32 logits dump")
     add("legacy_softmax_score_kernel",
-        timed(lambda: K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse,
-                                                scores=scores)),
+        timed(lambda c, d, l, s, i, p: K.page_scores_from_logits(d, c.kv_indptr, c.kv_last_page_len, mp, lse=l,
+                                                                  scores=s)),
         ntok_full * hq * 4 + B * mp * 4, "reads the logits dump once, writes page scores")
-    sc_dump = torch.empty_like(dump)
     add("page_score_kv (standalone scorer)",
-        timed(lambda: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, mp,
-                                   logits_dump=sc_dump, scores=scores)),
+        timed(lambda c, d, l, s, i, p: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                     c.kv_last_page_len, mp, logits_dump=d, scores=s)),
         ntok_full * row_kv + B * hq * 128 * esz + B * mp * 4 + B * mp * 4,
         "K read once + q + page table + scores (logit spill not counted)")
     add("select_pages_kernel",
-        timed(lambda: K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L, out_indices=idx, out_indptr=ip)),
+        timed(lambda c, d, l, s, i, p: K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L, out_indices=i,
+                                                       out_indptr=p)),
         B * mp * 4 * 2 + B * c.k * 4, "latency-bound selection (reported in us)")
-    del c, dump, sc_dump
+    del layers, c
     torch.cuda.empty_cache()
     return res
 
@@ -226,7 +238,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-full-compare", action="store_true")
-    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--kernel-reps", type=int, default=48)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}). "

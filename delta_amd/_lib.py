@@ -50,7 +50,11 @@ SIGNATURES = {
     "delta_append_kv": (c_int, [
         _P, c_int64, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int,
         c_int, c_int, _P]),
-    "delta_argmax_rows": (c_int, [_P, c_int64, c_int, c_int, c_int, _P, c_int64, _P]),
+    "delta_argmax_workspace_bytes": (c_size_t, [c_int]),
+    "delta_argmax_rows": (c_int, [_P, c_int64, c_int, c_int, c_int, _P, c_int64, _P, c_size_t, _P]),
+    "delta_add_rmsnorm": (c_int, [_P, c_int64, _P, c_int64, _P, c_float, _P, c_int64, _P, c_int64, c_int, c_int,
+                                  c_int, _P]),
+    "delta_silu_mul": (c_int, [_P, c_int64, _P, c_int64, c_int, c_int, c_int, _P]),
     "delta_rope": (c_int, [
         _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_float, c_int, c_float, c_float, c_float, _P]),

@@ -28,8 +28,7 @@ namespace delta {
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+constexpr int kMaxWaves = 16;  // waves per block (a block never exceeds one CU's 16 slots at <= 128 VGPRs)
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -46,6 +45,7 @@ struct DecodeArgs {
   float *dump;
   int64_t dump_stride_b, dump_stride_h;
   int dump_cap;     // tokens per dump row the caller guarantees (max_pages_per_row * 16)
+  int dump_vec;     // dump rows are 16-byte aligned: 4 tokens per store
   float *part_acc;  // [batch][hkv][nsplit][G][128]
   float *part_ml;   // [batch][hkv][nsplit][G][2]  (m in log2 units, l)
   int batch, hq, hkv, nsplit;
@@ -73,24 +73,76 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs &a, int b) {
   return r;
 }
 
+// LDS row of a staged V tile: 128 elements + 8 padding (272 B), so the 16 rows of a
+// transposed read start on distinct 4-bank offsets.
+constexpr int kVStride = 136;
+constexpr int kVTile = kPageSize * kVStride;  // elements per wave
+
+template <int DT>
+struct Mfma16;
+template <>
+struct Mfma16<DELTA_BF16> {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  __device__ __forceinline__ static f32x4 run(s4 a, s4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static short pack(float x) { return __builtin_bit_cast(short, (__bf16)x); }
+};
+template <>
+struct Mfma16<DELTA_FP16> {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  __device__ __forceinline__ static f32x4 run(s4 a, s4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static short pack(float x) { return __builtin_bit_cast(short, (_Float16)x); }
+};
+
+typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4_t lds_s4_t;
+
+// max / sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950 permlane swaps.
+__device__ __forceinline__ float rows4_max(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// One (row, kv head, split) per block, blockDim/64 waves taking the split's pages round robin.
+//   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows (lane%16 = token,
+//         lane/16 picks d in [32s + 8c, +8) at step s), B = the group's query rows (zero padded
+//         to 16 columns).  D puts tokens 4c..4c+3 of head g = lane%16 in lane (c, g).
+//   softmax: per lane 4 tokens of one head; row reductions are 3 in-lane ops + 2 permlane swaps.
+//   P.V : v_mfma_f32_16x16x16 -- A = P (already in A layout: row g = lane%16, k = tokens 4c..),
+//         B = V read back from a padded LDS tile with ds_read_b64_tr_b16 (lane (c, j) gets
+//         V[4c..4c+3][16n + j]), D = O[g = 4c + r][d = 16n + lane%16].
 template <int DT, int G, bool WITH_V, bool WITH_DUMP>
 __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
   using E = Elem<DT>;
+  using M16 = Mfma16<DT>;
 
+  const int nw = blockDim.x >> 6;
   const int split = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int c = lane >> 4;  // 16-lane row of the wave
-  const int t = lane & 15;  // lane within the row
+  const int c = lane >> 4;
+  const int t = lane & 15;
 
   const RowInfo ri = row_info(a, b);
   const int pps = (ri.np + a.nsplit - 1) / a.nsplit;
   const int j0 = split * pps;
   const int j1 = min(ri.np, j0 + pps);
 
-  // Query fragment (MFMA A operand): row g = t, d = 32s + 8c + [0, 8).
+  // Query fragment (B operand of q.K): column g = t, d = 32s + 8c + [0, 8).
   u32x4 qf[4];
   if (t < G) {
     const uint16_t *qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + t) * a.q_stride_h + 8 * c;
@@ -103,27 +155,20 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
-  const int64_t k_off = (int64_t)t * row_elems + 8 * c;
-  const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;
+  const int64_t k_off = (int64_t)t * row_elems + 8 * c;                        // + 32 s
+  const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;  // + 4 i rows
+  uint16_t *vt = reinterpret_cast<uint16_t *>(smem) + wave * kVTile;           // this wave's V tile
 
-  float m[4], l[4];
+  float m = -INFINITY, l = 0.f;  // running stats of head g = t
+  f32x4 acc[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    m[r] = -INFINITY;
-    l[r] = 0.f;
-  }
-  float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const float sm_scale = a.sm_scale;
-  float *dump_row =
-      WITH_DUMP ? a.dump + (int64_t)b * a.dump_stride_b + (int64_t)(h * G) * a.dump_stride_h : nullptr;
+  float *dump_g = (WITH_DUMP && t < G)
+                      ? a.dump + (int64_t)b * a.dump_stride_b + (int64_t)(h * G + t) * a.dump_stride_h
+                      : nullptr;
 
-  // Page j's base pointer for head h; a page id outside the cache is replaced
-  // by page 0 and all of its tokens are masked.
   auto page_base = [&](int j, bool &ok) -> const uint16_t * {
     int pid = a.kv_indices[ri.p0 + j];
     ok = pid >= 0 && (int64_t)pid < a.num_pages;
@@ -131,143 +176,127 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     return a.kv + (int64_t)pid * page_elems + (int64_t)h * kHeadDim;
   };
 
-  auto load = [&](const uint16_t *base, u32x4 *kf, u32x4 *vf) {
+  const int first = j0 + wave;
+  const int count = first < j1 ? (j1 - first + nw - 1) / nw : 0;
+  if (count > 0) {
+    bool ok;
+    const uint16_t *base = page_base(first, ok);
+    u32x4 kf[4], vf[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) kf[s] = ld128(base + k_off + 32 * s);
     if (WITH_V) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) vf[i] = ld128(base + v_off + (int64_t)(4 * i) * row_elems);
     }
-  };
-
-  auto process = [&](int j, bool ok, const u32x4 *kf, const u32x4 *vf) {
-    f32x4 S = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) S = E::mfma(qf[s], kf[s], S);
-
-    const int tok = j * kPageSize + t;
-    const bool valid = ok && tok < ri.kv_len;
-    float y[4], p[4], alpha[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float x = valid ? S[r] * sm_scale : -INFINITY;
-      if (WITH_DUMP) {
-        const int g = 4 * c + r;
-        if (g < G && valid && tok < a.dump_cap) dump_row[(int64_t)g * a.dump_stride_h + tok] = x;
-      }
-      y[r] = x * kLog2e;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float mn = fmaxf(m[r], row16_max(y[r]));
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      alpha[r] = fast_exp2(m[r] - mref);
-      p[r] = fast_exp2(y[r] - mref);
-      l[r] = l[r] * alpha[r] + row16_sum(p[r]);
-      m[r] = mn;
-    }
-    if (WITH_V) {
-      // Rescale the accumulators by each head's alpha (uniform per head).
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float al = readlane(alpha[g & 3], (g >> 2) << 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] *= al;
-      }
-      const bool tail = (j + 1) * kPageSize > ri.kv_len || !ok;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tt = c + 4 * i;  // V row handled by this lane
-        float pv[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) pv[g] = shfl(p[g & 3], ((g >> 2) << 4) + tt);
-        float vv[8];
-        const u32x4 w = vf[i];
-#pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) {
-          vv[2 * q2] = E::lo(w[q2]);
-          vv[2 * q2 + 1] = E::hi(w[q2]);
-        }
-        if (tail && (!ok || j * kPageSize + tt >= ri.kv_len)) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vv[e] = 0.f;  // stale rows may hold NaN/Inf
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pv[g], vv[e], acc[g][e]);
-      }
-    }
-  };
-
-  // Pages j0 + wave, j0 + wave + 4, ...: software pipelined one page ahead.
-  const int first = j0 + wave;
-  const int count = first < j1 ? (j1 - first + kWaves - 1) / kWaves : 0;
-  if (count > 0) {
-    u32x4 kc[4], vc[4], kn[4], vn[4];
-    bool okc, okn;
-    load(page_base(first, okc), kc, vc);
     int j = first;
-    for (int it = 0; it + 1 < count; ++it) {
-      const int jn = j + kWaves;
-      load(page_base(jn, okn), kn, vn);
-      process(j, okc, kc, vc);
+    for (int it = 0; it < count; ++it) {
+      // The next page (or this one again on the last iteration: an L2 hit, keeps the loads unconditional).
+      const int jn = it + 1 < count ? j + nw : j;
+      bool okn;
+      const uint16_t *nbase = page_base(jn, okn);
+
+      f32x4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        kc[s] = kn[s];
-        vc[s] = vn[s];
+      for (int s = 0; s < 4; ++s) S = E::mfma(kf[s], qf[s], S);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[s] = ld128(nbase + k_off + 32 * s);
+
+      const int tok0 = j * kPageSize + 4 * c;
+      float x[4], p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = (ok && tok0 + r < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
+      if (WITH_DUMP && t < G) {
+        if (ok && tok0 + 3 < ri.kv_len && tok0 + 3 < a.dump_cap && a.dump_vec) {
+          *reinterpret_cast<f32x4 *>(dump_g + tok0) = f32x4{x[0], x[1], x[2], x[3]};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (ok && tok0 + r < ri.kv_len && tok0 + r < a.dump_cap) dump_g[tok0 + r] = x[r];
+        }
       }
-      okc = okn;
+      float pm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] *= kLog2e;
+        pm = fmaxf(pm, x[r]);
+      }
+      const float mn = fmaxf(m, rows4_max(pm));
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = fast_exp2(m - mref);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = fast_exp2(x[r] - mref);
+        ps += p[r];
+      }
+      l = l * alpha + rows4_sum(ps);
+      m = mn;
+
+      if (WITH_V) {
+        // Stage V (stale rows past kv_len zeroed: they may hold NaN/Inf and meet p = 0).
+        const bool tail = !ok || (j + 1) * kPageSize > ri.kv_len;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          u32x4 w = vf[i];
+          if (tail && (!ok || j * kPageSize + 4 * i + c >= ri.kv_len)) w = u32x4{0u, 0u, 0u, 0u};
+          st128(vt + (4 * i + c) * kVStride + 8 * t, w);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vf[i] = ld128(nbase + v_off + (int64_t)(4 * i) * row_elems);
+
+        // Rescale the accumulators only when some head's running max moved.
+        if (__ballot(alpha != 1.f)) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float al = shfl(alpha, 4 * c + r);
+#pragma unroll
+            for (int n = 0; n < 8; ++n) acc[n][r] *= al;
+          }
+        }
+        s4_t pa;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pa[r] = t < G ? M16::pack(p[r]) : (short)0;
+        const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStride + 4 * (t & 3);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          const s4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t *)(rd + 16 * n));
+          acc[n] = M16::run(pa, bv, acc[n]);
+        }
+      }
       j = jn;
+      ok = okn;
     }
-    process(j, okc, kc, vc);
   }
 
-  // Sum the four token subsets of the P.V accumulators (lanes l, l^16, l^32, l^48).
+  // Merge the block's waves in LDS (the V tiles are dead once every wave left the loop).
+  __syncthreads();
+  float *s_ml = smem;                  // [nw][G][2]
+  float *s_acc = smem + nw * G * 2;    // [nw][G][128]
+  if (c == 0 && t < G) {
+    s_ml[(wave * G + t) * 2 + 0] = m;
+    s_ml[(wave * G + t) * 2 + 1] = l;
+  }
   if (WITH_V) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        acc[g][e] += shfl_xor(acc[g][e], 16);
-        acc[g][e] += shfl_xor(acc[g][e], 32);
-      }
-  }
-
-  // Merge the block's waves in LDS.
-  float *s_ml = smem;                       // [kWaves][G][2]
-  float *s_acc = smem + kWaves * G * 2;     // [kWaves][G][128]
-  if (t == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int g = 4 * c + r;
       if (g < G) {
-        s_ml[(wave * G + g) * 2 + 0] = m[r];
-        s_ml[(wave * G + g) * 2 + 1] = l[r];
+#pragma unroll
+        for (int n = 0; n < 8; ++n) s_acc[(wave * G + g) * kHeadDim + 16 * n + t] = acc[n][r];
       }
-    }
-  }
-  if (WITH_V && c == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float *dst = s_acc + (wave * G + g) * kHeadDim + 8 * t;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dst[e] = acc[g][e];
     }
   }
   __syncthreads();
 
   const int n_out = WITH_V ? G * kHeadDim : G;
-  for (int idx = threadIdx.x; idx < n_out; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < n_out; idx += blockDim.x) {
     const int g = WITH_V ? idx / kHeadDim : idx;
     const int dd = WITH_V ? idx % kHeadDim : 0;
     float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
     const float Mr = M == -INFINITY ? 0.f : M;
     float L = 0.f, A = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < nw; ++w) {
       const float sc = fast_exp2(s_ml[(w * G + g) * 2] - Mr);
       L = fmaf(s_ml[(w * G + g) * 2 + 1], sc, L);
       if (WITH_V) A = fmaf(s_acc[(w * G + g) * kHeadDim + dd], sc, A);
@@ -279,7 +308,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(ov);
       }
       if (dd == 0 && a.lse != nullptr)
-        a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+        a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
     } else {
       const int64_t pidx = (((int64_t)b * a.hkv + h) * a.nsplit + split) * G + g;
       if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
@@ -296,22 +325,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
 //   pages), plan = target_decode_plan (full CSR + logits dump),
 //   score = the standalone K-only scorer.
 template <int DT, int G>
-__global__ void __launch_bounds__(kThreads) paged_decode_full_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_full_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
   decode_split_body<DT, G, true, false>(a, smem);
 }
 template <int DT, int G>
-__global__ void __launch_bounds__(kThreads) paged_decode_subset_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_subset_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
   decode_split_body<DT, G, true, false>(a, smem);
 }
 template <int DT, int G>
-__global__ void __launch_bounds__(kThreads) paged_decode_plan_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_plan_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
   decode_split_body<DT, G, true, true>(a, smem);
 }
 template <int DT, int G>
-__global__ void __launch_bounds__(kThreads) page_score_kv_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
   decode_split_body<DT, G, false, true>(a, smem);
 }
@@ -365,53 +394,70 @@ __global__ void decode_merge_lse_kernel(DecodeArgs a, int G) {
 enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
 
 template <int DT, int G>
-void launch_split(const DecodeArgs &a, int mode, hipStream_t stream) {
+void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
   dim3 grid(a.nsplit, a.hkv, a.batch);
-  const size_t sm_attn = (size_t)kWaves * G * (2 + kHeadDim) * sizeof(float);
-  const size_t sm_score = (size_t)kWaves * G * 2 * sizeof(float);
+  dim3 block(64 * waves);
+  const size_t merge = (size_t)waves * G * (2 + kHeadDim) * sizeof(float);
+  const size_t tiles = (size_t)waves * kVTile * sizeof(uint16_t);
+  const size_t sm_attn = merge > tiles ? merge : tiles;
+  const size_t sm_score = (size_t)waves * G * 2 * sizeof(float);
   switch (mode) {
     case kAttn:
-      hipLaunchKernelGGL((paged_decode_full_kernel<DT, G>), grid, dim3(kThreads), sm_attn, stream, a);
+      hipLaunchKernelGGL((paged_decode_full_kernel<DT, G>), grid, block, sm_attn, stream, a);
       break;
     case kAttnSubset:
-      hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G>), grid, dim3(kThreads), sm_attn, stream, a);
+      hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G>), grid, block, sm_attn, stream, a);
       break;
     case kAttnDump:
-      hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G>), grid, dim3(kThreads), sm_attn, stream, a);
+      hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G>), grid, block, sm_attn, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, dim3(kThreads), sm_score, stream, a);
+      hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, sm_score, stream, a);
       break;
   }
 }
 
 template <int DT>
-void launch_split_g(const DecodeArgs &a, int G, int mode, hipStream_t stream) {
+void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t stream) {
   switch (G) {
-    case 1: launch_split<DT, 1>(a, mode, stream); break;
-    case 2: launch_split<DT, 2>(a, mode, stream); break;
-    case 3: launch_split<DT, 3>(a, mode, stream); break;
-    case 4: launch_split<DT, 4>(a, mode, stream); break;
-    case 5: launch_split<DT, 5>(a, mode, stream); break;
-    case 6: launch_split<DT, 6>(a, mode, stream); break;
-    case 7: launch_split<DT, 7>(a, mode, stream); break;
-    default: launch_split<DT, 8>(a, mode, stream); break;
+    case 1: launch_split<DT, 1>(a, waves, mode, stream); break;
+    case 2: launch_split<DT, 2>(a, waves, mode, stream); break;
+    case 3: launch_split<DT, 3>(a, waves, mode, stream); break;
+    case 4: launch_split<DT, 4>(a, waves, mode, stream); break;
+    case 5: launch_split<DT, 5>(a, waves, mode, stream); break;
+    case 6: launch_split<DT, 6>(a, waves, mode, stream); break;
+    case 7: launch_split<DT, 7>(a, waves, mode, stream); break;
+    default: launch_split<DT, 8>(a, waves, mode, stream); break;
   }
 }
 
 }  // namespace
 
-int decode_num_splits(int batch, int hkv, int max_pages) {
+// Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
+// captured graph keeps a valid shape): 4096 waves fill MI355X's 256 CUs at 4 waves per SIMD.
+// Few (row, head) pairs -> 16-wave blocks (one per CU, merged in LDS, no split-K partials);
+// many pairs -> smaller blocks.  Splits only when the pairs cannot fill the chip, and never
+// below 2 pages per wave.
+void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves) {
   const int64_t pairs = (int64_t)batch * hkv;
-  if (pairs <= 0 || max_pages <= 0) return 1;
-  const int64_t target_waves = 256 /*CUs*/ * 4 /*SIMDs*/ * 4 /*waves per SIMD*/;
-  int64_t ns = ceil_div(target_waves, pairs * kWaves);
-  int64_t cap = max_pages / (2 * kWaves);  // >= 2 pages per wave
-  if (cap < 1) cap = 1;
-  if (ns > cap) ns = cap;
-  if (ns < 1) ns = 1;
-  if (ns > 256) ns = 256;
-  return (int)ns;
+  int w = pairs <= 256 ? 16 : (pairs <= 512 ? 8 : 4);
+  int64_t ns = 1;
+  if (pairs > 0 && max_pages > 0) {
+    ns = ceil_div(256 * 4 * 4, pairs * w);
+    int64_t cap = max_pages / (2 * w);
+    if (cap < 1) cap = 1;
+    if (ns > cap) ns = cap;
+    if (ns < 1) ns = 1;
+    if (ns > 256) ns = 256;
+  }
+  *nsplit = (int)ns;
+  *waves = w;
+}
+
+int decode_num_splits(int batch, int hkv, int max_pages) {
+  int ns, w;
+  decode_plan(batch, hkv, max_pages, &ns, &w);
+  return ns;
 }
 
 static size_t partial_bytes(int batch, int hq, int nsplit, bool with_acc) {
@@ -466,10 +512,12 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.dump_stride_b = dump_stride_b;
   a.dump_stride_h = dump_stride_h;
   a.dump_cap = max_pages * kPageSize;
+  a.dump_vec = dump && !((uintptr_t)dump & 15u) && !(dump_stride_b & 3) && !(dump_stride_h & 3);
   a.batch = batch;
   a.hq = hq;
   a.hkv = hkv;
-  a.nsplit = decode_num_splits(batch, hkv, max_pages);
+  int waves;
+  decode_plan(batch, hkv, max_pages, &a.nsplit, &waves);
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;
@@ -488,9 +536,9 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
     return set_error(DELTA_ERR_INVALID, "%s: scorer needs an lse buffer", who);
 
   if (dtype == DELTA_BF16)
-    launch_split_g<DELTA_BF16>(a, G, mode, stream);
+    launch_split_g<DELTA_BF16>(a, G, waves, mode, stream);
   else
-    launch_split_g<DELTA_FP16>(a, G, mode, stream);
+    launch_split_g<DELTA_FP16>(a, G, waves, mode, stream);
   int rc = check_launch(who);
   if (rc) return rc;
   if (a.nsplit > 1) {

@@ -400,9 +400,10 @@ def rope(q: torch.Tensor, k: torch.Tensor, indptr: torch.Tensor, offsets: torch.
     return q_out, k_out
 
 
-def argmax_rows(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+def argmax_rows(logits: torch.Tensor, out: Optional[torch.Tensor] = None,
+                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """First index of each row's maximum (``delta_argmax_rows``); logits [rows, cols]."""
-    dev = _check_cuda(logits, out)
+    dev = _check_cuda(logits, out, workspace)
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be [rows, cols] with unit inner stride")
     rows, cols = logits.shape
@@ -410,6 +411,54 @@ def argmax_rows(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> tor
         out = torch.empty(rows, dtype=torch.int64, device=dev)
     if out.dtype != torch.int64 or out.dim() != 1 or out.shape[0] < rows:
         raise ValueError("out must be int64 [>=rows]")
+    need = int(_lib.query("delta_argmax_workspace_bytes", rows))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    nbytes = workspace.numel() * workspace.element_size()
     _lib.call("delta_argmax_rows", logits.data_ptr(), logits.stride(0), int(rows), int(cols),
-              _dtype_code(logits), out.data_ptr(), out.stride(0), _stream(dev))
+              _dtype_code(logits), out.data_ptr(), out.stride(0), workspace.data_ptr(), nbytes, _stream(dev))
+    return out
+
+
+def _rows2d(name: str, t: torch.Tensor, dim: int) -> torch.Tensor:
+    t2 = t.reshape(-1, dim)
+    if t2.stride(1) != 1 or t2.stride(0) % 8 or t2.data_ptr() % 16:
+        raise ValueError(f"{name} must have 16-byte aligned contiguous rows")
+    return t2
+
+
+def add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                out: Optional[torch.Tensor] = None):
+    """(x + residual, RMSNorm(x + residual) * weight) in one kernel (``delta_add_rmsnorm``).
+
+    Returns ``(h, y)``; ``h`` is ``x`` itself when ``residual`` is None."""
+    dev = _check_cuda(x, residual, weight, out)
+    dim = x.shape[-1]
+    _dtype_code(x)
+    if weight.dtype != x.dtype or weight.numel() != dim or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [dim] tensor of x's dtype")
+    x2 = _rows2d("x", x, dim)
+    rows = x2.shape[0]
+    h = x if residual is None else torch.empty_like(x)
+    r2 = None if residual is None else _rows2d("residual", residual, dim)
+    h2 = None if residual is None else _rows2d("h", h, dim)
+    if out is None:
+        out = torch.empty_like(x)
+    o2 = _rows2d("out", out, dim)
+    _lib.call("delta_add_rmsnorm", x2.data_ptr(), x2.stride(0), _ptr(r2), 0 if r2 is None else r2.stride(0),
+              weight.data_ptr(), float(eps), _ptr(h2), 0 if h2 is None else h2.stride(0), o2.data_ptr(),
+              o2.stride(0), int(rows), int(dim), _dtype_code(x), _stream(dev))
+    return h, out
+
+
+def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(gate) * up of a ``[..., 2 * inter]`` gate|up tensor (``delta_silu_mul``)."""
+    dev = _check_cuda(gate_up, out)
+    inter = gate_up.shape[-1] // 2
+    g2 = _rows2d("gate_up", gate_up, 2 * inter)
+    if out is None:
+        out = torch.empty(*gate_up.shape[:-1], inter, dtype=gate_up.dtype, device=dev)
+    o2 = _rows2d("out", out, inter)
+    _lib.call("delta_silu_mul", g2.data_ptr(), g2.stride(0), o2.data_ptr(), o2.stride(0), int(g2.shape[0]),
+              int(inter), _dtype_code(gate_up), _stream(dev))
     return out

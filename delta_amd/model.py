@@ -5,9 +5,12 @@ Mirrors DELTA/Engine/DELTA/model.py: ``ModelArgs`` and the model-shape table
 per-layer binding of ``attn_decode`` to ``target_decode`` /
 ``target_decode_plan`` (last full layer before a non-full one) /
 ``target_subset_decode`` (146-196), and the block structure (330-532).  The
-dense parts (GEMMs, RMSNorm, SiLU) stay torch ops (hipBLASLt on ROCm); the
-final argmax is the HIP ``delta_argmax_rows`` kernel so a captured decode step
-records no torch multi-block reduction.
+GEMMs stay torch ops (hipBLASLt on ROCm).  By default (``fused=True``) the
+element-wise chains between them are HIP kernels: the residual add + RMSNorm
+(``delta_add_rmsnorm``), ``silu(w1 x) * w3 x`` on one merged ``w13`` GEMM
+(``delta_silu_mul``) and the final argmax (``delta_argmax_rows``), so a captured
+decode step is not dominated by a dozen tiny launches per layer.  ``fused=False``
+runs the reference's op-by-op structure (same math, same roundings).
 
 No checkpoints ship with this build: ``init_random_weights`` gives every
 parameter seeded N(0, std) values of the named architecture.
@@ -124,7 +127,7 @@ class Transformer(nn.Module):
         self.norm = RMSNorm(config.dim, eps=config.norm_eps)
         self.output = nn.Linear(config.dim, config.vocab_size, bias=False)
         self.layer_roles: List[str] = []
-        self._argmax_out: Optional[Tensor] = None
+        self.fused = True
 
     def setup_caches(self, num_pages: int, page_size: int):
         """Allocate per-layer caches and bind each layer's attention op (model.py:146-196)."""
@@ -160,9 +163,18 @@ class Transformer(nn.Module):
 
     def forward_logits(self, idx, input_pos, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen):
         x = self.tok_embeddings(idx)
+        if not self.fused:
+            for layer in self.layers:
+                x = layer(x, input_pos, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen)
+            return self.output(self.norm(x))
+        # Residual stream carried as (x, pending): block i's output x + ffn is summed by the
+        # next block's fused add + norm.
+        pending = None
         for layer in self.layers:
-            x = layer(x, input_pos, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen)
-        return self.output(self.norm(x))
+            x, pending = layer.forward_fused(x, pending, input_pos, kv_append_indptr, kv_page_indices,
+                                             kv_page_indptr, kv_page_lastlen)
+        _, y = K.add_rmsnorm(x, pending, self.norm.weight, self.norm.eps)
+        return self.output(y)
 
     def _finalize_logits(self, logits: Tensor) -> Tensor:
         """argmax over the vocabulary on the HIP kernel; returns int64 [bsz, seqlen]."""
@@ -189,6 +201,15 @@ class TransformerBlock(nn.Module):
         h = x + self.attention(self.attention_norm(x), offsets, kv_append_indptr, kv_page_indices,
                                kv_page_indptr, kv_page_lastlen)
         return h + self.feed_forward(self.ffn_norm(h))
+
+    def forward_fused(self, x, pending, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr,
+                      kv_page_lastlen):
+        """Same block as ``forward`` with the input ``x + pending`` left unsummed; returns
+        ``(h, ffn_out)`` whose sum is the block output."""
+        x, a_in = K.add_rmsnorm(x, pending, self.attention_norm.weight, self.attention_norm.eps)
+        attn = self.attention(a_in, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen)
+        h, f_in = K.add_rmsnorm(x, attn, self.ffn_norm.weight, self.ffn_norm.eps)
+        return h, self.feed_forward.forward_fused(f_in)
 
 
 class Attention(nn.Module):
@@ -227,14 +248,30 @@ class Attention(nn.Module):
 
 
 class FeedForward(nn.Module):
+    """SwiGLU FFN; ``w1`` and ``w3`` live in one ``w13`` weight ``[2 * inter, dim]`` so the
+    gate and up projections are a single GEMM.  Checkpoints with separate ``w1`` / ``w3``
+    (the reference's names) are merged on load."""
+
     def __init__(self, config: ModelArgs) -> None:
         super().__init__()
-        self.w1 = nn.Linear(config.dim, config.intermediate_size, bias=False)
-        self.w3 = nn.Linear(config.dim, config.intermediate_size, bias=False)
+        self.inter = config.intermediate_size
+        self.w13 = nn.Linear(config.dim, 2 * config.intermediate_size, bias=False)
         self.w2 = nn.Linear(config.intermediate_size, config.dim, bias=False)
+        self._register_load_state_dict_pre_hook(self._merge_w1_w3)
+
+    @staticmethod
+    def _merge_w1_w3(state_dict, prefix, *args):
+        if prefix + "w1.weight" in state_dict:
+            w1 = state_dict.pop(prefix + "w1.weight")
+            w3 = state_dict.pop(prefix + "w3.weight")
+            state_dict[prefix + "w13.weight"] = torch.cat([w1, w3])
 
     def forward(self, x: Tensor) -> Tensor:
-        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+        g, u = self.w13(x).split(self.inter, dim=-1)
+        return self.w2(F.silu(g) * u)
+
+    def forward_fused(self, x: Tensor) -> Tensor:
+        return self.w2(K.silu_mul(self.w13(x)))
 
 
 class RMSNorm(nn.Module):

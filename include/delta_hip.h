@@ -249,15 +249,32 @@ int delta_rope(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
                float high_freq_factor, float old_context_len, delta_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
-/* Decode-step helper                                                         */
+/* Dense decode-step helpers (the element-wise chains between the GEMMs)      */
 /* ------------------------------------------------------------------------ */
 
 /* out[r * out_stride] = first index of the maximum of logits[r, :cols]
  * (bf16/fp16 rows with stride row_stride; NaN ranks highest), as torch.argmax
- * in _finalize_logits (model.py:320-323).  Used inside the captured decode
- * step in place of torch's multi-block reduction. */
+ * in _finalize_logits (model.py:320-323).  Two passes through a caller
+ * workspace of delta_argmax_workspace_bytes(rows); no memset, so it can sit
+ * inside a captured decode step. */
+size_t delta_argmax_workspace_bytes(int rows);
 int delta_argmax_rows(const void *logits, int64_t row_stride, int rows, int cols, int dtype,
-                      int64_t *out, int64_t out_stride, delta_stream_t stream);
+                      int64_t *out, int64_t out_stride, void *workspace, size_t workspace_bytes,
+                      delta_stream_t stream);
+
+/* Residual add + RMSNorm of rows of length dim (<= 8192, multiple of 8):
+ *   h = x + residual (rounded to the dtype; skipped when residual == NULL, h = x),
+ *   out = dtype(dtype(h * rsqrt(mean(h^2) + eps)) * weight),
+ * i.e. RMSNorm.forward (model.py:527-532) applied to TransformerBlock's residual
+ * sum (model.py:338-341).  sum_out (optional) receives h. */
+int delta_add_rmsnorm(const void *x, int64_t x_stride, const void *residual, int64_t r_stride,
+                      const void *weight, float eps, void *sum_out, int64_t s_stride, void *out,
+                      int64_t out_stride, int rows, int dim, int dtype, delta_stream_t stream);
+
+/* out[r, i] = dtype(dtype(silu(g)) * u) with g = gate_up[r, i], u = gate_up[r, inter + i]:
+ * FeedForward's silu(w1 x) * w3 x (model.py:509-514) on the merged w1|w3 GEMM output. */
+int delta_silu_mul(const void *gate_up, int64_t gu_stride, void *out, int64_t out_stride, int rows,
+                   int inter, int dtype, delta_stream_t stream);
 
 #ifdef __cplusplus
 }

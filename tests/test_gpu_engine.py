@@ -186,3 +186,29 @@ def test_prefill_rows_are_causal():
     ref, _ = O.paged_decode_attention(q.cpu(), cache, ip, torch.tensor(ind, dtype=torch.int32),
                                       torch.tensor(lastl, dtype=torch.int32), 1 / 128 ** 0.5)
     assert_close(o, ref, "prefill layer 0")
+
+
+def test_fused_dense_path_matches_reference_structure():
+    """The fused element-wise kernels give the same logits as the reference's op-by-op blocks."""
+    eng = make_engine(B=3)
+    eng.prepare_synthetic_decode([100, 200, 300], decode_budget=16, seed=7)
+    sel = eng.page_selector
+    outs = []
+    with torch.inference_mode():
+        for fused in (True, False):
+            eng.model.fused = fused
+            eng._step = eng._decode_csr()
+            import delta_amd.kernels as K
+            K.decode_page_info(eng.cachelens, eng.slot_block_table, eng.batch_size, eng.k_eff,
+                               eng.compression_ratio, True, sel.paged_kv_indptr, sel.paged_kv_indices,
+                               sel.paged_kv_last_page_len, row_block_table=sel._block_table,
+                               subset_indices=sel.paged_subset_kv_indices,
+                               subset_indptr=sel.paged_subset_kv_indptr, use_subset=eng.use_subset_flag)
+            outs.append(eng.model.forward_logits(eng.static_tokens, eng.cachelens, eng.qo_indptr,
+                                                 sel.paged_kv_indices, sel.paged_kv_indptr,
+                                                 sel.paged_kv_last_page_len).float())
+            eng._step = None
+    a, b = outs
+    cos = torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0).item()
+    assert cos > 0.999, cos
+    assert (a - b).abs().max().item() < 0.05 * b.abs().max().item()

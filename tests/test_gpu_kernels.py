@@ -48,10 +48,10 @@ def gpu(c):
 
 def assert_ulp_close(a, b):
     """Two kernel variants (with / without the logits dump) round the same math
-    differently in the last bit at most."""
+    differently by a few ulp at most (P is rounded to the KV dtype for the P.V MFMA)."""
     ulp = torch.finfo(a.dtype).eps
     a, b = a.float(), b.float()
-    assert ((a - b).abs() <= ulp * b.abs() + 1e-6).all()
+    assert ((a - b).abs() <= 4 * ulp * b.abs() + 1e-5).all()
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -356,3 +356,33 @@ def test_decode_is_deterministic_full_size():
     pos = inv[idx.long()].view(B, c.k)
     assert bool((pos[:, 1:] > pos[:, :-1]).all())
     assert bool((pos[:, -c.L:] == torch.arange(mp - c.L, mp, device=DEV)).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dense_step_helpers_match_torch(dtype):
+    """add_rmsnorm / silu_mul / argmax against the torch ops they replace (model.py:320-323, 509-532)."""
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    rows, dim, inter = 32, 4096, 1024
+    x = torch.randn(rows, dim, generator=gen, device=DEV).to(dtype)
+    r = torch.randn(rows, dim, generator=gen, device=DEV).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim, generator=gen, device=DEV)).to(dtype)
+    h, y = K.add_rmsnorm(x, r, w, 1e-5)
+    h_ref = x + r
+    hf = h_ref.float()
+    y_ref = (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(dtype) * w
+    assert torch.equal(h, h_ref)
+    ulp = torch.finfo(dtype).eps
+    assert ((y.float() - y_ref.float()).abs() <= 2 * ulp * y_ref.float().abs() + 1e-6).all()
+    _, y0 = K.add_rmsnorm(x, None, w, 1e-5)
+    xf = x.float()
+    y0_ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(dtype) * w
+    assert ((y0.float() - y0_ref.float()).abs() <= 2 * ulp * y0_ref.float().abs() + 1e-6).all()
+    gu = torch.randn(rows, 2 * inter, generator=gen, device=DEV).to(dtype) * 3
+    s = K.silu_mul(gu)
+    s_ref = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
+    assert ((s.float() - s_ref.float()).abs() <= 2 * ulp * s_ref.float().abs() + 1e-6).all()
+    logits = torch.randn(rows, 128256, generator=gen, device=DEV).to(dtype)
+    logits[3, 77] = logits[3].max() + 1
+    logits[4, 10] = logits[4, 20] = logits[4].max() + 1   # tie: first index wins
+    logits[5, 1000] = float("nan")                         # NaN ranks highest, as torch.argmax
+    assert torch.equal(K.argmax_rows(logits), torch.argmax(logits, -1))

@@ -227,8 +227,11 @@ class LMBackend:
 
     def attn_full(self, q, kv_cache):
         st = self._step
+        # Prefill rows (one per prompt token) can outnumber the decode batch the static
+        # workspace was sized for; they use the grow-only shared workspace (never captured).
+        ws = self.workspace if st.mode == "decode" else None
         return K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                              max_pages_per_row=st.max_pages, workspace=self.workspace)
+                              max_pages_per_row=st.max_pages, workspace=ws)
 
     def attn_subset(self, q, kv_cache):
         if not (self.enable_selective_cache and self._decode_mode()):

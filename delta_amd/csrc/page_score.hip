@@ -26,6 +26,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
                int head_dim, int dtype, float sm_scale, int max_pages, int mode,
                void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who);
 int decode_num_splits(int batch, int hkv, int max_pages);
+size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc);
 
 namespace {
 
@@ -156,10 +157,10 @@ extern "C" DELTA_EXPORT int delta_page_scores_from_logits(const float *logits_du
 
 extern "C" DELTA_EXPORT size_t delta_page_score_kv_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                                                    int max_pages_per_row) {
+  // [partials of the K-only decode][lse]
   const int ns = delta::decode_num_splits(batch, num_kv_heads, max_pages_per_row);
-  size_t lse_bytes = ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
-  size_t part = ns > 1 ? (size_t)batch * num_qo_heads * ns * 2 * sizeof(float) : 0;
-  return lse_bytes + part;
+  const size_t lse_bytes = ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
+  return delta::decode_workspace_bytes(batch, num_qo_heads, ns, false) + lse_bytes;
 }
 
 extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -184,13 +185,13 @@ extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, 
     return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
   if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
   hipStream_t st = (hipStream_t)stream;
-  float *lse_ws = (float *)workspace;
-  const size_t lse_bytes = ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
-  void *part = (char *)workspace + lse_bytes;
+  const int ns = decode_num_splits(batch, num_kv_heads, max_pages);
+  const size_t dec = decode_workspace_bytes(batch, num_qo_heads, ns, false);
+  float *lse_ws = (float *)((char *)workspace + dec);
   int rc = run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
                       kv_last_page_len, nullptr, 0, 0, lse_ws, logits_dump, dump_stride_b, dump_stride_h, batch,
-                      num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale, max_pages, /*kScoreOnly*/ 2, part,
-                      workspace_bytes - lse_bytes, st, who);
+                      num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale, max_pages, /*kScoreOnly*/ 2, workspace,
+                      dec, st, who);
   if (rc) return rc;
   return launch_scores(logits_dump, dump_stride_b, dump_stride_h, lse_ws, kv_indptr, kv_last_page_len, scores,
                        score_stride, batch, num_qo_heads, max_pages, st, who);

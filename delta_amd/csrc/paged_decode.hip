@@ -5,19 +5,16 @@
 // BatchDumpAttentionWeights logits side-write (backend.py:175-222, 518-585).
 //
 // Work decomposition
-//   grid  = (num_splits, num_kv_heads, batch); block = 4 waves (256 threads).
-//   A block owns one (row, kv head, split) and its 4 waves take the split's
-//   pages round robin, so a block streams 4 consecutive pages of one head.
-//   Per page and wave:
-//     q.K  : 4 x v_mfma_f32_16x16x32_{bf16,f16}.  A = the G query heads of the
-//            group (rows g = lane%16, zero padded to 16), B = the page's 16 K
-//            rows (cols t = lane%16).  Lane group c = lane/16 supplies
-//            d in [32s + 8c, 32s + 8c + 8) at step s, so each load instruction
-//            covers 16 rows x 64 contiguous bytes.
-//     softmax: online, log2 domain, DPP reductions across the 16-lane rows.
-//     P.V  : VALU fp32 FMA; lane (c, t) owns d in [8t, 8t+8) of V rows
-//            c, c+4, c+8, c+12 (each load instruction covers 4 full rows).
-//   The 4 waves merge in LDS; with num_splits > 1 the block writes an
+//   grid = (num_splits * Hkv / hb, batch); block = 16 waves = hb kv heads x R waves each.
+//   Page-major (hb = Hkv): wave w works on kv head w % Hkv and takes every R-th page of
+//   the block's split, so the Hkv waves of one page slot read all heads of the same page
+//   (its K and V are each one contiguous 16 * Hkv * 256-byte run).  Head-major (hb = 1):
+//   the 16 waves of a (row, kv head) block take its pages round robin, with no split.
+//   The choice per shape is decode_plan's.
+//   Per page and wave (details at decode_split_body): q.K and P.V on MFMA, online
+//   softmax in the log2 domain; page ids preloaded 64 per register, the next page's
+//   K and V always in flight.
+//   The block's waves merge in LDS per head; with num_splits > 1 the block writes an
 //   un-normalised partial (acc, m, l) and a merge kernel combines the splits.
 //
 // HBM bytes per launch (algorithmic): K and V of every attended token once,
@@ -49,6 +46,7 @@ struct DecodeArgs {
   float *part_acc;  // [batch][hkv][nsplit][G][128]
   float *part_ml;   // [batch][hkv][nsplit][G][2]  (m in log2 units, l)
   int batch, hq, hkv, nsplit;
+  int hb;           // kv heads per block (hkv: page-major, 1: head-major)
   float sm_scale;
 };
 
@@ -115,7 +113,8 @@ __device__ __forceinline__ float rows4_sum(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// One (row, kv head, split) per block, blockDim/64 waves taking the split's pages round robin.
+// One (row, split, group of hb kv heads) per block; R = blockDim/64/hb waves per head take the
+// split's pages round robin.
 //   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows (lane%16 = token,
 //         lane/16 picks d in [32s + 8c, +8) at step s), B = the group's query rows (zero padded
 //         to 16 columns).  D puts tokens 4c..4c+3 of head g = lane%16 in lane (c, g).
@@ -129,10 +128,15 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   using M16 = Mfma16<DT>;
 
   const int nw = blockDim.x >> 6;
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  const int hb = a.hb;
+  const int R = nw / hb;  // waves per kv head
+  const int hgroups = a.hkv / hb;
+  const int split = blockIdx.x / hgroups;
+  const int head0 = (blockIdx.x % hgroups) * hb;
+  const int b = blockIdx.y;
   const int wave = uniform(threadIdx.x >> 6);
+  const int h = head0 + wave % hb;
+  const int rslot = wave / hb;
   const int lane = threadIdx.x & 63;
   const int c = lane >> 4;
   const int t = lane & 15;
@@ -158,6 +162,11 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   const int64_t k_off = (int64_t)t * row_elems + 8 * c;                        // + 32 s
   const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;  // + 4 i rows
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem) + wave * kVTile;           // this wave's V tile
+  // Logits staged per wave for kDumpSlots pages, then written out together: on gfx9 a
+  // vector store pending beside loads makes the next load wait drain the whole queue, so
+  // stores are batched instead of issued every page.
+  constexpr int kDumpSlots = G <= 4 ? 16 : 8;
+  float *dbuf = reinterpret_cast<float *>(smem + (WITH_V ? nw * kVTile / 2 : 0)) + wave * (kDumpSlots * G * kPageSize);
 
   float m = -INFINITY, l = 0.f;  // running stats of head g = t
   f32x4 acc[8];
@@ -165,35 +174,46 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const float sm_scale = a.sm_scale;
-  float *dump_g = (WITH_DUMP && t < G)
-                      ? a.dump + (int64_t)b * a.dump_stride_b + (int64_t)(h * G + t) * a.dump_stride_h
-                      : nullptr;
+  const int first = j0 + rslot;
+  const int count = first < j1 ? (j1 - first + R - 1) / R : 0;
 
-  auto page_base = [&](int j, bool &ok) -> const uint16_t * {
-    int pid = a.kv_indices[ri.p0 + j];
-    ok = pid >= 0 && (int64_t)pid < a.num_pages;
-    pid = ok ? pid : 0;
-    return a.kv + (int64_t)pid * page_elems + (int64_t)h * kHeadDim;
+  // Page ids of this wave's pages, 64 per register: lane i holds iteration 64 * chunk + i
+  // (-1 marks an id outside the cache).  Loading them ahead keeps the page loop free of
+  // dependent index loads; each page address comes from one readlane.
+  auto load_ids = [&](int it0) -> int {
+    const int it = it0 + lane;
+    int pid = -1;
+    if (it < count) pid = a.kv_indices[ri.p0 + first + (int64_t)R * it];
+    return (pid >= 0 && (int64_t)pid < a.num_pages) ? pid : -1;
+  };
+  auto page_ptr = [&](int pid) -> const uint16_t * {
+    return a.kv + (int64_t)(pid < 0 ? 0 : pid) * page_elems + (int64_t)h * kHeadDim;
   };
 
-  const int first = j0 + wave;
-  const int count = first < j1 ? (j1 - first + nw - 1) / nw : 0;
-  if (count > 0) {
-    bool ok;
-    const uint16_t *base = page_base(first, ok);
+  // Chunks of up to 64 pages: one id load (and one pipeline drain) per chunk.
+  for (int c0 = 0; c0 < count; c0 += 64) {
+    const int cn = count - c0 < 64 ? count - c0 : 64;
+    const int ids = load_ids(c0);
+    int pid = __builtin_amdgcn_readlane(ids, 0);
+    const uint16_t *base = page_ptr(pid);
     u32x4 kf[4], vf[4];
+    // Issue order K then V, as in the loop body, so the loop's waits can stay partial.
 #pragma unroll
     for (int s = 0; s < 4; ++s) kf[s] = ld128(base + k_off + 32 * s);
+    __builtin_amdgcn_sched_barrier(0);
     if (WITH_V) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) vf[i] = ld128(base + v_off + (int64_t)(4 * i) * row_elems);
     }
-    int j = first;
-    for (int it = 0; it < count; ++it) {
-      // The next page (or this one again on the last iteration: an L2 hit, keeps the loads unconditional).
-      const int jn = it + 1 < count ? j + nw : j;
-      bool okn;
-      const uint16_t *nbase = page_base(jn, okn);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t okmask = 0;  // dump slots holding a valid page
+    for (int it = 0; it < cn; ++it) {
+      const int j = first + R * (c0 + it);
+      const bool ok = pid >= 0;
+      // The next page (or this one again on the chunk's last iteration: an L2 hit, keeps the
+      // loads unconditional).
+      const int pidn = __builtin_amdgcn_readlane(ids, it + 1 < cn ? it + 1 : it);
+      const uint16_t *nbase = page_ptr(pidn);
 
       f32x4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -205,13 +225,31 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       float x[4], p[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = (ok && tok0 + r < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
-      if (WITH_DUMP && t < G) {
-        if (ok && tok0 + 3 < ri.kv_len && tok0 + 3 < a.dump_cap && a.dump_vec) {
-          *reinterpret_cast<f32x4 *>(dump_g + tok0) = f32x4{x[0], x[1], x[2], x[3]};
-        } else {
+      if (WITH_DUMP) {
+        const int slot = it % kDumpSlots;
+        if (t < G) *reinterpret_cast<f32x4 *>(dbuf + (slot * G + t) * kPageSize + 4 * c) = f32x4{x[0], x[1], x[2], x[3]};
+        okmask |= (ok ? 1u : 0u) << slot;
+        if (slot == kDumpSlots - 1 || it + 1 == cn) {
+          // Write the staged pages: 4 lanes per (page, head) run of 16 logits.
+          const int it0 = c0 + it - slot;
+          const int nseg = (slot + 1) * G;
+          for (int e = lane; e < 4 * nseg; e += 64) {
+            const int seg = e >> 2, qq = e & 3;
+            const int sl = seg / G, g = seg % G;
+            const int tk = (first + R * (it0 + sl)) * kPageSize + 4 * qq;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(dbuf + seg * kPageSize + 4 * qq);
+            float *dst = a.dump + (int64_t)b * a.dump_stride_b + (int64_t)(h * G + g) * a.dump_stride_h + tk;
+            if ((okmask >> sl) & 1u) {
+              if (tk + 3 < ri.kv_len && tk + 3 < a.dump_cap && a.dump_vec) {
+                *reinterpret_cast<f32x4 *>(dst) = v;
+              } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (ok && tok0 + r < ri.kv_len && tok0 + r < a.dump_cap) dump_g[tok0 + r] = x[r];
+                for (int r = 0; r < 4; ++r)
+                  if (tk + r < ri.kv_len && tk + r < a.dump_cap) dst[r] = v[r];
+              }
+            }
+          }
+          okmask = 0;
         }
       }
       float pm = -INFINITY;
@@ -233,12 +271,13 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       m = mn;
 
       if (WITH_V) {
-        // Stage V (stale rows past kv_len zeroed: they may hold NaN/Inf and meet p = 0).
-        const bool tail = !ok || (j + 1) * kPageSize > ri.kv_len;
+        // Stage V; rows past kv_len (and all rows of an invalid page) are zeroed by mask, since
+        // they may hold NaN/Inf and meet p = 0.
+        const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          u32x4 w = vf[i];
-          if (tail && (!ok || j * kPageSize + 4 * i + c >= ri.kv_len)) w = u32x4{0u, 0u, 0u, 0u};
+          const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
+          const u32x4 w = vf[i] & u32x4{keep, keep, keep, keep};
           st128(vt + (4 * i + c) * kVStride + 8 * t, w);
         }
 #pragma unroll
@@ -263,8 +302,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
           acc[n] = M16::run(pa, bv, acc[n]);
         }
       }
-      j = jn;
-      ok = okn;
+      pid = pidn;
     }
   }
 
@@ -288,20 +326,24 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   }
   __syncthreads();
 
-  const int n_out = WITH_V ? G * kHeadDim : G;
+  // One output per (kv head, group row, d): combine the R waves of that head.
+  const int n_out = hb * (WITH_V ? G * kHeadDim : G);
   for (int idx = threadIdx.x; idx < n_out; idx += blockDim.x) {
-    const int g = WITH_V ? idx / kHeadDim : idx;
+    const int hl = WITH_V ? idx / (G * kHeadDim) : idx / G;  // head within the block
+    const int hh = head0 + hl;
+    const int g = WITH_V ? (idx / kHeadDim) % G : idx % G;
     const int dd = WITH_V ? idx % kHeadDim : 0;
     float M = -INFINITY;
-    for (int w = 0; w < nw; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
+    for (int r = 0; r < R; ++r) M = fmaxf(M, s_ml[((r * hb + hl) * G + g) * 2]);
     const float Mr = M == -INFINITY ? 0.f : M;
     float L = 0.f, A = 0.f;
-    for (int w = 0; w < nw; ++w) {
+    for (int r = 0; r < R; ++r) {
+      const int w = r * hb + hl;
       const float sc = fast_exp2(s_ml[(w * G + g) * 2] - Mr);
       L = fmaf(s_ml[(w * G + g) * 2 + 1], sc, L);
       if (WITH_V) A = fmaf(s_acc[(w * G + g) * kHeadDim + dd], sc, A);
     }
-    const int hq = h * G + g;
+    const int hq = hh * G + g;
     if (a.nsplit == 1) {
       if (WITH_V) {
         const float ov = L > 0.f ? A / L : 0.f;
@@ -310,7 +352,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       if (dd == 0 && a.lse != nullptr)
         a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
     } else {
-      const int64_t pidx = (((int64_t)b * a.hkv + h) * a.nsplit + split) * G + g;
+      const int64_t pidx = (((int64_t)b * a.hkv + hh) * a.nsplit + split) * G + g;
       if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
       if (dd == 0) {
         a.part_ml[pidx * 2 + 0] = M;
@@ -345,62 +387,68 @@ __global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArg
   decode_split_body<DT, G, false, true>(a, smem);
 }
 
-// Combines the split partials of one (row, q head): o = sum A_s 2^(m_s-M) / sum l_s 2^(m_s-M).
+// Combines the split partials of one (row, kv head): for each of its G query rows and d,
+//   o = sum_s A_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),  lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2,
+// accumulated online (running max) so every partial is loaded in a single pass.
 template <int DT>
-__global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a, int G) {
   using E = Elem<DT>;
-  const int bh = blockIdx.x;
-  const int b = bh / a.hq;
-  const int hq = bh % a.hq;
-  const int h = hq / G;
-  const int g = hq % G;
-  const int dd = threadIdx.x;
-  const int64_t base = (((int64_t)b * a.hkv + h) * a.nsplit) * G + g;
-  float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(base + (int64_t)s * G) * 2]);
-  const float Mr = M == -INFINITY ? 0.f : M;
-  float L = 0.f, A = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const int64_t pidx = base + (int64_t)s * G;
-    const float sc = fast_exp2(a.part_ml[pidx * 2] - Mr);
-    L = fmaf(a.part_ml[pidx * 2 + 1], sc, L);
-    A = fmaf(a.part_acc[pidx * kHeadDim + dd], sc, A);
+  const int b = blockIdx.x / a.hkv;
+  const int h = blockIdx.x % a.hkv;
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
+    const int g = idx / kHeadDim;
+    const int dd = idx % kHeadDim;
+    const int64_t base = ((int64_t)b * a.hkv + h) * a.nsplit * G + g;
+    float M = -INFINITY, L = 0.f, A = 0.f;
+#pragma unroll 4
+    for (int s = 0; s < a.nsplit; ++s) {
+      const int64_t pidx = base + (int64_t)s * G;
+      const float ms = a.part_ml[pidx * 2], ls = a.part_ml[pidx * 2 + 1], as = a.part_acc[pidx * kHeadDim + dd];
+      const float mn = fmaxf(M, ms);
+      const float mr = mn == -INFINITY ? 0.f : mn;
+      const float co = fast_exp2(M - mr), cs = fast_exp2(ms - mr);
+      L = L * co + ls * cs;
+      A = A * co + as * cs;
+      M = mn;
+    }
+    const int hq = h * G + g;
+    a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(L > 0.f ? A / L : 0.f);
+    if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
   }
-  const float ov = L > 0.f ? A / L : 0.f;
-  a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(ov);
-  if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
 }
 
-// lse-only merge (scorer path without V).
-__global__ void decode_merge_lse_kernel(DecodeArgs a, int G) {
+// lse-only merge (scorer path without V), one thread per (row, q head).
+__global__ void __launch_bounds__(256) decode_merge_lse_kernel(DecodeArgs a, int G) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= a.batch * a.hq) return;
   const int b = idx / a.hq;
   const int hq = idx % a.hq;
-  const int h = hq / G;
-  const int g = hq % G;
-  const int64_t base = (((int64_t)b * a.hkv + h) * a.nsplit) * G + g;
-  float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(base + (int64_t)s * G) * 2]);
-  const float Mr = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
+  const int64_t base = ((int64_t)b * a.hkv + hq / G) * a.nsplit * G + hq % G;
+  float M = -INFINITY, L = 0.f;
+#pragma unroll 4
   for (int s = 0; s < a.nsplit; ++s) {
     const int64_t pidx = base + (int64_t)s * G;
-    L = fmaf(a.part_ml[pidx * 2 + 1], fast_exp2(a.part_ml[pidx * 2] - Mr), L);
+    const float ms = a.part_ml[pidx * 2], ls = a.part_ml[pidx * 2 + 1];
+    const float mn = fmaxf(M, ms);
+    const float mr = mn == -INFINITY ? 0.f : mn;
+    L = L * fast_exp2(M - mr) + ls * fast_exp2(ms - mr);
+    M = mn;
   }
-  a.lse[idx] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+  a.lse[idx] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
 
 enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
 
 template <int DT, int G>
 void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
-  dim3 grid(a.nsplit, a.hkv, a.batch);
+  dim3 grid(a.nsplit * (a.hkv / a.hb), a.batch);
   dim3 block(64 * waves);
   const size_t merge = (size_t)waves * G * (2 + kHeadDim) * sizeof(float);
   const size_t tiles = (size_t)waves * kVTile * sizeof(uint16_t);
+  const size_t dumps = (size_t)waves * (G <= 4 ? 16 : 8) * G * kPageSize * sizeof(float);
   const size_t sm_attn = merge > tiles ? merge : tiles;
-  const size_t sm_score = (size_t)waves * G * 2 * sizeof(float);
+  const size_t sm_plan = merge > tiles + dumps ? merge : tiles + dumps;
+  const size_t sm_score = dumps > (size_t)waves * G * 2 * sizeof(float) ? dumps : (size_t)waves * G * 2 * sizeof(float);
   switch (mode) {
     case kAttn:
       hipLaunchKernelGGL((paged_decode_full_kernel<DT, G>), grid, block, sm_attn, stream, a);
@@ -409,7 +457,7 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
       hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G>), grid, block, sm_attn, stream, a);
       break;
     case kAttnDump:
-      hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G>), grid, block, sm_attn, stream, a);
+      hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G>), grid, block, sm_plan, stream, a);
       break;
     default:
       hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, sm_score, stream, a);
@@ -434,36 +482,51 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 }  // namespace
 
 // Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
-// captured graph keeps a valid shape): 4096 waves fill MI355X's 256 CUs at 4 waves per SIMD.
-// Few (row, head) pairs -> 16-wave blocks (one per CU, merged in LDS, no split-K partials);
-// many pairs -> smaller blocks.  Splits only when the pairs cannot fill the chip, and never
-// below 2 pages per wave.
-void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves) {
-  const int64_t pairs = (int64_t)batch * hkv;
-  int w = pairs <= 256 ? 16 : (pairs <= 512 ? 8 : 4);
+// captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads
+// (hb * R = 16 waves):
+//   page-major (hb = Hkv): the Hkv waves of one page slot read all heads of a page
+//     together (whole 32 KiB K and V runs: ~5.9 TB/s on MI355X), and the split count
+//     brings the launch to 4096 waves (4 per SIMD on 256 CUs), never below 2 pages per
+//     wave; splits cost a merge launch (~5 us);
+//   head-major (hb = 1) when the (row, kv head) pairs alone give >= 256 blocks and the
+//     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
+//     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
+//     faster page-major gather repays the merge.
+constexpr int kHeadMajorPairs = 256;
+constexpr int64_t kHeadMajorPageHeads = 65536;
+
+void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int *hb) {
+  int h = hkv;
+  if ((int64_t)batch * hkv >= kHeadMajorPairs && (int64_t)batch * hkv * max_pages <= kHeadMajorPageHeads) h = 1;
+  int R = h > 0 ? kMaxWaves / h : 1;
+  if (R < 1) R = 1;
+  const int w = h * R;
+  const int groups = h > 0 ? hkv / h : 1;
   int64_t ns = 1;
-  if (pairs > 0 && max_pages > 0) {
-    ns = ceil_div(256 * 4 * 4, pairs * w);
-    int64_t cap = max_pages / (2 * w);
+  if (batch > 0 && max_pages > 0) {
+    ns = ceil_div(256 * 4 * 4, (int64_t)batch * groups * w);
+    int64_t cap = max_pages / (2 * R);
     if (cap < 1) cap = 1;
     if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;
-    if (ns > 256) ns = 256;
+    if (ns > 1024) ns = 1024;
   }
   *nsplit = (int)ns;
   *waves = w;
+  *hb = h;
 }
 
 int decode_num_splits(int batch, int hkv, int max_pages) {
-  int ns, w;
-  decode_plan(batch, hkv, max_pages, &ns, &w);
+  int ns, w, hb;
+  decode_plan(batch, hkv, max_pages, &ns, &w, &hb);
   return ns;
 }
 
-static size_t partial_bytes(int batch, int hq, int nsplit, bool with_acc) {
+// Workspace of a split launch: the partials, (m, l) for every (row, q head, split) then acc.
+size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc) {
   if (nsplit <= 1) return 0;
   const size_t per = (with_acc ? kHeadDim : 0) + 2;
-  return (size_t)batch * hq * nsplit * per * sizeof(float);
+  return ((size_t)batch * hq * nsplit * per * sizeof(float) + 255) & ~(size_t)255;
 }
 
 // Shared validation + launch used by the attention and the scorer entry points.
@@ -481,6 +544,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
     return set_error(DELTA_ERR_INVALID, "%s: num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", who, hq, hkv);
   const int G = hq / hkv;
   if (G > kMaxGroup) return set_error(DELTA_ERR_INVALID, "%s: group size %d > %d unsupported", who, G, kMaxGroup);
+  if (hkv > kMaxWaves) return set_error(DELTA_ERR_INVALID, "%s: num_kv_heads %d > %d unsupported", who, hkv, kMaxWaves);
   if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
   if (!q || !kv_cache || !kv_indptr || !kv_indices || !kv_last_page_len)
     return set_error(DELTA_ERR_INVALID, "%s: null input pointer", who);
@@ -517,17 +581,17 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.hq = hq;
   a.hkv = hkv;
   int waves;
-  decode_plan(batch, hkv, max_pages, &a.nsplit, &waves);
+  decode_plan(batch, hkv, max_pages, &a.nsplit, &waves, &a.hb);
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;
 
   const bool with_acc = mode != kScoreOnly;
-  const size_t need = partial_bytes(batch, hq, a.nsplit, with_acc);
+  const size_t need = decode_workspace_bytes(batch, hq, a.nsplit, with_acc);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
       return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
-    if ((uintptr_t)workspace & 15u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
+    if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
     float *ws = (float *)workspace;
     a.part_ml = ws;
     a.part_acc = ws + (size_t)batch * hq * a.nsplit * 2;
@@ -540,20 +604,17 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   else
     launch_split_g<DELTA_FP16>(a, G, waves, mode, stream);
   int rc = check_launch(who);
-  if (rc) return rc;
-  if (a.nsplit > 1) {
-    if (with_acc) {
-      if (dtype == DELTA_BF16)
-        hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
-      else
-        hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
-    } else {
-      const int n = batch * hq;
-      hipLaunchKernelGGL(decode_merge_lse_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a, G);
-    }
-    rc = check_launch(who);
+  if (rc || a.nsplit == 1) return rc;
+  if (with_acc) {
+    if (dtype == DELTA_BF16)
+      hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hkv), dim3(256), 0, stream, a, G);
+    else
+      hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hkv), dim3(256), 0, stream, a, G);
+  } else {
+    const int n = batch * hq;
+    hipLaunchKernelGGL(decode_merge_lse_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a, G);
   }
-  return rc;
+  return check_launch(who);
 }
 
 }  // namespace delta
@@ -565,7 +626,7 @@ extern "C" DELTA_EXPORT int delta_decode_num_splits(int batch, int num_kv_heads,
 extern "C" DELTA_EXPORT size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                                                   int max_pages_per_row) {
   const int ns = delta::decode_num_splits(batch, num_kv_heads, max_pages_per_row);
-  return delta::partial_bytes(batch, num_qo_heads, ns, true);
+  return delta::decode_workspace_bytes(batch, num_qo_heads, ns, true);
 }
 
 extern "C" DELTA_EXPORT int delta_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,

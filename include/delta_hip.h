@@ -24,7 +24,7 @@
  *     (pages_b - 1) * 16 + last_page_len_b tokens;
  *   - kernels never allocate, never synchronise and never read host memory, so
  *     every call can be recorded in a hipGraph; caller-provided workspaces are
- *     sized by the *_workspace_bytes queries;
+ *     sized by the *_workspace_bytes queries and 256-byte aligned;
  *   - out-of-range page ids / indptr entries are masked (the kernel never
  *     faults on a bad table, it drops the offending pages);
  *   - return 0 on success; otherwise a non-zero code and delta_last_error()
@@ -70,7 +70,8 @@ int delta_abi_version(void);
  * of pages_b over the rows. */
 int delta_decode_num_splits(int batch, int num_kv_heads, int max_pages_per_row);
 
-/* Bytes of workspace delta_paged_decode needs (split-K partials). */
+/* Bytes of workspace delta_paged_decode needs: 0 when the shape runs unsplit,
+ * else the split-K partials. */
 size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                           int max_pages_per_row);
 

@@ -51,17 +51,25 @@ def test_no_undeclared_exports(lib):
 def test_queries_without_gpu(lib):
     assert lib.delta_abi_version() == 100
     assert lib.delta_last_error() == b""
-    # split heuristic: deterministic, >= 1, and >= 2 pages per wave
-    # config 3: 256 (row, head) pairs fill the chip with 16-wave blocks -> no split-K
-    assert lib.delta_decode_num_splits(32, 8, 128) == 1
-    assert lib.delta_decode_num_splits(32, 8, 513) == 1
+    # split heuristic: deterministic, >= 1, and >= 2 pages per wave.
+    # Page-major blocks (Hkv heads x R waves = 16) split up to 4096 waves in total;
+    # head-major blocks (one kv head, 16 waves) when batch*Hkv >= 256 and
+    # batch*Hkv*max_pages <= 65536 never split.
+    assert lib.delta_decode_num_splits(32, 8, 128) == 1        # config 3 subset: head-major
+    assert lib.delta_decode_num_splits(64, 4, 128) == 1        # head-major
+    assert lib.delta_decode_num_splits(32, 8, 513) == 8        # config 3 full: page-major, 256 blocks
     assert lib.delta_decode_num_splits(1024, 8, 2048) == 1
-    assert lib.delta_decode_num_splits(8, 8, 128) == 4        # config 2: 64 pairs
-    assert lib.delta_decode_num_splits(4, 4, 4096) == 16      # config 4: 16 pairs
-    assert lib.delta_decode_num_splits(4, 4, 256) == 8        # >= 2 pages per wave
+    assert lib.delta_decode_num_splits(8, 8, 128) == 32        # config 2
+    assert lib.delta_decode_num_splits(4, 4, 4096) == 64       # config 4: R = 4
+    assert lib.delta_decode_num_splits(4, 4, 256) == 32        # >= 2 pages per wave
     assert lib.delta_decode_num_splits(1, 8, 4) == 1
+    assert lib.delta_paged_decode_workspace_bytes(1024, 32, 8, 2048) == 0
     assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 128) == 0
-    assert lib.delta_paged_decode_workspace_bytes(8, 32, 8, 128) == 8 * 32 * 4 * 130 * 4
+    # partials (m, l, acc[128]) per (row, q head, split)
+    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 130 * 4
+    assert lib.delta_page_score_workspace_bytes(32, 32) == 32 * 32 * 4
+    assert lib.delta_page_score_kv_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 2 * 4 + 32 * 32 * 4
+    assert lib.delta_page_score_kv_workspace_bytes(1024, 32, 8, 2048) == 1024 * 32 * 4
 
 
 def test_argument_errors_reported_without_launch(lib):

@@ -27,6 +27,10 @@ def cases():
         "ragged_g1": lambda: make_case(batch=5, hq=8, hkv=8, kv_lens=[1, 15, 16, 17, 300], seed=3, k=4, L=2),
         "ragged_g8_trailing": lambda: make_case(batch=4, hq=16, hkv=2, kv_lens=[32, 48, 7, 129], seed=4,
                                                 k=3, L=1, trailing_empty_page=True, dtype=torch.float16),
+        # 36 rows x 8 kv heads >= 256 blocks and <= 65536 page-heads: the head-major mapping
+        "head_major_ragged_g2": lambda: make_case(batch=36, hq=16, hkv=8,
+                                                  kv_lens=[1 + (37 * i) % 900 for i in range(36)], seed=5,
+                                                  page_order="shuffle", k=8, L=2),
     }
 
 

@@ -162,6 +162,30 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
     return res
 
 
+def copy_calibration(torch, mib: int = 256, reps: int = 8):
+    """A plain device copy of known size (``mib`` MiB read + ``mib`` MiB written per launch).
+
+    Run under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` beside the hot-path kernels, it
+    gives the factor between those counters and real bytes on this GPU."""
+    n = mib * (1 << 20) // 2
+    src = torch.randn(n, device="cuda:0", dtype=torch.float32).to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    dst.copy_(src)
+    s.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) * 1e3 / reps
+    nbytes = 2 * n * 2
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"us": round(us, 2), "bytes": nbytes, "GB_s": round(nbytes / us / 1e3, 1),
+            "what": f"torch bf16 copy of {mib} MiB (read + write)"}
+
+
 def cpu_baseline(torch, sample_rows: int = 2):
     """Oracle (PyTorch CPU, fp32) timing of the same step, composed from per-op timings.
 
@@ -239,6 +263,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-full-compare", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=48)
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the per-kernel roofline loop and a copy of known size (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -250,6 +276,13 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     torch.manual_seed(0)
+    if args.kernels_only:
+        kern = kernel_roofline(torch, args.kernel_reps)
+        kern["copy_calibration"] = copy_calibration(torch)
+        for k, v in kern.items():
+            log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s")
+        print(json.dumps({"kernels": kern}), flush=True)
+        return
     budget = args.warmup + args.steps + 16
     if not args.no_full_compare:
         budget += args.warmup + args.steps

@@ -115,15 +115,24 @@ __device__ __forceinline__ float rows4_sum(float v) {
 
 // One (row, split, group of hb kv heads) per block; R = blockDim/64/hb waves per head take the
 // split's pages round robin.
-//   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows (lane%16 = token,
-//         lane/16 picks d in [32s + 8c, +8) at step s), B = the group's query rows (zero padded
-//         to 16 columns).  D puts tokens 4c..4c+3 of head g = lane%16 in lane (c, g).
+//   q.K : v_mfma_f32_16x16x32, one per (8-token half f, 64-d half sp) of the page.  A row
+//         i = 2u + e is token 8f + u restricted to d in 64 sp + 32 e + [0, 32): lane (c, t)
+//         loads K[8f + t/2][64 sp + 32 (t%2) + 8c, +8), so one load instruction covers 8 token
+//         rows x 128 contiguous bytes (whole cache lines; a 16-row x 64-byte pattern costs
+//         ~10% of HBM bandwidth).  B column g < 8 holds q_g[64 sp + 8c, +8) and column 8 + g
+//         holds q_g[64 sp + 32 + 8c, +8), so D[2u][g] + D[2u + 1][8 + g] = q_g . K[8f + u]
+//         over the 64 d of sp: one DPP row rotate by 8 joins the two halves.  Lane (c, g)
+//         ends with tokens tok(r) = 8 (r/2) + 2c + r%2, r = 0..3, of head g.
 //   softmax: per lane 4 tokens of one head; row reductions are 3 in-lane ops + 2 permlane swaps.
-//   P.V : v_mfma_f32_16x16x16 -- A = P (already in A layout: row g = lane%16, k = tokens 4c..),
-//         B = V read back from a padded LDS tile with ds_read_b64_tr_b16 (lane (c, j) gets
-//         V[4c..4c+3][16n + j]), D = O[g = 4c + r][d = 16n + lane%16].
+//   P.V : v_mfma_f32_16x16x16 -- A = P (row g = lane%16, k = 4c + r <-> token tok(r)),
+//         B = V from a padded LDS tile whose row 4c + r holds token tok(r), read with
+//         ds_read_b64_tr_b16 (lane (c, j) gets tile rows 4c..4c+3 at d = 16n + j),
+//         D = O[g = 4c + r][d = 16n + lane%16].
 template <int DT, int G, bool WITH_V, bool WITH_DUMP>
 __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
+  // No FMA contraction: every instantiation (with or without the dump) rounds the softmax
+  // arguments identically, so P -- rounded to the KV dtype for the P.V MFMA -- is the same.
+#pragma clang fp contract(off)
   using E = Elem<DT>;
   using M16 = Mfma16<DT>;
 
@@ -146,20 +155,23 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   const int j0 = split * pps;
   const int j1 = min(ri.np, j0 + pps);
 
-  // Query fragment (B operand of q.K): column g = t, d = 32s + 8c + [0, 8).
-  u32x4 qf[4];
-  if (t < G) {
-    const uint16_t *qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + t) * a.q_stride_h + 8 * c;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = ld128(qp + 32 * s);
+  // Query fragments (B operand of q.K) for the two 64-d halves sp: column t holds head t % 8
+  // at d = 64 sp + 32 (t / 8) + 8c + [0, 8); zero for heads past the group.
+  u32x4 qf[2];
+  if ((t & 7) < G) {
+    const uint16_t *qp = a.q + (int64_t)b * a.q_stride_b + (int64_t)(h * G + (t & 7)) * a.q_stride_h +
+                         32 * (t >> 3) + 8 * c;
+    qf[0] = ld128(qp);
+    qf[1] = ld128(qp + 64);
   } else {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
+    qf[0] = qf[1] = u32x4{0u, 0u, 0u, 0u};
   }
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
-  const int64_t k_off = (int64_t)t * row_elems + 8 * c;                        // + 32 s
+  const int64_t k_off = (int64_t)(t >> 1) * row_elems + 32 * (t & 1) + 8 * c;  // + k_step(s)
+  // K fragment s covers tokens 8 (s / 2) + [0, 8) and d half sp = s % 2.
+  auto k_step = [&](int s) -> int64_t { return (int64_t)(s >> 1) * 8 * row_elems + 64 * (s & 1); };
   const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;  // + 4 i rows
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem) + wave * kVTile;           // this wave's V tile
   // Logits staged per wave for kDumpSlots pages, then written out together: on gfx9 a
@@ -190,44 +202,60 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     return a.kv + (int64_t)(pid < 0 ? 0 : pid) * page_elems + (int64_t)h * kHeadDim;
   };
 
-  // Chunks of up to 64 pages: one id load (and one pipeline drain) per chunk.
-  for (int c0 = 0; c0 < count; c0 += 64) {
-    const int cn = count - c0 < 64 ? count - c0 : 64;
-    const int ids = load_ids(c0);
-    int pid = __builtin_amdgcn_readlane(ids, 0);
+  // Chunks of up to 64 pages: one id load per chunk, the next chunk's ids loaded a chunk ahead.
+  // The next page's K and V are always in flight; the wave's last page issues no load (a
+  // repeated streaming load would miss and cost a page of HBM traffic).
+  int ids = count > 0 ? load_ids(0) : -1;
+  int pid = __builtin_amdgcn_readlane(ids, 0);
+  u32x4 kf[4], vf[4];
+  if (count > 0) {
     const uint16_t *base = page_ptr(pid);
-    u32x4 kf[4], vf[4];
     // Issue order K then V, as in the loop body, so the loop's waits can stay partial.
 #pragma unroll
-    for (int s = 0; s < 4; ++s) kf[s] = ld128(base + k_off + 32 * s);
+    for (int s = 0; s < 4; ++s) kf[s] = ld128_stream(base + k_off + k_step(s));
     __builtin_amdgcn_sched_barrier(0);
     if (WITH_V) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vf[i] = ld128(base + v_off + (int64_t)(4 * i) * row_elems);
+      for (int i = 0; i < 4; ++i) vf[i] = ld128_stream(base + v_off + (int64_t)(4 * i) * row_elems);
     }
     __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int c0 = 0; c0 < count; c0 += 64) {
+    const int cn = count - c0 < 64 ? count - c0 : 64;
+    const int ids_next = c0 + 64 < count ? load_ids(c0 + 64) : -1;
     uint32_t okmask = 0;  // dump slots holding a valid page
     for (int it = 0; it < cn; ++it) {
       const int j = first + R * (c0 + it);
       const bool ok = pid >= 0;
-      // The next page (or this one again on the chunk's last iteration: an L2 hit, keeps the
-      // loads unconditional).
-      const int pidn = __builtin_amdgcn_readlane(ids, it + 1 < cn ? it + 1 : it);
+      const bool more = c0 + it + 1 < count;
+      const int pidn = it + 1 < cn ? __builtin_amdgcn_readlane(ids, it + 1) : __builtin_amdgcn_readlane(ids_next, 0);
       const uint16_t *nbase = page_ptr(pidn);
 
-      f32x4 S = {0.f, 0.f, 0.f, 0.f};
+      f32x4 S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
+      S0 = E::mfma(kf[0], qf[0], S0);
+      S1 = E::mfma(kf[2], qf[0], S1);
+      S0 = E::mfma(kf[1], qf[1], S0);
+      S1 = E::mfma(kf[3], qf[1], S1);
+      if (more) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) S = E::mfma(kf[s], qf[s], S);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kf[s] = ld128(nbase + k_off + 32 * s);
+        for (int s = 0; s < 4; ++s) kf[s] = ld128_stream(nbase + k_off + k_step(s));
+      }
 
-      const int tok0 = j * kPageSize + 4 * c;
+      // Join the d halves: q_g . K[tok(r)] = D[rows 2u, 2u + 1] of columns g and 8 + g.
+      const float S[4] = {S0[0] + dpp_f<0x128>(S0[1]), S0[2] + dpp_f<0x128>(S0[3]),
+                          S1[0] + dpp_f<0x128>(S1[1]), S1[2] + dpp_f<0x128>(S1[3])};
+      const int tok0 = j * kPageSize + 2 * c;  // tok(r) = tok0 + 8 (r / 2) + r % 2
       float x[4], p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = (ok && tok0 + r < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
+      for (int r = 0; r < 4; ++r)
+        x[r] = (ok && tok0 + 8 * (r >> 1) + (r & 1) < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
       if (WITH_DUMP) {
         const int slot = it % kDumpSlots;
-        if (t < G) *reinterpret_cast<f32x4 *>(dbuf + (slot * G + t) * kPageSize + 4 * c) = f32x4{x[0], x[1], x[2], x[3]};
+        if (t < G) {
+          float *dl = dbuf + (slot * G + t) * kPageSize + 2 * c;
+          *reinterpret_cast<float2 *>(dl) = float2{x[0], x[1]};
+          *reinterpret_cast<float2 *>(dl + 8) = float2{x[2], x[3]};
+        }
         okmask |= (ok ? 1u : 0u) << slot;
         if (slot == kDumpSlots - 1 || it + 1 == cn) {
           // Write the staged pages: 4 lanes per (page, head) run of 16 logits.
@@ -272,16 +300,20 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
 
       if (WITH_V) {
         // Stage V; rows past kv_len (and all rows of an invalid page) are zeroed by mask, since
-        // they may hold NaN/Inf and meet p = 0.
+        // they may hold NaN/Inf and meet p = 0.  Token 4i + c goes to tile row
+        // 8 (i % 2) + 4 (c / 2) + 2 (i / 2) + c % 2, the row whose k slot holds its p.
         const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
           const u32x4 w = vf[i] & u32x4{keep, keep, keep, keep};
-          st128(vt + (4 * i + c) * kVStride + 8 * t, w);
+          const int trow = 8 * (i & 1) + 4 * (c >> 1) + 2 * (i >> 1) + (c & 1);
+          st128(vt + trow * kVStride + 8 * t, w);
         }
+        if (more) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vf[i] = ld128(nbase + v_off + (int64_t)(4 * i) * row_elems);
+          for (int i = 0; i < 4; ++i) vf[i] = ld128_stream(nbase + v_off + (int64_t)(4 * i) * row_elems);
+        }
 
         // Rescale the accumulators only when some head's running max moved.
         if (__ballot(alpha != 1.f)) {
@@ -304,6 +336,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       }
       pid = pidn;
     }
+    ids = ids_next;
   }
 
   // Merge the block's waves in LDS (the V tiles are dead once every wave left the loop).

@@ -41,8 +41,7 @@ struct DecodeArgs {
   float *lse;
   float *dump;
   int64_t dump_stride_b, dump_stride_h;
-  int dump_cap;     // tokens per dump row the caller guarantees (max_pages_per_row * 16)
-  int dump_vec;     // dump rows are 16-byte aligned: 4 tokens per store
+  int dump_pages;   // pages per dump row the caller guarantees (max_pages_per_row)
   float *part_acc;  // [batch][hkv][nsplit][G][128]
   float *part_ml;   // [batch][hkv][nsplit][G][2]  (m in log2 units, l)
   int batch, hq, hkv, nsplit;
@@ -98,6 +97,15 @@ struct Mfma16<DELTA_FP16> {
 
 typedef short s4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s4_t lds_s4_t;
+
+// Pages of logits a wave stages in LDS before writing them out.  Interleaving the dump's HBM
+// writes with the K/V read stream costs far more than their bandwidth share, so the scorer
+// (no V tiles in LDS) stages 32 / 16 pages -- a whole split at the usual launch shapes, one
+// write burst at the end; the planner (V tiles beside) stages 16 / 8.
+template <int G, bool WITH_V>
+constexpr int dump_slots() {
+  return WITH_V ? (G <= 4 ? 16 : 8) : (G <= 4 ? 32 : 16);
+}
 
 // max / sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950 permlane swaps.
 __device__ __forceinline__ float rows4_max(float v) {
@@ -174,10 +182,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   auto k_step = [&](int s) -> int64_t { return (int64_t)(s >> 1) * 8 * row_elems + 64 * (s & 1); };
   const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;  // + 4 i rows
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem) + wave * kVTile;           // this wave's V tile
-  // Logits staged per wave for kDumpSlots pages, then written out together: on gfx9 a
-  // vector store pending beside loads makes the next load wait drain the whole queue, so
-  // stores are batched instead of issued every page.
-  constexpr int kDumpSlots = G <= 4 ? 16 : 8;
+  // Logits staged per wave for a window of kDumpSlots pages, then written out together
+  // (flush_window) at the end of the window's last iteration.
+  constexpr int kDumpSlots = dump_slots<G, WITH_V>();
   float *dbuf = reinterpret_cast<float *>(smem + (WITH_V ? nw * kVTile / 2 : 0)) + wave * (kDumpSlots * G * kPageSize);
 
   float m = -INFINITY, l = 0.f;  // running stats of head g = t
@@ -205,6 +212,41 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   // Chunks of up to 64 pages: one id load per chunk, the next chunk's ids loaded a chunk ahead.
   // The next page's K and V are always in flight; the wave's last page issues no load (a
   // repeated streaming load would miss and cost a page of HBM traffic).
+  // Staged logits of one window: 4 lanes per (page, head) run of 16 logits, whole pages only
+  // (positions past kv_len hold -inf, as the reference's -inf-filled buffer does).
+  uint32_t okmask = 0;  // window slots holding a valid page
+  // Lane roles in a flush: one (slot, head, quarter) f32x4 per store instruction, kSpi slots
+  // per instruction; only two lane-constant 32-bit offsets stay live across the page loop.
+  constexpr int kSpi = 64 / (4 * G);                      // slots per store instruction
+  constexpr int kFlushInstr = (kDumpSlots + kSpi - 1) / kSpi;
+  const int f_sl = lane / (4 * G);                        // slot within an instruction
+  const int f_g = (lane % (4 * G)) >> 2, f_qq = lane & 3;
+  const bool f_lane = f_sl < kSpi;
+  const uint32_t f_lds = (uint32_t)(((f_sl * G + f_g) * kPageSize + 4 * f_qq) * sizeof(float));
+  const uint32_t f_dst = (uint32_t)(((int64_t)f_g * a.dump_stride_h + (int64_t)f_sl * R * kPageSize + 4 * f_qq) *
+                                    sizeof(float));
+  float *const dump_row = WITH_DUMP ? a.dump + (int64_t)b * a.dump_stride_b + (int64_t)h * G * a.dump_stride_h
+                                    : nullptr;
+  auto flush_window = [&](int gi0, int nslots) {
+#pragma unroll
+    for (int q = 0; q < kFlushInstr; ++q) {
+      const int sl = q * kSpi + f_sl;
+      const int jp = first + R * (gi0 + sl);
+      if (f_lane && sl < nslots && ((okmask >> sl) & 1u) && jp < a.dump_pages) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(dbuf) + f_lds +
+                                                         q * kSpi * G * kPageSize * sizeof(float));
+        // uniform part: first page of instruction q's slots
+        const int jq = first + R * (gi0 + q * kSpi);
+        float *dst = reinterpret_cast<float *>(reinterpret_cast<char *>(dump_row + (int64_t)jq * kPageSize) + f_dst);
+        dst[0] = v[0];
+        dst[1] = v[1];
+        dst[2] = v[2];
+        dst[3] = v[3];
+      }
+    }
+    okmask = 0;
+  };
+
   int ids = count > 0 ? load_ids(0) : -1;
   int pid = __builtin_amdgcn_readlane(ids, 0);
   u32x4 kf[4], vf[4];
@@ -223,7 +265,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   for (int c0 = 0; c0 < count; c0 += 64) {
     const int cn = count - c0 < 64 ? count - c0 : 64;
     const int ids_next = c0 + 64 < count ? load_ids(c0 + 64) : -1;
-    uint32_t okmask = 0;  // dump slots holding a valid page
     for (int it = 0; it < cn; ++it) {
       const int j = first + R * (c0 + it);
       const bool ok = pid >= 0;
@@ -231,14 +272,34 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       const int pidn = it + 1 < cn ? __builtin_amdgcn_readlane(ids, it + 1) : __builtin_amdgcn_readlane(ids_next, 0);
       const uint16_t *nbase = page_ptr(pidn);
 
+      if (WITH_V) {
+        // Stage this page's V (loaded one iteration ago) before anything else, so the wait at
+        // the top of the iteration is the only one on loaded data and the registers are free
+        // for the next page's V below.  Rows past kv_len (and all rows of an invalid page) are
+        // zeroed by mask, since they may hold NaN/Inf and meet p = 0.  Token 4i + c goes to
+        // tile row 8 (i % 2) + 4 (c / 2) + 2 (i / 2) + c % 2, the row whose k slot holds its p.
+        const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
+          const u32x4 w = vf[i] & u32x4{keep, keep, keep, keep};
+          const int trow = 8 * (i & 1) + 4 * (c >> 1) + 2 * (i >> 1) + (c & 1);
+          st128(vt + trow * kVStride + 8 * t, w);
+        }
+      }
       f32x4 S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
       S0 = E::mfma(kf[0], qf[0], S0);
       S1 = E::mfma(kf[2], qf[0], S1);
       S0 = E::mfma(kf[1], qf[1], S0);
       S1 = E::mfma(kf[3], qf[1], S1);
+      // The next page's K and V are in flight for the rest of the iteration.
       if (more) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) kf[s] = ld128_stream(nbase + k_off + k_step(s));
+        if (WITH_V) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vf[i] = ld128_stream(nbase + v_off + (int64_t)(4 * i) * row_elems);
+        }
       }
 
       // Join the d halves: q_g . K[tok(r)] = D[rows 2u, 2u + 1] of columns g and 8 + g.
@@ -249,36 +310,15 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         x[r] = (ok && tok0 + 8 * (r >> 1) + (r & 1) < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
+      const int slot = (c0 + it) % kDumpSlots;
       if (WITH_DUMP) {
-        const int slot = it % kDumpSlots;
+        // Logits staged in LDS, one slot per page of a kDumpSlots-page window.
         if (t < G) {
           float *dl = dbuf + (slot * G + t) * kPageSize + 2 * c;
           *reinterpret_cast<float2 *>(dl) = float2{x[0], x[1]};
           *reinterpret_cast<float2 *>(dl + 8) = float2{x[2], x[3]};
         }
         okmask |= (ok ? 1u : 0u) << slot;
-        if (slot == kDumpSlots - 1 || it + 1 == cn) {
-          // Write the staged pages: 4 lanes per (page, head) run of 16 logits.
-          const int it0 = c0 + it - slot;
-          const int nseg = (slot + 1) * G;
-          for (int e = lane; e < 4 * nseg; e += 64) {
-            const int seg = e >> 2, qq = e & 3;
-            const int sl = seg / G, g = seg % G;
-            const int tk = (first + R * (it0 + sl)) * kPageSize + 4 * qq;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(dbuf + seg * kPageSize + 4 * qq);
-            float *dst = a.dump + (int64_t)b * a.dump_stride_b + (int64_t)(h * G + g) * a.dump_stride_h + tk;
-            if ((okmask >> sl) & 1u) {
-              if (tk + 3 < ri.kv_len && tk + 3 < a.dump_cap && a.dump_vec) {
-                *reinterpret_cast<f32x4 *>(dst) = v;
-              } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  if (tk + r < ri.kv_len && tk + r < a.dump_cap) dst[r] = v[r];
-              }
-            }
-          }
-          okmask = 0;
-        }
       }
       float pm = -INFINITY;
 #pragma unroll
@@ -299,22 +339,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       m = mn;
 
       if (WITH_V) {
-        // Stage V; rows past kv_len (and all rows of an invalid page) are zeroed by mask, since
-        // they may hold NaN/Inf and meet p = 0.  Token 4i + c goes to tile row
-        // 8 (i % 2) + 4 (c / 2) + 2 (i / 2) + c % 2, the row whose k slot holds its p.
-        const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
-          const u32x4 w = vf[i] & u32x4{keep, keep, keep, keep};
-          const int trow = 8 * (i & 1) + 4 * (c >> 1) + 2 * (i >> 1) + (c & 1);
-          st128(vt + trow * kVStride + 8 * t, w);
-        }
-        if (more) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) vf[i] = ld128_stream(nbase + v_off + (int64_t)(4 * i) * row_elems);
-        }
-
         // Rescale the accumulators only when some head's running max moved.
         if (__ballot(alpha != 1.f)) {
 #pragma unroll
@@ -334,6 +358,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
           acc[n] = M16::run(pa, bv, acc[n]);
         }
       }
+      // Last page of a window (or of the wave): write the window's staged logits.  The
+      // stores go out after the next page's loads, which therefore never wait behind them.
+      if (WITH_DUMP && (slot == kDumpSlots - 1 || !more)) flush_window(c0 + it - slot, slot + 1);
       pid = pidn;
     }
     ids = ids_next;
@@ -478,10 +505,11 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
   dim3 block(64 * waves);
   const size_t merge = (size_t)waves * G * (2 + kHeadDim) * sizeof(float);
   const size_t tiles = (size_t)waves * kVTile * sizeof(uint16_t);
-  const size_t dumps = (size_t)waves * (G <= 4 ? 16 : 8) * G * kPageSize * sizeof(float);
+  const size_t dumps = (size_t)waves * dump_slots<G, true>() * G * kPageSize * sizeof(float);
+  const size_t dumps_score = (size_t)waves * dump_slots<G, false>() * G * kPageSize * sizeof(float);
   const size_t sm_attn = merge > tiles ? merge : tiles;
   const size_t sm_plan = merge > tiles + dumps ? merge : tiles + dumps;
-  const size_t sm_score = dumps > (size_t)waves * G * 2 * sizeof(float) ? dumps : (size_t)waves * G * 2 * sizeof(float);
+  const size_t sm_score = dumps_score > (size_t)waves * G * 2 * sizeof(float) ? dumps_score : (size_t)waves * G * 2 * sizeof(float);
   switch (mode) {
     case kAttn:
       hipLaunchKernelGGL((paged_decode_full_kernel<DT, G>), grid, block, sm_attn, stream, a);
@@ -589,6 +617,11 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   if ((q_stride_h % 8) || (q_stride_b % 8))
     return set_error(DELTA_ERR_INVALID, "%s: q strides must be multiples of 8 elements", who);
   if (num_pages <= 0 || kv_indices_len < 0) return set_error(DELTA_ERR_INVALID, "%s: empty cache", who);
+  // The dump writer addresses a (row, kv head) block of G dump rows with 32-bit offsets.
+  if (dump && (dump_stride_b < 0 || dump_stride_h < 0 || (int64_t)(G - 1) * dump_stride_h > (int64_t)1 << 28 ||
+               ((uintptr_t)dump & 3u)))
+    return set_error(DELTA_ERR_INVALID, "%s: logits dump strides must be non-negative, 4-byte aligned and "
+                     "(G - 1) * stride_h <= 2^28", who);
   if (max_pages <= 0) max_pages = 1;
 
   DecodeArgs a;
@@ -608,8 +641,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.dump = dump;
   a.dump_stride_b = dump_stride_b;
   a.dump_stride_h = dump_stride_h;
-  a.dump_cap = max_pages * kPageSize;
-  a.dump_vec = dump && !((uintptr_t)dump & 15u) && !(dump_stride_b & 3) && !(dump_stride_h & 3);
+  a.dump_pages = max_pages;
   a.batch = batch;
   a.hq = hq;
   a.hkv = hkv;

@@ -162,6 +162,102 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
     return res
 
 
+def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
+    """Planner, score, selection and subset-attention kernels at one layer of BASELINE config
+    ``config`` (2, 4 or 5) at its full size, HIP-event timed over ``n_rot`` rotating layers.
+    Algorithmic bytes count each row's real pages (ragged rows, per-row budgets)."""
+    from delta_amd import kernels as K
+    from delta_amd.workloads import config_case
+    layers = []
+    for r in range(n_rot):
+        c = config_case(config, device="cuda:0")
+        if r:  # independent K/V and q for the rotation (same shapes and page tables)
+            c.kv_cache.normal_()
+            c.q.normal_()
+        B, hq = c.q.shape[:2]
+        mp = c.max_pages
+        dump = torch.empty((B, hq, mp * 16), device="cuda:0")
+        lse = torch.empty((B, hq), device="cuda:0")
+        K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
+                       lse=lse, logits_dump=dump)
+        scores = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+        idx, ip = K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L, k_per_row=c.k_per_row)
+        layers.append((c, dump, lse, scores, idx, ip))
+    torch.cuda.synchronize()
+    c, _, _, _, _, ip = layers[0]
+    B, hq = c.q.shape[:2]
+    hkv = c.kv_cache.shape[3]
+    esz = c.kv_cache.element_size()
+    mp = c.max_pages
+    kmax = int(c.k_per_row.max()) if c.k_per_row is not None else c.k
+    last = c.kv_last_page_len.cpu().tolist()
+    nsel = (ip[1:] - ip[:-1]).cpu().tolist()
+    npages = (c.kv_indptr[1:] - c.kv_indptr[:-1]).cpu().tolist()
+    ntok_full = sum(c.kv_lens)
+    ntok_sub = sum((n - 1) * 16 + l if n else 0 for n, l in zip(nsel, last))
+    row_kv = hkv * 128 * esz
+    qo = 2 * B * hq * 128 * esz
+
+    def timed(fn):
+        for i in range(n_rot):
+            fn(*layers[i])
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(reps):
+            fn(*layers[i % n_rot])
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / reps
+
+    res = {"shape": f"B={B}, {hq}q/{hkv}kv, {ntok_full} cached tokens ({min(c.kv_lens)}-{max(c.kv_lens)} per row), "
+                    f"{sum(nsel)} selected pages, {str(c.kv_cache.dtype).replace('torch.', '')}"}
+
+    def add(name, us, nbytes):
+        res[name] = {"us": round(us, 2), "bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
+
+    add("paged_decode_plan_kernel",
+        timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                       c.kv_last_page_len, max_pages_per_row=mp, lse=l,
+                                                       logits_dump=d)),
+        ntok_full * 2 * row_kv + qo + sum(npages) * 4 + ntok_full * hq * 4)
+    add("legacy_softmax_score_kernel",
+        timed(lambda c, d, l, s, i, p: K.page_scores_from_logits(d, c.kv_indptr, c.kv_last_page_len, mp, lse=l,
+                                                                  scores=s)),
+        ntok_full * hq * 4 + B * mp * 4)
+    add("select_pages_kernel",
+        timed(lambda c, d, l, s, i, p: K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L,
+                                                       k_per_row=c.k_per_row, out_indices=i, out_indptr=p)),
+        B * mp * 4 * 2 + sum(nsel) * 4)
+    add("paged_decode_subset_kernel",
+        timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
+                                                       max_pages_per_row=kmax, subset=True)),
+        ntok_sub * 2 * row_kv + qo + sum(nsel) * 4)
+    add("page_score_kv (standalone scorer)",
+        timed(lambda c, d, l, s, i, p: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                     c.kv_last_page_len, mp, logits_dump=d, scores=s)),
+        ntok_full * row_kv + B * hq * 128 * esz + sum(npages) * 4 + B * mp * 4)
+    del layers, c
+    torch.cuda.empty_cache()
+    return res
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE, scaled by a copy of known size); None when the summary does not list it."""
+    path = os.path.join(ROOT, "profiles", "decode_kernels_config3_roofline.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def copy_calibration(torch, mib: int = 256, reps: int = 8):
     """A plain device copy of known size (``mib`` MiB read + ``mib`` MiB written per launch).
 
@@ -262,6 +358,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-full-compare", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the kernel-level measurements at BASELINE configs 2, 4 and 5")
     ap.add_argument("--kernel-reps", type=int, default=48)
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel roofline loop and a copy of known size (for rocprofv3 --pmc runs)")
@@ -308,6 +406,20 @@ def main():
     for k, v in kern.items():
         log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s ({100 * v['frac']:.1f}% of peak)")
     dom = kern["paged_decode_subset_kernel"]
+    others = None
+    if not args.no_other_configs:
+        others = {}
+        for cfg in (2, 4, 5):
+            log(f"kernels at config {cfg}")
+            try:
+                others[f"config{cfg}"] = config_kernels(torch, cfg)
+                for k, v in others[f"config{cfg}"].items():
+                    if isinstance(v, dict):
+                        log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s ({100 * v['frac']:.1f}% of peak)")
+            except Exception as exc:  # reported in the line, never fatal for the headline number
+                others[f"config{cfg}"] = {"error": repr(exc)}
+                log(f"  failed: {exc!r}")
+            torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
@@ -331,11 +443,13 @@ def main():
                                "2048-token budget (128 pages, L=8), full layers [0,1], one hipGraph per step",
                    "batch": BATCH, "context": CONTEXT, "budget_pages": BUDGET_PAGES, "page_size": 16},
         "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": dom["frac"], "traffic": None, "kernel": "paged_decode_subset_kernel"},
+                     "frac": dom["frac"], "traffic": profiled_traffic("paged_decode_subset_kernel"),
+                     "algorithmic_bytes": dom["bytes"], "kernel": "paged_decode_subset_kernel"},
         "cpu_baseline": cpu,
         "full_cache": full,
         "speedup_vs_full_cache": round(tok_s / full["tokens_per_s"], 3) if full else None,
         "kernels": kern,
+        "kernels_other_configs": others,
     }
     print(json.dumps(line), flush=True)
 

@@ -5,12 +5,16 @@
 // BatchDumpAttentionWeights logits side-write (backend.py:175-222, 518-585).
 //
 // Work decomposition
-//   grid = (num_splits * Hkv / hb, batch); block = 16 waves = hb kv heads x R waves each.
-//   Page-major (hb = Hkv): wave w works on kv head w % Hkv and takes every R-th page of
-//   the block's split, so the Hkv waves of one page slot read all heads of the same page
-//   (its K and V are each one contiguous 16 * Hkv * 256-byte run).  Head-major (hb = 1):
-//   the 16 waves of a (row, kv head) block take its pages round robin, with no split.
-//   The choice per shape is decode_plan's.
+//   block = 16 waves = hb kv heads x R waves each.
+//   Page-major (hb = Hkv), grid = (batch * num_splits): a block takes one work unit, a chunk
+//   of up to `chunk` pages of one row; a row has clamp(ceil(pages / chunk), 1, num_splits)
+//   units and the units are packed row by row at the front of the grid, so ragged rows cost
+//   blocks in proportion to their pages (blocks past the last unit exit at once).  Wave w
+//   works on kv head w % Hkv and takes every R-th page of the unit, so the Hkv waves of one
+//   page slot read all heads of the same page (its K and V are each one contiguous
+//   16 * Hkv * 256-byte run).  Head-major (hb = 1), grid = (Hkv, batch): the 16 waves of a
+//   (row, kv head) block take its pages round robin, with no split.  The choice per shape
+//   is decode_plan's.
 //   Per page and wave (details at decode_split_body): q.K and P.V on MFMA, online
 //   softmax in the log2 domain; page ids preloaded 64 per register, the next page's
 //   K and V always in flight.
@@ -42,9 +46,11 @@ struct DecodeArgs {
   float *dump;
   int64_t dump_stride_b, dump_stride_h;
   int dump_pages;   // pages per dump row the caller guarantees (max_pages_per_row)
-  float *part_acc;  // [batch][hkv][nsplit][G][128]
-  float *part_ml;   // [batch][hkv][nsplit][G][2]  (m in log2 units, l)
+  float *part_acc;  // [unit][hkv][G][128]   (units < batch * nsplit)
+  float *part_ml;   // [unit][hkv][G][2]     (m in log2 units, l)
+  int32_t *unit_start;  // [batch]: first unit of each row (written by the row's unit 0)
   int batch, hq, hkv, nsplit;
+  int chunk;        // pages per work unit (split launches)
   int hb;           // kv heads per block (hkv: page-major, 1: head-major)
   float sm_scale;
 };
@@ -98,6 +104,43 @@ struct Mfma16<DELTA_FP16> {
 typedef short s4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s4_t lds_s4_t;
 
+// Work units of a split launch: row b has units_of(b) = clamp(ceil(pages_b / chunk), 1,
+// nsplit) of them (its last unit takes any pages past units * chunk, so a row longer than the
+// planned maximum is still covered), numbered row by row.
+__device__ __forceinline__ int units_of(const DecodeArgs &a, int b) {
+  const RowInfo r = row_info(a, b);
+  const int n = (r.np + a.chunk - 1) / a.chunk;
+  return n < 1 ? 1 : (n > a.nsplit ? a.nsplit : n);
+}
+
+// Row, split and unit count of unit u (every wave of the block computes the same answer):
+// a running inclusive scan of units_of over 64 rows at a time.  False past the last unit.
+__device__ __forceinline__ bool find_unit(const DecodeArgs &a, int u, int lane, int *row, int *split, int *nu) {
+  int base = 0;
+  for (int r0 = 0; r0 < a.batch; r0 += 64) {
+    const int r = r0 + lane;
+    const int n = r < a.batch ? units_of(a, r) : 0;
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    const int total = __shfl(incl, 63, 64);
+    if (u < base + total) {
+      const uint64_t m = __ballot(base + incl > u);
+      const int l = __builtin_ctzll(m);
+      const int start = base + __shfl(incl - n, l, 64);
+      *row = r0 + l;
+      *split = u - start;
+      *nu = __shfl(n, l, 64);
+      return true;
+    }
+    base += total;
+  }
+  return false;
+}
+
 // Pages of logits a wave stages in LDS before writing them out.  Interleaving the dump's HBM
 // writes with the K/V read stream costs far more than their bandwidth share, so the scorer
 // (no V tiles in LDS) stages 32 / 16 pages -- a whole split at the usual launch shapes, one
@@ -148,9 +191,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   const int hb = a.hb;
   const int R = nw / hb;  // waves per kv head
   const int hgroups = a.hkv / hb;
-  const int split = blockIdx.x / hgroups;
   const int head0 = (blockIdx.x % hgroups) * hb;
-  const int b = blockIdx.y;
   const int wave = uniform(threadIdx.x >> 6);
   const int h = head0 + wave % hb;
   const int rslot = wave / hb;
@@ -158,10 +199,21 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   const int c = lane >> 4;
   const int t = lane & 15;
 
-  const RowInfo ri = row_info(a, b);
-  const int pps = (ri.np + a.nsplit - 1) / a.nsplit;
-  const int j0 = split * pps;
-  const int j1 = min(ri.np, j0 + pps);
+  int b, split = 0, j0 = 0, j1;
+  RowInfo ri;
+  const int unit = blockIdx.x;
+  if (a.nsplit > 1) {
+    int nu;
+    if (!find_unit(a, unit, lane, &b, &split, &nu)) return;  // past the last unit: whole block
+    ri = row_info(a, b);
+    j0 = split * a.chunk;
+    j1 = split == nu - 1 ? ri.np : min(ri.np, j0 + a.chunk);
+    if (split == 0 && threadIdx.x == 0) a.unit_start[b] = unit;
+  } else {
+    b = blockIdx.y;
+    ri = row_info(a, b);
+    j1 = ri.np;
+  }
 
   // Query fragments (B operand of q.K) for the two 64-d halves sp: column t holds head t % 8
   // at d = 64 sp + 32 (t / 8) + 8c + [0, 8); zero for heads past the group.
@@ -412,7 +464,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       if (dd == 0 && a.lse != nullptr)
         a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
     } else {
-      const int64_t pidx = (((int64_t)b * a.hkv + hh) * a.nsplit + split) * G + g;
+      const int64_t pidx = ((int64_t)unit * a.hkv + hh) * G + g;
       if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
       if (dd == 0) {
         a.part_ml[pidx * 2 + 0] = M;
@@ -447,7 +499,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArg
   decode_split_body<DT, G, false, true>(a, smem);
 }
 
-// Combines the split partials of one (row, kv head): for each of its G query rows and d,
+// Combines the unit partials of one (row, kv head): for each of its G query rows and d,
 //   o = sum_s A_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),  lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2,
 // accumulated online (running max) so every partial is loaded in a single pass.
 template <int DT>
@@ -455,14 +507,15 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a, int G) 
   using E = Elem<DT>;
   const int b = blockIdx.x / a.hkv;
   const int h = blockIdx.x % a.hkv;
+  const int u0 = a.unit_start[b];
+  const int nu = units_of(a, b);
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
     const int g = idx / kHeadDim;
     const int dd = idx % kHeadDim;
-    const int64_t base = ((int64_t)b * a.hkv + h) * a.nsplit * G + g;
     float M = -INFINITY, L = 0.f, A = 0.f;
 #pragma unroll 4
-    for (int s = 0; s < a.nsplit; ++s) {
-      const int64_t pidx = base + (int64_t)s * G;
+    for (int s = 0; s < nu; ++s) {
+      const int64_t pidx = ((int64_t)(u0 + s) * a.hkv + h) * G + g;
       const float ms = a.part_ml[pidx * 2], ls = a.part_ml[pidx * 2 + 1], as = a.part_acc[pidx * kHeadDim + dd];
       const float mn = fmaxf(M, ms);
       const float mr = mn == -INFINITY ? 0.f : mn;
@@ -483,11 +536,12 @@ __global__ void __launch_bounds__(256) decode_merge_lse_kernel(DecodeArgs a, int
   if (idx >= a.batch * a.hq) return;
   const int b = idx / a.hq;
   const int hq = idx % a.hq;
-  const int64_t base = ((int64_t)b * a.hkv + hq / G) * a.nsplit * G + hq % G;
+  const int u0 = a.unit_start[b];
+  const int nu = units_of(a, b);
   float M = -INFINITY, L = 0.f;
 #pragma unroll 4
-  for (int s = 0; s < a.nsplit; ++s) {
-    const int64_t pidx = base + (int64_t)s * G;
+  for (int s = 0; s < nu; ++s) {
+    const int64_t pidx = ((int64_t)(u0 + s) * a.hkv + hq / G) * G + hq % G;
     const float ms = a.part_ml[pidx * 2], ls = a.part_ml[pidx * 2 + 1];
     const float mn = fmaxf(M, ms);
     const float mr = mn == -INFINITY ? 0.f : mn;
@@ -501,7 +555,7 @@ enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
 
 template <int DT, int G>
 void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
-  dim3 grid(a.nsplit * (a.hkv / a.hb), a.batch);
+  dim3 grid = a.nsplit > 1 ? dim3(a.batch * a.nsplit) : dim3(a.hkv / a.hb, a.batch);
   dim3 block(64 * waves);
   const size_t merge = (size_t)waves * G * (2 + kHeadDim) * sizeof(float);
   const size_t tiles = (size_t)waves * kVTile * sizeof(uint16_t);
@@ -553,10 +607,13 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
 //     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
 //     faster page-major gather repays the merge.
+//   Work units hold at most kMaxChunk pages (64 per wave at Hkv = 8), so a ragged batch is cut
+//   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
 constexpr int64_t kHeadMajorPageHeads = 65536;
+constexpr int kMaxChunk = 128;
 
-void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int *hb) {
+void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int *hb, int *chunk) {
   int h = hkv;
   if ((int64_t)batch * hkv >= kHeadMajorPairs && (int64_t)batch * hkv * max_pages <= kHeadMajorPageHeads) h = 1;
   int R = h > 0 ? kMaxWaves / h : 1;
@@ -572,22 +629,30 @@ void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int
     if (ns < 1) ns = 1;
     if (ns > 1024) ns = 1024;
   }
+  int64_t ch = max_pages > 0 ? ceil_div(max_pages, ns) : 1;
+  if (ns > 1 && ch > kMaxChunk) {
+    ch = kMaxChunk;
+    ns = ceil_div(max_pages, ch);
+  }
   *nsplit = (int)ns;
   *waves = w;
   *hb = h;
+  *chunk = (int)(ch < 1 ? 1 : ch);
 }
 
 int decode_num_splits(int batch, int hkv, int max_pages) {
-  int ns, w, hb;
-  decode_plan(batch, hkv, max_pages, &ns, &w, &hb);
+  int ns, w, hb, ch;
+  decode_plan(batch, hkv, max_pages, &ns, &w, &hb, &ch);
   return ns;
 }
 
-// Workspace of a split launch: the partials, (m, l) for every (row, q head, split) then acc.
+// Workspace of a split launch: (m, l) for every (unit, q head), then acc, then each row's
+// first unit.  At most batch * nsplit units.
 size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc) {
   if (nsplit <= 1) return 0;
   const size_t per = (with_acc ? kHeadDim : 0) + 2;
-  return ((size_t)batch * hq * nsplit * per * sizeof(float) + 255) & ~(size_t)255;
+  const size_t parts = ((size_t)batch * hq * nsplit * per * sizeof(float) + 255) & ~(size_t)255;
+  return parts + (((size_t)batch * sizeof(int32_t) + 255) & ~(size_t)255);
 }
 
 // Shared validation + launch used by the attention and the scorer entry points.
@@ -646,11 +711,14 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.hq = hq;
   a.hkv = hkv;
   int waves;
-  decode_plan(batch, hkv, max_pages, &a.nsplit, &waves, &a.hb);
+  decode_plan(batch, hkv, max_pages, &a.nsplit, &waves, &a.hb, &a.chunk);
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;
+  a.unit_start = nullptr;
 
+  if (a.nsplit > 1 && a.hb != a.hkv)
+    return set_error(DELTA_ERR_INVALID, "%s: split launch planned with %d of %d kv heads per block", who, a.hb, a.hkv);
   const bool with_acc = mode != kScoreOnly;
   const size_t need = decode_workspace_bytes(batch, hq, a.nsplit, with_acc);
   if (need > 0) {
@@ -658,8 +726,11 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
       return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
     if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
     float *ws = (float *)workspace;
+    const size_t per = (with_acc ? kHeadDim : 0) + 2;
     a.part_ml = ws;
     a.part_acc = ws + (size_t)batch * hq * a.nsplit * 2;
+    a.unit_start = (int32_t *)((char *)workspace +
+                               ((((size_t)batch * hq * a.nsplit * per * sizeof(float)) + 255) & ~(size_t)255));
   }
   if (mode == kScoreOnly && !lse && a.nsplit > 1)
     return set_error(DELTA_ERR_INVALID, "%s: scorer needs an lse buffer", who);

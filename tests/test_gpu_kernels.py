@@ -231,6 +231,40 @@ def test_selective_step_end_to_end(name):
             assert planted_phys <= sel, f"row {b}: planted-page recall < 100%"
 
 
+@pytest.mark.parametrize("plan_pages", ["exact", "short"])
+def test_ragged_work_units(plan_pages):
+    """Rows of very different lengths in one split launch: each row is cut into work units of
+    at most 128 pages, packed at the front of the grid.  "short" plans for fewer pages than
+    the longest row holds: that row's last unit takes the remainder.  Attention, lse and the
+    dump must still cover every page of every row."""
+    lens = [1, 16, 17, 2500 * 16 + 3, 40, 900 * 16, 5, 3000]
+    c = make_case(batch=len(lens), hq=16, hkv=8, kv_lens=lens, seed=11, page_order="randperm", k=4, L=2)
+    g = gpu(c)
+    B, hq = c.q.shape[:2]
+    mp = c.max_pages if plan_pages == "exact" else 100
+    assert K._lib.query("delta_decode_num_splits", B, 8, mp) > 1  # a split (work-unit) launch
+    dump = torch.full((B, hq, c.max_pages * 16), 12345.0, device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    o = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                       max_pages_per_row=mp, lse=lse, logits_dump=dump)
+    o2 = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                              c.kv_last_page_len, c.sm_scale)
+    assert_attn_close(o, o_ref, "ragged units")
+    assert torch.equal(o, o2)
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
+    x_ref = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                          c.sm_scale, c.max_pages * 16)
+    d = dump.cpu()
+    written = min(mp, c.max_pages) * 16  # the dump holds max_pages_per_row pages per row
+    valid = torch.isfinite(x_ref)
+    valid[:, :, written:] = False
+    err = (d[valid] - x_ref[valid]).abs() / (1 + x_ref[valid].abs())
+    assert err.max().item() < 1e-4
+    assert torch.all(d[:, :, written:] == 12345.0)
+
+
 def test_sparse_equals_full_when_budget_covers_all():
     c = config_case(3, scale=0.25, batch=4)
     g = gpu(c)

@@ -8,7 +8,7 @@
 //   tie order unspecified; this build fixes it), positions emitted in
 //   ascending j (132-134) as physical ids from the row's block table (147-150).
 //
-// Algorithm per row (256 threads): fp32 keys map to order-preserving uint32
+// Algorithm per row (1024 threads): fp32 keys map to order-preserving uint32
 // (+0/-0 folded); a 4-pass 8-bit radix select finds the k-th largest key T and
 // how many keys equal to T are taken (r); one ordered pass then marks
 // key > T, or key == T among the first r such pages, and compacts the marked
@@ -22,8 +22,9 @@
 namespace delta {
 namespace {
 
-constexpr int kSelThreads = 256;
+constexpr int kSelThreads = 1024;  // long rows (4 k+ pages) take few key loads per thread
 constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kBins = 256;         // radix digit bins, handled by the first 4 waves
 constexpr uint32_t kKeyPosInf = 0xFF800000u;  // order_key(+inf)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -119,7 +120,7 @@ __device__ int block_prefix(bool flag, int *scratch, int *total) {
 
 __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
   __shared__ int s_scratch[kSelWaves];
-  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_hist[kBins];
   __shared__ int s_digit, s_remaining;
 
   const int b = blockIdx.x;
@@ -167,25 +168,25 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
   uint32_t prefix = 0, pmask = 0;
   int remaining = kb;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    s_hist[tid] = 0;
+    if (tid < kBins) s_hist[tid] = 0;
     __syncthreads();
     for (int j = tid; j < tp; j += kSelThreads) {
       const uint32_t key = key_of(j);
       if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
     }
     __syncthreads();
-    // Suffix sums over the 256 bins: suf[d] = #keys with digit >= d.
+    // Suffix sums over the 256 bins (thread d < 256 holds bin d): suf[d] = #keys with digit >= d.
     const int lane = tid & 63, wave = tid >> 6;
-    const int hd = (int)s_hist[tid];
+    const int hd = tid < kBins ? (int)s_hist[tid] : 0;
     int suf = hd;
     for (int off = 1; off < 64; off <<= 1) {
       const int y = __shfl_down(suf, off);
       if (lane + off < 64) suf += y;
     }
-    if (lane == 0) s_scratch[wave] = suf;
+    if (lane == 0 && tid < kBins) s_scratch[wave] = suf;
     __syncthreads();
-    for (int w = wave + 1; w < kSelWaves; ++w) suf += s_scratch[w];
-    if (suf >= remaining && suf - hd < remaining) {
+    for (int w = wave + 1; w < kBins / 64; ++w) suf += s_scratch[w];
+    if (tid < kBins && suf >= remaining && suf - hd < remaining) {
       s_digit = tid;
       s_remaining = remaining - (suf - hd);
     }

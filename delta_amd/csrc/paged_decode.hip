@@ -499,56 +499,60 @@ __global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArg
   decode_split_body<DT, G, false, true>(a, smem);
 }
 
-// Combines the unit partials of one (row, kv head): for each of its G query rows and d,
-//   o = sum_s A_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),  lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2,
-// accumulated online (running max) so every partial is loaded in a single pass.
+// Combines the unit partials of one (row, q head): thread d of the block computes
+//   M = max_s m_s,  o[d] = sum_s A_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M),
+//   lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2
+// in two passes (the maxima, then independent scaled loads), so the loads of all units are in
+// flight together instead of one online-merge step at a time.
 template <int DT>
-__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeArgs a, int G) {
+__global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
   using E = Elem<DT>;
-  const int b = blockIdx.x / a.hkv;
-  const int h = blockIdx.x % a.hkv;
+  const int b = blockIdx.x / a.hq;
+  const int hq = blockIdx.x % a.hq;
+  const int h = hq / G, g = hq % G;
+  const int dd = threadIdx.x;
   const int u0 = a.unit_start[b];
   const int nu = units_of(a, b);
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
-    const int g = idx / kHeadDim;
-    const int dd = idx % kHeadDim;
-    float M = -INFINITY, L = 0.f, A = 0.f;
-#pragma unroll 4
-    for (int s = 0; s < nu; ++s) {
-      const int64_t pidx = ((int64_t)(u0 + s) * a.hkv + h) * G + g;
-      const float ms = a.part_ml[pidx * 2], ls = a.part_ml[pidx * 2 + 1], as = a.part_acc[pidx * kHeadDim + dd];
-      const float mn = fmaxf(M, ms);
-      const float mr = mn == -INFINITY ? 0.f : mn;
-      const float co = fast_exp2(M - mr), cs = fast_exp2(ms - mr);
-      L = L * co + ls * cs;
-      A = A * co + as * cs;
-      M = mn;
-    }
-    const int hq = h * G + g;
-    a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(L > 0.f ? A / L : 0.f);
-    if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+  const int64_t stride = (int64_t)a.hkv * G;  // partial rows per unit
+  const int64_t p0 = ((int64_t)u0 * a.hkv + h) * G + g;
+  float M = -INFINITY;
+#pragma unroll 8
+  for (int s = 0; s < nu; ++s) M = fmaxf(M, a.part_ml[(p0 + s * stride) * 2]);
+  const float Mr = M == -INFINITY ? 0.f : M;
+  float L = 0.f, A = 0.f;
+#pragma unroll 8
+  for (int s = 0; s < nu; ++s) {
+    const int64_t pidx = p0 + s * stride;
+    const float sc = fast_exp2(a.part_ml[pidx * 2] - Mr);
+    L = fmaf(a.part_ml[pidx * 2 + 1], sc, L);
+    A = fmaf(a.part_acc[pidx * kHeadDim + dd], sc, A);
   }
+  a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(L > 0.f ? A / L : 0.f);
+  if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
 
-// lse-only merge (scorer path without V), one thread per (row, q head).
+// lse-only merge (scorer path without V): one 64-lane wave per (row, q head), lanes over units.
 __global__ void __launch_bounds__(256) decode_merge_lse_kernel(DecodeArgs a, int G) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (idx >= a.batch * a.hq) return;
   const int b = idx / a.hq;
   const int hq = idx % a.hq;
   const int u0 = a.unit_start[b];
   const int nu = units_of(a, b);
-  float M = -INFINITY, L = 0.f;
-#pragma unroll 4
-  for (int s = 0; s < nu; ++s) {
-    const int64_t pidx = ((int64_t)(u0 + s) * a.hkv + hq / G) * G + hq % G;
-    const float ms = a.part_ml[pidx * 2], ls = a.part_ml[pidx * 2 + 1];
-    const float mn = fmaxf(M, ms);
-    const float mr = mn == -INFINITY ? 0.f : mn;
-    L = L * fast_exp2(M - mr) + ls * fast_exp2(ms - mr);
-    M = mn;
+  const int64_t stride = (int64_t)a.hkv * G;
+  const int64_t p0 = ((int64_t)u0 * a.hkv + hq / G) * G + hq % G;
+  float M = -INFINITY;
+  for (int s = lane; s < nu; s += 64) M = fmaxf(M, a.part_ml[(p0 + s * stride) * 2]);
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+  const float Mr = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  for (int s = lane; s < nu; s += 64) {
+    const int64_t pidx = p0 + s * stride;
+    L = fmaf(a.part_ml[pidx * 2 + 1], fast_exp2(a.part_ml[pidx * 2] - Mr), L);
   }
-  a.lse[idx] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+  for (int off = 32; off > 0; off >>= 1) L += shfl_xor(L, off);
+  if (lane == 0) a.lse[idx] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
 
 enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
@@ -743,12 +747,12 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   if (rc || a.nsplit == 1) return rc;
   if (with_acc) {
     if (dtype == DELTA_BF16)
-      hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hkv), dim3(256), 0, stream, a, G);
+      hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
     else
-      hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hkv), dim3(256), 0, stream, a, G);
+      hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
   } else {
     const int n = batch * hq;
-    hipLaunchKernelGGL(decode_merge_lse_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a, G);
+    hipLaunchKernelGGL(decode_merge_lse_kernel, dim3((n + 3) / 4), dim3(256), 0, stream, a, G);
   }
   return check_launch(who);
 }

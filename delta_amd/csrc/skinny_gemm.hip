@@ -1,0 +1,169 @@
+// Decode-batch GEMM for gfx950: out[m, n] = sum_k x[m, k] * W[n, k] (+ bias[n]), M <= 32.
+//
+// The projections of a decode step (model.py:412 wqkv, 432 wo, 509-514 w1/w3/w2, 328 lm_head;
+// nn.Linear layout, W is [N, K] row-major) multiply a handful of token rows by a large weight,
+// so they are weight-streaming: 2 bytes of W per 2 * M flops.  At M = 32 hipBLASLt streams the
+// smaller weights at 1.7-3.7 TB/s (few, large tiles); this kernel is built to stream W once at
+// HBM rate:
+//
+//   grid = (N / (8 * NB), ceil(M / 32)), block = 8 waves splitting K; wave w owns k in
+//   [w * kper, (w + 1) * kper) for the block's 8 * NB output columns and 32 token rows.
+//   Per 64-wide k step and 8-column block, one v_mfma_f32_16x16x32 per 8 token rows:
+//     A = W: row i = 2u + e is column n0 + u restricted to k in 32 e + [0, 32); lane (c, t)
+//         loads W[n0 + t/2][k + 32 (t%2) + 8c, +8), so one load instruction covers 8 weight
+//         rows x 128 contiguous bytes (whole cache lines, streaming hint);
+//     B = x^T: column j = 8 e' + v is token v of the group restricted to the same k slice e';
+//     D[2u + e][8 e' + v] is a partial dot product only when e == e', so
+//     out(u, v) = D[2u][v] + D[2u + 1][8 + v] -- one DPP row rotate by 8, done once at the end
+//     (the join is linear, so the accumulators stay raw over all k steps).
+//   The 8 waves' partials meet in LDS and the block writes bf16/fp16 rows (fp32 sum, bias
+//   added before the one rounding).
+//
+// HBM bytes per launch (algorithmic): W once (N * K * 2) + x and out (small).  Measured on
+// MI355X against hipBLASLt (torch.nn.functional.linear): at M = 4 this kernel streams the
+// Llama-3-8B projections at 4.2-6.0 TB/s (hipBLASLt 1.8-5.6).  At M = 32 it is faster standalone
+// for weights up to ~48 MB (wo: 12.5 vs 19.7 us) and slower for the large ones: every block
+// re-reads the x fragments of its k range (as many load instructions as for W), which costs
+// most inside a decode step, where x was just written across all 8 XCDs' L2s.
+#include "delta_common.h"
+
+namespace delta {
+namespace {
+
+constexpr int kGemmWaves = 8;  // 2-3 blocks per CU overlap one block's reduction with another's loads
+constexpr int kGemmRows = 32;  // token rows per block
+
+struct GemmArgs {
+  const uint16_t *x;
+  int64_t ldx;
+  const uint16_t *w;
+  int64_t ldw;
+  const uint16_t *bias;
+  uint16_t *out;
+  int64_t ldo;
+  int M, N, K, kper;
+};
+
+template <int DT, int NB>
+__global__ void __launch_bounds__(kGemmWaves * 64) gemm_skinny_kernel(GemmArgs a) {
+  using E = Elem<DT>;
+  extern __shared__ float red[];  // [wave][32 token rows][8 * NB columns]
+  constexpr int kCols = 8 * NB;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane >> 4, t = lane & 15;
+  const int n0 = blockIdx.x * kCols;
+  const int m0 = blockIdx.y * kGemmRows;
+  const int kb = wave * a.kper;
+  const int ke = min(a.K, kb + a.kper);
+
+  const uint16_t *wp = a.w + (int64_t)(n0 + (t >> 1)) * a.ldw + 32 * (t & 1) + 8 * c;
+  const uint16_t *xp[4];
+  bool xok[4];
+#pragma unroll
+  for (int tg = 0; tg < 4; ++tg) {
+    const int r = m0 + 8 * tg + (t & 7);
+    xok[tg] = r < a.M;
+    xp[tg] = a.x + (int64_t)(xok[tg] ? r : 0) * a.ldx + 32 * (t >> 3) + 8 * c;
+  }
+
+  f32x4 acc[NB][4];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) acc[nb][tg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 wf[NB], xf[4];
+  if (kb < ke) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) wf[nb] = ld128_stream(wp + (int64_t)nb * 8 * a.ldw + kb);
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) xf[tg] = xok[tg] ? ld128(xp[tg] + kb) : u32x4{0u, 0u, 0u, 0u};
+  }
+  for (int k = kb; k < ke; k += 64) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int tg = 0; tg < 4; ++tg) acc[nb][tg] = E::mfma(wf[nb], xf[tg], acc[nb][tg]);
+    // The next k step's fragments are in flight while the other waves compute.
+    if (k + 64 < ke) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wf[nb] = ld128_stream(wp + (int64_t)nb * 8 * a.ldw + k + 64);
+#pragma unroll
+      for (int tg = 0; tg < 4; ++tg) xf[tg] = xok[tg] ? ld128(xp[tg] + k + 64) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // Join the k slices and park this wave's partials: lane (c, v < 8) holds columns
+  // n0 + 8 nb + 2c + {0, 1} of token row 8 tg + v.
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) {
+      const float s0 = acc[nb][tg][0] + dpp_f<0x128>(acc[nb][tg][1]);
+      const float s1 = acc[nb][tg][2] + dpp_f<0x128>(acc[nb][tg][3]);
+      if (t < 8) {
+        float *r = red + ((int64_t)wave * kGemmRows + 8 * tg + t) * kCols + 8 * nb + 2 * c;
+        r[0] = s0;
+        r[1] = s1;
+      }
+    }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < kGemmRows * kCols; idx += kGemmWaves * 64) {
+    const int row = idx / kCols, col = idx % kCols;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGemmWaves; ++w) s += red[(w * kGemmRows + row) * kCols + col];
+    if (m0 + row < a.M) {
+      if (a.bias) s += (float)E::lo(a.bias[n0 + col]);
+      a.out[(int64_t)(m0 + row) * a.ldo + n0 + col] = (uint16_t)E::from_float(s);
+    }
+  }
+}
+
+template <int DT>
+int launch_gemm(const GemmArgs &a, int nb, hipStream_t stream) {
+  const dim3 block(kGemmWaves * 64);
+  if (nb == 4) {
+    const dim3 grid(a.N / 32, (a.M + kGemmRows - 1) / kGemmRows);
+    hipLaunchKernelGGL((gemm_skinny_kernel<DT, 4>), grid, block, kGemmWaves * kGemmRows * 32 * sizeof(float), stream, a);
+  } else {
+    const dim3 grid(a.N / 16, (a.M + kGemmRows - 1) / kGemmRows);
+    hipLaunchKernelGGL((gemm_skinny_kernel<DT, 2>), grid, block, kGemmWaves * kGemmRows * 16 * sizeof(float), stream, a);
+  }
+  return check_launch("delta_gemm_skinny");
+}
+
+}  // namespace
+}  // namespace delta
+
+extern "C" DELTA_EXPORT int delta_gemm_skinny(const void *x, int64_t ldx, const void *w, int64_t ldw,
+                                              const void *bias, void *out, int64_t ldo, int M, int N, int K,
+                                              int dtype, delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_gemm_skinny";
+  if (M <= 0 || N <= 0) return DELTA_OK;
+  if (!x || !w || !out) return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
+  if (K <= 0 || K % 64) return set_error(DELTA_ERR_INVALID, "%s: K (%d) must be a positive multiple of 64", who, K);
+  if (N % 16) return set_error(DELTA_ERR_INVALID, "%s: N (%d) must be a multiple of 16", who, N);
+  if (ldx < K || ldw < K || ldo < N) return set_error(DELTA_ERR_INVALID, "%s: leading dimensions too small", who);
+  if ((ldx % 8) || (ldw % 8) || (((uintptr_t)x | (uintptr_t)w) & 15u))
+    return set_error(DELTA_ERR_INVALID, "%s: x and W rows must be 16-byte aligned", who);
+  GemmArgs a;
+  a.x = (const uint16_t *)x;
+  a.ldx = ldx;
+  a.w = (const uint16_t *)w;
+  a.ldw = ldw;
+  a.bias = (const uint16_t *)bias;
+  a.out = (uint16_t *)out;
+  a.ldo = ldo;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.kper = (int)(ceil_div(K / 64, kGemmWaves) * 64);
+  // 32 columns per block when that still gives every CU a block, else 16.
+  const int nb = (N % 32 == 0 && N / 32 >= 256) ? 4 : 2;
+  return dtype == DELTA_BF16 ? launch_gemm<DELTA_BF16>(a, nb, (hipStream_t)stream)
+                             : launch_gemm<DELTA_FP16>(a, nb, (hipStream_t)stream);
+}

@@ -462,3 +462,38 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
     _lib.call("delta_silu_mul", g2.data_ptr(), g2.stride(0), o2.data_ptr(), o2.stride(0), int(g2.shape[0]),
               int(inter), _dtype_code(gate_up), _stream(dev))
     return out
+
+
+def gemm_skinny_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """True when ``delta_gemm_skinny`` takes ``x @ weight.T``: decode-sized rows, K % 64 == 0,
+    N % 16 == 0, 16-byte aligned rows of a bf16/fp16 weight of x's dtype."""
+    if x.dtype not in _DTYPES or weight.dtype != x.dtype or weight.dim() != 2 or not x.is_cuda:
+        return False
+    N, Kd = weight.shape
+    rows = x.numel() // max(x.shape[-1], 1)
+    return (x.shape[-1] == Kd and Kd % 64 == 0 and N % 16 == 0 and 0 < rows <= 32
+            and weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def gemm_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``F.linear(x, weight, bias)`` for decode-sized x on ``delta_gemm_skinny``."""
+    dev = _check_cuda(x, weight, bias, out)
+    N, Kd = weight.shape
+    if x.shape[-1] != Kd:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects {Kd}")
+    if weight.dtype != x.dtype or (bias is not None and (bias.dtype != x.dtype or bias.numel() != N
+                                                         or not bias.is_contiguous())):
+        raise TypeError("x, weight and bias must share a dtype; bias must be contiguous [N]")
+    if weight.stride(1) != 1:
+        raise ValueError("weight rows must be contiguous")
+    x2 = _rows2d("x", x, Kd)
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
+    o2 = out.reshape(-1, N)
+    if o2.stride(1) != 1 or o2.shape[0] != M:
+        raise ValueError("out must be [..., N] with contiguous rows")
+    _lib.call("delta_gemm_skinny", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0),
+              _ptr(bias), o2.data_ptr(), o2.stride(0), int(M), int(N), int(Kd), _dtype_code(x), _stream(dev))
+    return out

@@ -174,7 +174,7 @@ class Transformer(nn.Module):
             x, pending = layer.forward_fused(x, pending, input_pos, kv_append_indptr, kv_page_indices,
                                              kv_page_indptr, kv_page_lastlen)
         _, y = K.add_rmsnorm(x, pending, self.norm.weight, self.norm.eps)
-        return self.output(y)
+        return dense(y, self.output)
 
     def _finalize_logits(self, logits: Tensor) -> Tensor:
         """argmax over the vocabulary on the HIP kernel; returns int64 [bsz, seqlen]."""
@@ -187,6 +187,25 @@ class Transformer(nn.Module):
     @classmethod
     def from_name(cls, name: str):
         return cls(ModelArgs.from_name(name))
+
+
+# Decode projections go to delta_gemm_skinny where it beats hipBLASLt on MI355X inside the
+# captured step: every shape at <= 8 token rows.  At 32 rows it wins standalone for weights up to
+# ~48 MB but loses inside the step (6.36 vs 6.17-6.25 ms per config-3 step, same process): its
+# blocks re-read the activation rows, which the previous kernel left spread over the 8 XCDs'
+# L2s, so the weight-size rule is off (0) until that re-read is gone.
+_SKINNY_ROWS_ANY = 8
+_SKINNY_MAX_WEIGHT_BYTES = 0
+
+
+def dense(x: Tensor, layer: nn.Linear) -> Tensor:
+    """``layer(x)`` on the decode GEMM kernel when it is the faster one, else torch."""
+    w = layer.weight
+    if K.gemm_skinny_ok(x, w):
+        rows = x.numel() // x.shape[-1]
+        if rows <= _SKINNY_ROWS_ANY or w.numel() * w.element_size() <= _SKINNY_MAX_WEIGHT_BYTES:
+            return K.gemm_skinny(x, w, layer.bias)
+    return layer(x)
 
 
 class TransformerBlock(nn.Module):
@@ -207,7 +226,8 @@ class TransformerBlock(nn.Module):
         """Same block as ``forward`` with the input ``x + pending`` left unsummed; returns
         ``(h, ffn_out)`` whose sum is the block output."""
         x, a_in = K.add_rmsnorm(x, pending, self.attention_norm.weight, self.attention_norm.eps)
-        attn = self.attention(a_in, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen)
+        attn = self.attention(a_in, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen,
+                              fused=True)
         h, f_in = K.add_rmsnorm(x, attn, self.ffn_norm.weight, self.ffn_norm.eps)
         return h, self.feed_forward.forward_fused(f_in)
 
@@ -229,11 +249,13 @@ class Attention(nn.Module):
         # debug capture (tests): when a list, each call appends (q, o)
         self.record: Optional[list] = None
 
-    def forward(self, x, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen):
+    def forward(self, x, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen,
+                fused: bool = False):
         bsz, seqlen, _ = x.shape
         q_size = self.n_head * self.head_dim
         kv_size = self.n_local_heads * self.head_dim
-        q, k, v = self.wqkv(x).split([q_size, kv_size, kv_size], dim=-1)
+        lin = dense if fused else (lambda t, layer: layer(t))
+        q, k, v = lin(x, self.wqkv).split([q_size, kv_size, kv_size], dim=-1)
         q = q.view(bsz * seqlen, self.n_head, self.head_dim)
         k = k.view(bsz * seqlen, self.n_local_heads, self.head_dim)
         v = v.view(bsz * seqlen, self.n_local_heads, self.head_dim)
@@ -244,7 +266,7 @@ class Attention(nn.Module):
         if self.record is not None:
             self.record.append((q.detach().clone(), y.detach().clone()))
         y = y.contiguous().view(bsz, seqlen, self.dim)
-        return self.wo(y)
+        return lin(y, self.wo)
 
 
 class FeedForward(nn.Module):
@@ -273,7 +295,7 @@ class FeedForward(nn.Module):
         return self.w2(F.silu(g) * u)
 
     def forward_fused(self, x: Tensor) -> Tensor:
-        return self.w2(K.silu_mul(torch.matmul(x, self.w13_t)))
+        return dense(K.silu_mul(torch.matmul(x, self.w13_t)), self.w2)
 
 
 class RMSNorm(nn.Module):

@@ -285,6 +285,15 @@ int delta_add_rmsnorm(const void *x, int64_t x_stride, const void *residual, int
 int delta_silu_mul(const void *gate_up, int64_t gu_stride, void *out, int64_t out_stride, int rows,
                    int inter, int dtype, delta_stream_t stream);
 
+/* out[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]) for decode-sized M: the nn.Linear
+ * projections of a decode step (model.py:412 wqkv, 432 wo, 509-514 w1/w3/w2, 328 lm_head),
+ * which torch runs through cuBLAS in the reference.  x [M, K] (row stride ldx), w [N, K]
+ * (row stride ldw, the nn.Linear weight layout), out [M, N] (row stride ldo), bias [N] or
+ * NULL, all of dtype; fp32 accumulation, one rounding.  K % 64 == 0, N % 16 == 0, x and w
+ * rows 16-byte aligned.  Built for M <= 32 (larger M works, re-reading w per 32 rows). */
+int delta_gemm_skinny(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *bias,
+                      void *out, int64_t ldo, int M, int N, int K, int dtype, delta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -432,3 +432,24 @@ def test_dense_step_helpers_match_torch(dtype):
     logits[4, 10] = logits[4, 20] = logits[4].max() + 1   # tie: first index wins
     logits[5, 1000] = float("nan")                         # NaN ranks highest, as torch.argmax
     assert torch.equal(K.argmax_rows(logits), torch.argmax(logits, -1))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,Kd,bias", [(32, 4096, 4096, False), (1, 48, 64, True), (5, 6144, 4160, True),
+                                        (32, 272, 14336, False), (40, 64, 1024, False)])
+def test_gemm_skinny_matches_fp32_reference(dtype, M, N, Kd, bias):
+    """delta_gemm_skinny against x.float() @ w.float().T (+ b): fp32 accumulation then one
+    rounding, so the error is one output ulp plus fp32 summation-order noise."""
+    gen = torch.Generator(device=DEV).manual_seed(M * 7 + N + Kd)
+    x = torch.randn(M, Kd, generator=gen, device=DEV).to(dtype)
+    w = (torch.randn(N, Kd, generator=gen, device=DEV) * 0.05).to(dtype)
+    b = (torch.randn(N, generator=gen, device=DEV) * 0.1).to(dtype) if bias else None
+    out = K.gemm_skinny(x, w, b)
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().T + (b.float() if bias else 0.0)
+    mag = x.float().abs() @ w.float().abs().T
+    eps = torch.finfo(dtype).eps
+    err = (out.float() - ref).abs()
+    assert torch.all(err <= eps * ref.abs() + 1e-5 * mag + 1e-6), f"max err {err.max().item()}"
+    # deterministic
+    assert torch.equal(out, K.gemm_skinny(x, w, b))

@@ -59,6 +59,9 @@ SIGNATURES = {
     "delta_rope": (c_int, [
         _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_float, c_int, c_float, c_float, c_float, _P]),
+    "delta_rope_append": (c_int, [
+        _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, _P, c_int64, _P, c_int64, _P, _P,
+        c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, c_float, c_float, c_float, _P]),
 }
 
 _lib = None

@@ -11,7 +11,14 @@
 // f_j = theta^(-2j/d) / rope_scale, or for Llama 3.1 the blend
 // (1 - s) f_j/rope_scale + s f_j, s = clamp(f_j * old_ctx / (2 pi (hi - lo)) - 1/(hi/lo - 1), 0, 1).
 // fp32 angle and fp32 sin/cos as the reference's kernel; fp32 rotation, one
-// rounding to the storage dtype.
+// rounding to the storage dtype.  A block computes the 64 (cos, sin) pairs of its
+// token's position once, in LDS, and every head reads them.
+//
+// delta_rope_append fuses the two for a decode layer (Attention.forward, model.py:
+// 413-418): RoPE of q and k, then the append of the rotated k and of v -- one launch,
+// and k never makes a round trip through HBM before it lands in its page.  Same
+// arithmetic per element as delta_rope followed by delta_append_kv, so q and the
+// cache come out bit-identical.
 #include "delta_common.h"
 
 namespace delta {
@@ -88,32 +95,103 @@ struct RopeArgs {
   float rcp_scale, log2_theta, smooth_a, smooth_b;
 };
 
+constexpr int kPairs = kHeadDim / 2;
+
+// (cos, sin) of pos * f_j for the 64 pairs j, into tab[2 j], tab[2 j + 1] (threads 0..63).
+__device__ __forceinline__ void rope_table(const RopeArgs &a, float pos, float *tab) {
+  const int j = threadIdx.x;
+  if (j < kPairs) {
+    float f = exp2f(-(2.0f * (float)j / (float)kHeadDim) * a.log2_theta);  // theta^(-2j/d)
+    const float s = fminf(fmaxf(f * a.smooth_a + a.smooth_b, 0.f), 1.f);
+    f = (1.f - s) * (f * a.rcp_scale) + s * f;
+    float sn, cs;
+    sincosf(pos * f, &sn, &cs);
+    tab[2 * j] = cs;
+    tab[2 * j + 1] = sn;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t rope_pair(uint32_t pr, const float *tab, int j) {
+  using E = Elem<DT>;
+  const float cs = tab[2 * j], sn = tab[2 * j + 1];
+  const float x0 = E::lo(pr), x1 = E::hi(pr);
+  const float y0 = x0 * cs - x1 * sn;
+  const float y1 = x1 * cs + x0 * sn;
+  return E::from_float(y0) | (E::from_float(y1) << 16);
+}
+
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kernel(RopeArgs a) {
-  using E = Elem<DT>;
+  __shared__ float tab[2 * kPairs];
   const int i = blockIdx.x;
   const int b = find_row(a.indptr, a.batch, i);
   const float pos = (float)(a.offsets[b] + (i - a.indptr[b]));
-  constexpr int kPairs = kHeadDim / 2;
+  rope_table(a, pos, tab);
+  __syncthreads();
   const int total = (a.hq + a.hkv) * kPairs;
   for (int w = threadIdx.x; w < total; w += blockDim.x) {
     const int head = w / kPairs;
     const int j = w % kPairs;
-    float f = exp2f(-(2.0f * (float)j / (float)kHeadDim) * a.log2_theta);  // theta^(-2j/d)
-    float s = fminf(fmaxf(f * a.smooth_a + a.smooth_b, 0.f), 1.f);
-    f = (1.f - s) * (f * a.rcp_scale) + s * f;
-    float sn, cs;
-    sincosf(pos * f, &sn, &cs);
     const bool is_q = head < a.hq;
     const uint16_t *src = is_q ? a.q + (int64_t)i * a.q_stride + (int64_t)head * kHeadDim
                                : a.k + (int64_t)i * a.k_stride + (int64_t)(head - a.hq) * kHeadDim;
     uint16_t *dst = is_q ? a.q_out + (int64_t)i * a.q_out_stride + (int64_t)head * kHeadDim
                          : a.k_out + (int64_t)i * a.k_out_stride + (int64_t)(head - a.hq) * kHeadDim;
     const uint32_t pr = *reinterpret_cast<const uint32_t *>(src + 2 * j);
-    const float x0 = E::lo(pr), x1 = E::hi(pr);
-    const float y0 = x0 * cs - x1 * sn;
-    const float y1 = x1 * cs + x0 * sn;
-    *reinterpret_cast<uint32_t *>(dst + 2 * j) = E::from_float(y0) | (E::from_float(y1) << 16);
+    *reinterpret_cast<uint32_t *>(dst + 2 * j) = rope_pair<DT>(pr, tab, j);
+  }
+}
+
+// Fused RoPE + append, one block per token: q heads rotated into q_out, k heads rotated
+// straight into the token's page slot, v copied there (the slot as delta_append_kv finds it).
+template <int DT>
+__global__ void __launch_bounds__(256) rope_append_kernel(RopeArgs r, AppendArgs a) {
+  __shared__ float tab[2 * kPairs];
+  const int i = blockIdx.x;
+  const int b = find_row(a.append_indptr, a.batch, i);
+  const int a0 = a.append_indptr[b];
+  const float pos = (float)(r.offsets[b] + (i - a0));
+  rope_table(r, pos, tab);
+  // The cache slot (checks as in append_kv_kernel; an invalid slot drops the K/V write only).
+  const int alen = a.append_indptr[b + 1] - a0;
+  const int64_t p0 = a.kv_indptr[b], p1 = a.kv_indptr[b + 1];
+  int pid = -1, slot = 0;
+  if (i >= a0 && i - a0 < alen && p0 >= 0 && p1 >= p0 && p1 <= a.kv_indices_len) {
+    const int np = (int)(p1 - p0);
+    int lp = a.last_page_len[b];
+    lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+    const int seq = np > 0 ? (np - 1) * kPageSize + lp : lp;
+    const int apos = seq - alen + (i - a0);
+    if (apos >= 0 && apos / kPageSize < np) {
+      const int p = a.kv_indices[p0 + apos / kPageSize];
+      if (p >= 0 && (int64_t)p < a.num_pages) {
+        pid = p;
+        slot = apos % kPageSize;
+      }
+    }
+  }
+  const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
+  uint16_t *kdst = a.cache + (((int64_t)(pid < 0 ? 0 : pid) * 2 + 0) * kPageSize + slot) * row_elems;
+  uint16_t *vdst = a.cache + (((int64_t)(pid < 0 ? 0 : pid) * 2 + 1) * kPageSize + slot) * row_elems;
+  __syncthreads();
+  const int total = (r.hq + r.hkv) * kPairs;
+  for (int w = threadIdx.x; w < total; w += blockDim.x) {
+    const int head = w / kPairs;
+    const int j = w % kPairs;
+    if (head < r.hq) {
+      const uint32_t pr = *reinterpret_cast<const uint32_t *>(r.q + (int64_t)i * r.q_stride + (int64_t)head * kHeadDim + 2 * j);
+      *reinterpret_cast<uint32_t *>(r.q_out + (int64_t)i * r.q_out_stride + (int64_t)head * kHeadDim + 2 * j) =
+          rope_pair<DT>(pr, tab, j);
+    } else if (pid >= 0) {
+      const int hk = head - r.hq;
+      const uint32_t pr = *reinterpret_cast<const uint32_t *>(r.k + (int64_t)i * r.k_stride + (int64_t)hk * kHeadDim + 2 * j);
+      *reinterpret_cast<uint32_t *>(kdst + (int64_t)hk * kHeadDim + 2 * j) = rope_pair<DT>(pr, tab, j);
+    }
+  }
+  if (pid >= 0) {
+    for (int ch = threadIdx.x; ch < a.hkv * (kHeadDim / 8); ch += blockDim.x)
+      st128(vdst + 8 * ch, ld128(a.v + (int64_t)i * a.v_stride + 8 * ch));
   }
 }
 
@@ -201,5 +279,74 @@ extern "C" DELTA_EXPORT int delta_rope(const void *q, int64_t q_stride, const vo
     hipLaunchKernelGGL(rope_kernel<DELTA_BF16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL(rope_kernel<DELTA_FP16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch(who);
+}
+
+extern "C" DELTA_EXPORT int delta_rope_append(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+                                              const void *v, int64_t v_stride, void *q_out, int64_t q_out_stride,
+                                              const int32_t *kv_append_indptr, const int32_t *offsets,
+                                              void *kv_cache, int64_t num_pages, const int32_t *kv_indices,
+                                              int64_t kv_indices_len, const int32_t *kv_indptr,
+                                              const int32_t *kv_last_page_len, int nnz, int batch,
+                                              int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                                              float rope_scale, float rope_theta, int llama31, float low_freq_factor,
+                                              float high_freq_factor, float old_context_len, delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_rope_append";
+  if (nnz <= 0 || batch <= 0) return DELTA_OK;
+  if (head_dim != kHeadDim) return set_error(DELTA_ERR_INVALID, "%s: head_dim must be 128", who);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: bad dtype", who);
+  if (!q || !k || !v || !q_out || !kv_append_indptr || !offsets || !kv_cache || !kv_indices || !kv_indptr ||
+      !kv_last_page_len)
+    return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)q_out) & 3u || ((uintptr_t)v | (uintptr_t)kv_cache) & 15u ||
+      (v_stride % 8))
+    return set_error(DELTA_ERR_INVALID, "%s: q/k 4-byte, v/cache 16-byte aligned, v stride a multiple of 8", who);
+  if (!(rope_scale > 0.f) || !(rope_theta > 0.f)) return set_error(DELTA_ERR_INVALID, "%s: bad rope params", who);
+  RopeArgs r;
+  r.q = (const uint16_t *)q;
+  r.q_stride = q_stride;
+  r.k = (const uint16_t *)k;
+  r.k_stride = k_stride;
+  r.q_out = (uint16_t *)q_out;
+  r.q_out_stride = q_out_stride;
+  r.k_out = nullptr;
+  r.k_out_stride = 0;
+  r.indptr = kv_append_indptr;
+  r.offsets = offsets;
+  r.batch = batch;
+  r.hq = num_qo_heads;
+  r.hkv = num_kv_heads;
+  r.rcp_scale = 1.0f / rope_scale;
+  r.log2_theta = log2f(rope_theta);
+  if (llama31) {
+    if (!(high_freq_factor > low_freq_factor) || !(low_freq_factor > 0.f))
+      return set_error(DELTA_ERR_INVALID, "%s: bad llama3.1 frequency factors", who);
+    const float two_pi = 6.283185307179586f;
+    r.smooth_a = old_context_len / (two_pi * high_freq_factor - two_pi * low_freq_factor);
+    r.smooth_b = -1.0f / (high_freq_factor / low_freq_factor - 1.0f);
+  } else {
+    r.smooth_a = 0.f;
+    r.smooth_b = 0.f;
+  }
+  AppendArgs a;
+  a.k = nullptr;
+  a.k_stride = 0;
+  a.v = (const uint16_t *)v;
+  a.v_stride = v_stride;
+  a.append_indptr = kv_append_indptr;
+  a.cache = (uint16_t *)kv_cache;
+  a.num_pages = num_pages;
+  a.kv_indices = kv_indices;
+  a.kv_indices_len = kv_indices_len;
+  a.kv_indptr = kv_indptr;
+  a.last_page_len = kv_last_page_len;
+  a.batch = batch;
+  a.hkv = num_kv_heads;
+  if (dtype == DELTA_BF16)
+    hipLaunchKernelGGL(rope_append_kernel<DELTA_BF16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, r, a);
+  else
+    hipLaunchKernelGGL(rope_append_kernel<DELTA_FP16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, r, a);
   return check_launch(who);
 }

@@ -400,6 +400,44 @@ def rope(q: torch.Tensor, k: torch.Tensor, indptr: torch.Tensor, offsets: torch.
     return q_out, k_out
 
 
+def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_append_indptr: torch.Tensor,
+                offsets: torch.Tensor, kv_cache: torch.Tensor, kv_indices: torch.Tensor,
+                kv_indptr: torch.Tensor, kv_last_page_len: torch.Tensor, *, rope_scale: float = 1.0,
+                rope_theta: float = 1e4, low_freq_factor: Optional[float] = None,
+                high_freq_factor: Optional[float] = None, old_context_len: Optional[float] = None,
+                q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``rope`` then ``append_kv`` in one launch (``delta_rope_append``); returns the rotated q."""
+    dev = _check_cuda(q, k, v, kv_append_indptr, offsets, kv_cache, kv_indices, kv_indptr, kv_last_page_len, q_out)
+    _check_cache(kv_cache)
+    hkv = kv_cache.shape[3]
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM or q.stride(2) != 1 or q.stride(1) != HEAD_DIM:
+        raise ValueError("q must be [nnz, Hq, 128] with contiguous heads")
+    for name, t in (("k", k), ("v", v)):
+        if t.dim() != 3 or t.shape[1] != hkv or t.shape[2] != HEAD_DIM or t.stride(2) != 1 \
+                or t.stride(1) != HEAD_DIM or t.stride(0) % 8 or t.shape[0] != q.shape[0]:
+            raise ValueError(f"{name} must be [nnz, {hkv}, 128] with contiguous heads")
+        if t.dtype != kv_cache.dtype or q.dtype != kv_cache.dtype:
+            raise TypeError("q, k, v and kv_cache must share a dtype")
+    q_out = torch.empty_like(q) if q_out is None else q_out
+    if q_out.shape != q.shape or q_out.dtype != q.dtype or q_out.stride(2) != 1 or q_out.stride(1) != HEAD_DIM:
+        raise ValueError("q_out must match q's shape with contiguous heads")
+    B = kv_append_indptr.numel() - 1
+    _check_i32("kv_append_indptr", kv_append_indptr, B + 1)
+    _check_i32("offsets", offsets, B)
+    _check_i32("kv_indices", kv_indices)
+    _check_i32("kv_indptr", kv_indptr, B + 1)
+    _check_i32("kv_last_page_len", kv_last_page_len, B)
+    llama31 = low_freq_factor is not None and high_freq_factor is not None
+    _lib.call("delta_rope_append",
+              q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), q_out.data_ptr(),
+              q_out.stride(0), kv_append_indptr.data_ptr(), offsets.data_ptr(), kv_cache.data_ptr(),
+              kv_cache.shape[0], kv_indices.data_ptr(), kv_indices.numel(), kv_indptr.data_ptr(),
+              kv_last_page_len.data_ptr(), int(q.shape[0]), int(B), int(q.shape[1]), int(hkv), HEAD_DIM,
+              _dtype_code(q), float(rope_scale), float(rope_theta), int(llama31), float(low_freq_factor or 0.0),
+              float(high_freq_factor or 0.0), float(old_context_len or 0.0), _stream(dev))
+    return q_out
+
+
 def argmax_rows(logits: torch.Tensor, out: Optional[torch.Tensor] = None,
                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """First index of each row's maximum (``delta_argmax_rows``); logits [rows, cols]."""

@@ -259,9 +259,15 @@ class Attention(nn.Module):
         q = q.view(bsz * seqlen, self.n_head, self.head_dim)
         k = k.view(bsz * seqlen, self.n_local_heads, self.head_dim)
         v = v.view(bsz * seqlen, self.n_local_heads, self.head_dim)
-        q, k = self.rope(q, k, kv_append_indptr, offsets)
-        kv_cache = self.kv_cache.update_target(k, v, kv_append_indptr, kv_page_indices, kv_page_indptr,
-                                               kv_page_lastlen)
+        if fused:
+            # mylib::rope + mylib::update_kv in one launch (bit-identical to the two ops)
+            q = K.rope_append(q, k, v, kv_append_indptr, offsets, self.kv_cache.kv_cache, kv_page_indices,
+                              kv_page_indptr, kv_page_lastlen, **ops.active_backend().rope_params())
+            kv_cache = self.kv_cache.kv_cache
+        else:
+            q, k = self.rope(q, k, kv_append_indptr, offsets)
+            kv_cache = self.kv_cache.update_target(k, v, kv_append_indptr, kv_page_indices, kv_page_indptr,
+                                                   kv_page_lastlen)
         y = self.attn_decode(q, kv_cache)
         if self.record is not None:
             self.record.append((q.detach().clone(), y.detach().clone()))

@@ -257,6 +257,20 @@ int delta_rope(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
                float rope_scale, float rope_theta, int llama31, float low_freq_factor,
                float high_freq_factor, float old_context_len, delta_stream_t stream);
 
+/* mylib::rope followed by mylib::update_kv for one layer (Attention.forward,
+ * model.py:413-418) in one launch: q -> q_out rotated as delta_rope; k rotated and
+ * v copied into the paged cache at the slots delta_append_kv would use (token i of
+ * row b at offsets[b] + i - kv_append_indptr[b] for the rotation).  Results are
+ * bit-identical to the two calls; the rotated k is not returned. */
+int delta_rope_append(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+                      const void *v, int64_t v_stride, void *q_out, int64_t q_out_stride,
+                      const int32_t *kv_append_indptr, const int32_t *offsets, void *kv_cache,
+                      int64_t num_pages, const int32_t *kv_indices, int64_t kv_indices_len,
+                      const int32_t *kv_indptr, const int32_t *kv_last_page_len, int nnz, int batch,
+                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype, float rope_scale,
+                      float rope_theta, int llama31, float low_freq_factor, float high_freq_factor,
+                      float old_context_len, delta_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Dense decode-step helpers (the element-wise chains between the GEMMs)      */
 /* ------------------------------------------------------------------------ */

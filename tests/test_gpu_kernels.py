@@ -453,3 +453,37 @@ def test_gemm_skinny_matches_fp32_reference(dtype, M, N, Kd, bias):
     assert torch.all(err <= eps * ref.abs() + 1e-5 * mag + 1e-6), f"max err {err.max().item()}"
     # deterministic
     assert torch.equal(out, K.gemm_skinny(x, w, b))
+
+
+@pytest.mark.parametrize("llama31", [False, True])
+def test_rope_append_equals_rope_then_append(llama31):
+    """The fused launch writes the same q and the same cache bytes as delta_rope followed by
+    delta_append_kv (same per-element arithmetic), including a 2-token append and a row whose
+    append lands on a fresh page."""
+    gen = torch.Generator().manual_seed(21)
+    hq, hkv, B = 16, 4, 4
+    qo = [1, 2, 1, 1]
+    lens_after = [17, 33, 16, 300]  # tokens cached after the append
+    pages = [(n + 15) // 16 for n in lens_after]
+    num_pages = sum(pages) + 5
+    perm = torch.randperm(num_pages, generator=gen)[:sum(pages)].to(torch.int32)
+    indptr = torch.tensor([0] + list(torch.cumsum(torch.tensor(pages), 0)), dtype=torch.int32)
+    last = torch.tensor([n - (p - 1) * 16 for n, p in zip(lens_after, pages)], dtype=torch.int32)
+    app = torch.tensor([0] + list(torch.cumsum(torch.tensor(qo), 0)), dtype=torch.int32)
+    offsets = torch.tensor([n - a for n, a in zip(lens_after, qo)], dtype=torch.int32)
+    nnz = sum(qo)
+    qkv = torch.randn(nnz, (hq + 2 * hkv) * 128, generator=gen).to(torch.bfloat16).to(DEV)
+    q, k, v = qkv.split([hq * 128, hkv * 128, hkv * 128], dim=-1)
+    q, k, v = q.view(nnz, hq, 128), k.view(nnz, hkv, 128), v.view(nnz, hkv, 128)
+    cache = torch.randn(num_pages, 2, 16, hkv, 128, generator=gen).to(torch.bfloat16).to(DEV)
+    cache2 = cache.clone()
+    p = dict(rope_scale=8.0 if llama31 else 1.0, rope_theta=5e5)
+    if llama31:
+        p.update(low_freq_factor=1.0, high_freq_factor=4.0, old_context_len=8192.0)
+    g = lambda t: t.to(DEV)
+    q1, k1 = K.rope(q, k, g(app), g(offsets), **p)
+    K.append_kv(k1, v, g(app), cache, g(perm), g(indptr), g(last))
+    q2 = K.rope_append(q, k, v, g(app), g(offsets), cache2, g(perm), g(indptr), g(last), **p)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(cache, cache2)

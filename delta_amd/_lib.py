@@ -20,6 +20,9 @@ SIGNATURES = {
     "delta_abi_version": (c_int, []),
     "delta_decode_num_splits": (c_int, [c_int, c_int, c_int]),
     "delta_paged_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "delta_paged_prefill": (c_int, [
+        _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P,
+        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P]),
     "delta_paged_decode": (c_int, [
         _P, c_int64, c_int64,                 # q, strides
         _P, c_int64,                          # kv_cache, num_pages

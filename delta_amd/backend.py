@@ -17,8 +17,8 @@ work runs:
   the ``cachelens`` advance -- is one hipGraph.
 * Idle slots point at a private scratch page with ``cachelens = 0`` so the
   graph also covers partial batches.
-* Prefill / mixed steps run eagerly: each prompt token becomes a virtual
-  decode row over its causal prefix, on the same attention kernel.
+* Prefill / mixed steps run eagerly: all new tokens are appended, then the
+  causal paged prefill kernel attends each row's pages.
 
 Out of scope on this build (raise): tensor parallelism, ``torch.compile``
 (no Triton), the v1 selector, the ``delta_lse`` scorer and an fp16 dump.
@@ -46,16 +46,19 @@ PAGE_SIZE = 16
 
 
 class _StepCSR:
-    """Page tables the attention ops read during one forward."""
+    """Page tables the attention ops read during one forward (prefill steps also carry the
+    query-token CSR of the rows)."""
 
-    __slots__ = ("mode", "kv_indptr", "kv_indices", "kv_last", "max_pages")
+    __slots__ = ("mode", "kv_indptr", "kv_indices", "kv_last", "max_pages", "qo_indptr", "max_qo")
 
-    def __init__(self, mode, kv_indptr, kv_indices, kv_last, max_pages):
+    def __init__(self, mode, kv_indptr, kv_indices, kv_last, max_pages, qo_indptr=None, max_qo=1):
         self.mode = mode
         self.kv_indptr = kv_indptr
         self.kv_indices = kv_indices
         self.kv_last = kv_last
         self.max_pages = max_pages
+        self.qo_indptr = qo_indptr
+        self.max_qo = max_qo
 
 
 class LMBackend:
@@ -227,11 +230,11 @@ class LMBackend:
 
     def attn_full(self, q, kv_cache):
         st = self._step
-        # Prefill rows (one per prompt token) can outnumber the decode batch the static
-        # workspace was sized for; they use the grow-only shared workspace (never captured).
-        ws = self.workspace if st.mode == "decode" else None
+        if st.mode == "prefill":  # several query tokens per row: causal prefill kernel
+            return K.paged_prefill(q, kv_cache, st.qo_indptr, st.kv_indptr, st.kv_indices, st.kv_last,
+                                   max_qo_len=st.max_qo)
         return K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                              max_pages_per_row=st.max_pages, workspace=ws)
+                              max_pages_per_row=st.max_pages, workspace=self.workspace)
 
     def attn_subset(self, q, kv_cache):
         if not (self.enable_selective_cache and self._decode_mode()):
@@ -470,8 +473,8 @@ class LMBackend:
 
     @torch.inference_mode()
     def _prefill_forward(self, slots, reqs):
-        """Eager step for rows with several query tokens: each query token is a virtual
-        decode row over its causal prefix (same attention kernel)."""
+        """Eager step for rows with several query tokens (prompts): KV append of all new tokens,
+        then causal paged prefill attention over each row's pages."""
         dev = self.device
         toks, qo_lens, rows_pages, rows_last, offsets = [], [], [], [], []
         for s, r in zip(slots, reqs):
@@ -485,26 +488,21 @@ class LMBackend:
             rows_pages.append(list(r.page_indices))
             rows_last.append(r.page_lastlen)
             offsets.append(start)
-        # row CSR (KV append) and virtual rows (attention)
+        # the rows' page CSR (after planning, it covers the new tokens)
         kv_indptr, kv_indices = [0], []
-        v_indptr, v_indices, v_last = [0], [], []
-        for pages, q_len, start in zip(rows_pages, qo_lens, offsets):
+        for pages in rows_pages:
             kv_indices.extend(pages)
             kv_indptr.append(len(kv_indices))
-            for i in range(q_len):
-                pos = start + i
-                n = pos // PAGE_SIZE + 1
-                v_indices.extend(pages[:n])
-                v_indptr.append(len(v_indices))
-                v_last.append(pos % PAGE_SIZE + 1)
         i32 = dict(dtype=torch.int32, device=dev)
         tokens = torch.cat(toks).view(1, -1).to(dev)
         qo_indptr = torch.tensor([0] + list(torch.cumsum(torch.tensor(qo_lens), 0).tolist()), **i32)
-        self._step = _StepCSR("prefill", torch.tensor(v_indptr, **i32), torch.tensor(v_indices, **i32),
-                              torch.tensor(v_last, **i32), max(v_indptr[i + 1] - v_indptr[i] for i in range(len(v_last))))
+        row_ip = torch.tensor(kv_indptr, **i32)
+        row_ind = torch.tensor(kv_indices, **i32)
+        row_last = torch.tensor(rows_last, **i32)
+        self._step = _StepCSR("prefill", row_ip, row_ind, row_last, max(len(p) for p in rows_pages),
+                              qo_indptr=qo_indptr, max_qo=max(qo_lens))
         try:
-            out = self.model(tokens, torch.tensor(offsets, **i32), qo_indptr, torch.tensor(kv_indices, **i32),
-                             torch.tensor(kv_indptr, **i32), torch.tensor(rows_last, **i32))
+            out = self.model(tokens, torch.tensor(offsets, **i32), qo_indptr, row_ind, row_ip, row_last)
         finally:
             self._step = None
         for s, q_len, start in zip(slots, qo_lens, offsets):

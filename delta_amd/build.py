@@ -19,7 +19,7 @@ LIB_NAME = "_delta_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 SOURCES = ["capi.hip", "paged_decode.hip", "page_score.hip", "page_select.hip",
            "page_metadata.hip", "kv_rope.hip", "step_utils.hip",
-           "skinny_gemm.hip"]
+           "skinny_gemm.hip", "prefill.hip"]
 
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",

@@ -162,6 +162,35 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tenso
     return out
 
 
+def paged_prefill(q: torch.Tensor, kv_cache: torch.Tensor, qo_indptr: torch.Tensor,
+                  kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, *,
+                  max_qo_len: int, sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                  lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal paged prefill attention (``delta_paged_prefill``); q/out [nnz, Hq, 128]."""
+    dev = _check_cuda(q, kv_cache, qo_indptr, kv_indptr, kv_indices, kv_last_page_len, out, lse)
+    _check_cache(kv_cache)
+    hq, hkv = _check_heads(q, kv_cache)
+    B = qo_indptr.numel() - 1
+    _check_i32("qo_indptr", qo_indptr, B + 1)
+    _check_i32("kv_indptr", kv_indptr, B + 1)
+    _check_i32("kv_indices", kv_indices)
+    _check_i32("kv_last_page_len", kv_last_page_len, B)
+    if out is None:
+        out = torch.empty_like(q)
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError("out must match q's shape/dtype with unit inner stride")
+    if lse is not None and (lse.dtype != torch.float32 or tuple(lse.shape) != (q.shape[0], hq)
+                            or not lse.is_contiguous()):
+        raise ValueError("lse must be contiguous fp32 [nnz, Hq]")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HEAD_DIM)
+    _lib.call("delta_paged_prefill", q.data_ptr(), q.stride(0), q.stride(1), kv_cache.data_ptr(),
+              kv_cache.shape[0], qo_indptr.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+              kv_indices.numel(), kv_last_page_len.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+              _ptr(lse), int(B), hq, hkv, HEAD_DIM, _dtype_code(q), float(sm_scale), int(max_qo_len), _stream(dev))
+    return out
+
+
 def page_scores_from_logits(logits_dump: torch.Tensor, kv_indptr: torch.Tensor,
                             kv_last_page_len: torch.Tensor, max_pages: int, *,
                             lse: Optional[torch.Tensor] = None,

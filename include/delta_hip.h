@@ -123,6 +123,21 @@ int delta_paged_decode_subset(const void *q, int64_t q_stride_b, int64_t q_strid
                               int dtype, float sm_scale, int max_pages_per_row,
                               void *workspace, size_t workspace_bytes, delta_stream_t stream);
 
+/* Causal attention of several query tokens per row (prompt steps): FlashInfer
+ * BatchPrefillWithPagedKVCacheWrapper.run with causal=True (backend.py:1091-1105).
+ * q/o are [nnz, num_qo_heads, 128] (token stride, head stride), row b's tokens at
+ * qo_indptr[b] .. qo_indptr[b+1]; the cache already holds them (update_kv runs first,
+ * model.py:413-418), so token i of row b sits at kv_len_b - qo_len_b + i and attends
+ * tokens 0 .. that position.  lse [nnz, num_qo_heads] or NULL.  max_qo_len must be
+ * >= every qo_len_b (it sizes the grid).  No workspace. */
+int delta_paged_prefill(const void *q, int64_t q_stride_t, int64_t q_stride_h,
+                        const void *kv_cache, int64_t num_pages, const int32_t *qo_indptr,
+                        const int32_t *kv_indptr, const int32_t *kv_indices,
+                        int64_t kv_indices_len, const int32_t *kv_last_page_len, void *o,
+                        int64_t o_stride_t, int64_t o_stride_h, float *lse, int batch,
+                        int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                        float sm_scale, int max_qo_len, delta_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Page scoring (del3_legacy_softmax)                                         */
 /* ------------------------------------------------------------------------ */

@@ -273,6 +273,46 @@ def paged_decode_attention(q: torch.Tensor, kv_cache: torch.Tensor,
     return o, lse
 
 
+def paged_prefill_attention(q: torch.Tensor, qo_indptr: torch.Tensor, kv_cache: torch.Tensor,
+                            kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                            kv_last_page_len: torch.Tensor, sm_scale: float,
+                            compute_dtype: torch.dtype = torch.float64
+                            ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Causal attention of several query tokens per row over a paged CSR; (o, lse) fp32.
+
+    The FlashInfer paged prefill the reference plans with ``causal=True``
+    (backend.py:1091-1105) for rows with ``qo_len_b = qo_indptr[b+1] - qo_indptr[b]``
+    query tokens: the KV cache already holds the row's new tokens (update_kv runs
+    before attention, model.py:413-418), so query i of row b sits at position
+    ``kv_len_b - qo_len_b + i`` and attends the tokens ``0 .. position``.
+    ``q`` is ``[nnz, Hq, d]`` with rows ``qo_indptr[b] ..``.
+    """
+    nnz, Hq, d = q.shape
+    Hkv = kv_cache.shape[3]
+    G = Hq // Hkv
+    o = torch.zeros((nnz, Hq, d), dtype=torch.float32)
+    lse = torch.full((nnz, Hq), float("-inf"), dtype=torch.float32)
+    for b in range(len(qo_indptr) - 1):
+        q0, q1 = int(qo_indptr[b]), int(qo_indptr[b + 1])
+        if q1 <= q0:
+            continue
+        k, v = gather_row_kv(kv_cache, kv_indptr, kv_indices, kv_last_page_len, b)
+        n = k.shape[0]
+        kk = k.to(compute_dtype).repeat_interleave(G, dim=1)
+        vv = v.to(compute_dtype).repeat_interleave(G, dim=1)
+        s = torch.einsum("ihd,nhd->ihn", q[q0:q1].to(compute_dtype), kk) * float(sm_scale)  # [qo, Hq, n]
+        pos = n - (q1 - q0) + torch.arange(q1 - q0)
+        mask = torch.arange(n)[None, :] > pos[:, None]                                   # [qo, n]
+        s = s.masked_fill(mask[:, None, :], float("-inf"))
+        m = s.amax(dim=-1, keepdim=True)
+        ok = torch.isfinite(m)
+        e = torch.where(ok, torch.exp(s - torch.where(ok, m, 0.0)), 0.0)
+        den = e.sum(dim=-1, keepdim=True)
+        o[q0:q1] = torch.where(den > 0, torch.einsum("ihn,nhd->ihd", e, vv) / den.clamp_min(1e-300), 0.0).to(torch.float32)
+        lse[q0:q1] = torch.where(den > 0, m + torch.log(den.clamp_min(1e-300)), float("-inf")).squeeze(-1).to(torch.float32)
+    return o, lse
+
+
 # ---------------------------------------------------------------------------
 # Host/device metadata helpers
 # ---------------------------------------------------------------------------

@@ -188,6 +188,35 @@ def test_prefill_rows_are_causal():
     assert_close(o, ref, "prefill layer 0")
 
 
+def test_two_row_prefill_step_matches_oracle():
+    """One eager prompt step for two rows of different lengths: layer 0's attention output
+    equals the oracle's causal prefill over each row's own pages."""
+    eng = make_engine(B=2, max_len=256)
+    for layer in eng.model.layers:
+        layer.attention.record = []
+    prompts = [torch.arange(1, 24), torch.arange(30, 39)]
+    eng.add_requests(prompts, [60, 60], [])
+    with torch.inference_mode():  # the first iteration of run_scheduler_loop
+        new_slots, new_reqs = eng.scheduler.schedule_requests()
+        for slot_id, req in zip(new_slots, new_reqs):
+            req.initialize_pages(slot_id, eng.pages_per_slot)
+            eng.slot_block_table[slot_id].fill_(int(eng.scratch_pages[slot_id]))
+            eng._sync_slot_block_table(slot_id, req, 0)
+        eng._forward(1)
+    torch.cuda.synchronize()
+    (q, o), = eng.model.layers[0].attention.record[:1]
+    cache = eng.model.layers[0].attention.kv_cache.kv_cache.cpu()
+    reqs = [eng.scheduler.request_queue[int(eng.scheduler.runner_slots[s])] for s in new_slots]
+    lens = [len(p) for p in prompts]
+    pages = [r.page_indices[:(n + 15) // 16] for r, n in zip(reqs, lens)]
+    ip = torch.tensor([0, len(pages[0]), len(pages[0]) + len(pages[1])], dtype=torch.int32)
+    ind = torch.tensor(pages[0] + pages[1], dtype=torch.int32)
+    last = torch.tensor([n - ((n + 15) // 16 - 1) * 16 for n in lens], dtype=torch.int32)
+    qo_indptr = torch.tensor([0, lens[0], lens[0] + lens[1]], dtype=torch.int32)
+    ref, _ = O.paged_prefill_attention(q.cpu(), qo_indptr, cache, ip, ind, last, 1 / 128 ** 0.5)
+    assert_close(o, ref, "two-row prefill layer 0")
+
+
 def test_fused_dense_path_matches_reference_structure():
     """The fused element-wise kernels give the same logits as the reference's op-by-op blocks."""
     eng = make_engine(B=3)

@@ -487,3 +487,27 @@ def test_rope_append_equals_rope_then_append(llama31):
     torch.cuda.synchronize()
     assert torch.equal(q1, q2)
     assert torch.equal(cache, cache2)
+
+
+@pytest.mark.parametrize("hq,hkv,dtype", [(32, 8, torch.bfloat16), (28, 4, torch.bfloat16), (8, 8, torch.float16),
+                                          (40, 8, torch.bfloat16), (16, 2, torch.float16)])
+def test_paged_prefill_matches_oracle(hq, hkv, dtype):
+    """Causal prefill (several query tokens per row) against the oracle: ragged rows, a row
+    with one query token, a prompt longer than one block of waves, shuffled pages."""
+    kv_lens = [70, 16, 300, 33]
+    qo = [37, 1, 300, 9]
+    c = make_case(batch=4, hq=hq, hkv=hkv, kv_lens=kv_lens, seed=31, page_order="randperm", k=4, L=2,
+                  dtype=dtype)
+    gen = torch.Generator().manual_seed(32)
+    nnz = sum(qo)
+    q = torch.randn(nnz, hq, 128, generator=gen).to(dtype)
+    qo_indptr = torch.tensor([0] + list(torch.cumsum(torch.tensor(qo), 0)), dtype=torch.int32)
+    g = gpu(c)
+    lse = torch.empty(nnz, hq, device=DEV)
+    o = K.paged_prefill(q.to(DEV), g.kv_cache, qo_indptr.to(DEV), g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                        max_qo_len=max(qo), lse=lse)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = O.paged_prefill_attention(q, qo_indptr, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                               c.kv_last_page_len, c.sm_scale)
+    assert_attn_close(o, o_ref, f"prefill G={hq // hkv}")
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)

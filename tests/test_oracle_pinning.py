@@ -279,6 +279,49 @@ def test_attention_matches_sdpa():
         assert torch.allclose(lse[b].double(), torch.logsumexp(s, -1), atol=1e-5)
 
 
+def virtual_decode_rows(qo_lens, kv_indptr, kv_indices, kv_last_page_len, page_size=16):
+    """One decode row per prefill query token, over its causal prefix (an independent
+    construction: page lists cut from the row's CSR, last_page_len from the position)."""
+    ip, ind, last = [0], [], []
+    for b, qo in enumerate(qo_lens):
+        n = int(O.kv_lengths(kv_indptr[b:b + 2], kv_last_page_len[b:b + 1], page_size)[0])
+        pages = kv_indices[int(kv_indptr[b]):int(kv_indptr[b + 1])].tolist()
+        for i in range(qo):
+            pos = n - qo + i
+            npg = pos // page_size + 1
+            ind.extend(pages[:npg])
+            ip.append(len(ind))
+            last.append(pos % page_size + 1)
+    return (torch.tensor(ip, dtype=torch.int32), torch.tensor(ind, dtype=torch.int32),
+            torch.tensor(last, dtype=torch.int32))
+
+
+def test_prefill_equals_causal_virtual_rows():
+    """Causal prefill == one decode row per query token over its prefix, and == decode when
+    every row has one query token."""
+    c = tiny_case(seed=12, B=3, hq=8, hkv=2, lens=(40, 17, 64))
+    qo = [5, 1, 16]
+    gen = torch.Generator().manual_seed(3)
+    q = torch.randn(sum(qo), 8, 128, generator=gen, dtype=torch.float64)
+    qo_indptr = torch.tensor([0, 5, 6, 22], dtype=torch.int32)
+    o, lse = O.paged_prefill_attention(q, qo_indptr, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.088)
+    vip, vind, vlast = virtual_decode_rows(qo, c.kv_indptr, c.kv_indices, c.kv_last_page_len)
+    o2, lse2 = O.paged_decode_attention(q, c.kv_cache, vip, vind, vlast, 0.088)
+    assert torch.allclose(o, o2, atol=1e-6) and torch.allclose(lse, lse2, atol=1e-6)
+    # first query of row 0 (position 35) must not see token 36+: changing them leaves it unchanged
+    cache = c.kv_cache.clone()
+    pages0 = c.kv_indices[int(c.kv_indptr[0]):int(c.kv_indptr[1])].long()
+    cache[pages0[2], :, 4:] += 100.0  # tokens 36..47 of row 0
+    o3, _ = O.paged_prefill_attention(q, qo_indptr, cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.088)
+    assert torch.equal(o3[0], o[0]) and not torch.allclose(o3[4], o[4])
+    # one query per row: exactly the decode attention
+    q1 = q[[4, 5, 21]]
+    o4, lse4 = O.paged_prefill_attention(q1, torch.arange(4, dtype=torch.int32), c.kv_cache, c.kv_indptr,
+                                         c.kv_indices, c.kv_last_page_len, 0.088)
+    o5, lse5 = O.paged_decode_attention(q1, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, 0.088)
+    assert torch.allclose(o4, o5, atol=1e-7) and torch.allclose(lse4, lse5, atol=1e-7)
+
+
 def test_sparse_equals_full_when_all_pages_selected():
     c = tiny_case(seed=10, B=2, lens=(40, 70))
     res = O.selective_step(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, k=5, L=2)

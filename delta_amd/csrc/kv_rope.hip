@@ -98,7 +98,10 @@ struct RopeArgs {
 constexpr int kPairs = kHeadDim / 2;
 
 // (cos, sin) of pos * f_j for the 64 pairs j, into tab[2 j], tab[2 j + 1] (threads 0..63).
+// Contraction is off in both helpers: every kernel that inlines them then rounds each product
+// and sum the same way, so the fused and unfused launches give identical bits.
 __device__ __forceinline__ void rope_table(const RopeArgs &a, float pos, float *tab) {
+#pragma clang fp contract(off)
   const int j = threadIdx.x;
   if (j < kPairs) {
     float f = exp2f(-(2.0f * (float)j / (float)kHeadDim) * a.log2_theta);  // theta^(-2j/d)
@@ -113,6 +116,7 @@ __device__ __forceinline__ void rope_table(const RopeArgs &a, float pos, float *
 
 template <int DT>
 __device__ __forceinline__ uint32_t rope_pair(uint32_t pr, const float *tab, int j) {
+#pragma clang fp contract(off)
   using E = Elem<DT>;
   const float cs = tab[2 * j], sn = tab[2 * j + 1];
   const float x0 = E::lo(pr), x1 = E::hi(pr);
@@ -192,6 +196,93 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeArgs r, AppendArgs
   if (pid >= 0) {
     for (int ch = threadIdx.x; ch < a.hkv * (kHeadDim / 8); ch += blockDim.x)
       st128(vdst + 8 * ch, ld128(a.v + (int64_t)i * a.v_stride + 8 * ch));
+  }
+}
+
+
+// The same fused RoPE + append for 16-byte aligned q, k, v and q_out (the decode layer's
+// case), arranged for latency: the token's q, k and v are loaded first (they are addressed by
+// the token index alone), the row is found with one parallel probe of the append indptr
+// (thread t tests indptr[t] <= i < indptr[t + 1]) instead of a binary search, so the chain
+// of dependent loads is indptr -> (offsets, kv_indptr, last_page_len) -> kv_indices.  The
+// arithmetic per element is rope_append_kernel's, so both give identical bits.
+constexpr int kRopeThreads = 256;
+constexpr int kRopePre = 3;  // 16-byte q/k chunks per thread loaded ahead (40 heads at 256 threads)
+
+template <int DT>
+__global__ void __launch_bounds__(kRopeThreads) rope_append_vec_kernel(RopeArgs r, AppendArgs a) {
+  __shared__ float tab[2 * kPairs];
+  __shared__ int row_s;
+  const int i = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nqk = (r.hq + r.hkv) * (kHeadDim / 8);
+  const int nv = a.hkv * (kHeadDim / 8);
+  auto qk_src = [&](int u) {
+    const int head = u >> 4, c = u & 15;
+    return head < r.hq ? r.q + (int64_t)i * r.q_stride + (int64_t)head * kHeadDim + 8 * c
+                       : r.k + (int64_t)i * r.k_stride + (int64_t)(head - r.hq) * kHeadDim + 8 * c;
+  };
+  u32x4 pre[kRopePre];
+#pragma unroll
+  for (int c = 0; c < kRopePre; ++c) {
+    const int u = tid + kRopeThreads * c;
+    if (u < nqk) pre[c] = ld128(qk_src(u));
+  }
+  const u32x4 v0 = tid < nv ? ld128(a.v + (int64_t)i * a.v_stride + 8 * tid) : u32x4{0u, 0u, 0u, 0u};
+
+  if (tid == 0) row_s = -1;
+  __syncthreads();
+  for (int t = tid; t < a.batch; t += kRopeThreads)
+    if (a.append_indptr[t] <= i && i < a.append_indptr[t + 1]) row_s = t;
+  __syncthreads();
+  // A token outside every row (malformed indptr) takes the binary search's row, as the
+  // unfused kernels do.
+  const int b = row_s >= 0 ? row_s : find_row(a.append_indptr, a.batch, i);
+  const int a0 = a.append_indptr[b];
+  const float pos = (float)(r.offsets[b] + (i - a0));
+  const int alen = a.append_indptr[b + 1] - a0;
+  const int64_t p0 = a.kv_indptr[b], p1 = a.kv_indptr[b + 1];
+  int pid = -1, slot = 0;
+  if (i >= a0 && i - a0 < alen && p0 >= 0 && p1 >= p0 && p1 <= a.kv_indices_len) {
+    const int np = (int)(p1 - p0);
+    int lp = a.last_page_len[b];
+    lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+    const int seq = np > 0 ? (np - 1) * kPageSize + lp : lp;
+    const int apos = seq - alen + (i - a0);
+    if (apos >= 0 && apos / kPageSize < np) {
+      const int p = a.kv_indices[p0 + apos / kPageSize];
+      if (p >= 0 && (int64_t)p < a.num_pages) {
+        pid = p;
+        slot = apos % kPageSize;
+      }
+    }
+  }
+  rope_table(r, pos, tab);
+  const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
+  uint16_t *kdst = a.cache + (((int64_t)(pid < 0 ? 0 : pid) * 2 + 0) * kPageSize + slot) * row_elems;
+  uint16_t *vdst = a.cache + (((int64_t)(pid < 0 ? 0 : pid) * 2 + 1) * kPageSize + slot) * row_elems;
+  __syncthreads();
+
+  auto rotate_store = [&](int u, u32x4 x) {
+    const int head = u >> 4, c = u & 15;
+    u32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = rope_pair<DT>(x[e], tab, 4 * c + e);
+    if (head < r.hq)
+      st128(r.q_out + (int64_t)i * r.q_out_stride + (int64_t)head * kHeadDim + 8 * c, y);
+    else if (pid >= 0)
+      st128(kdst + (int64_t)(head - r.hq) * kHeadDim + 8 * c, y);
+  };
+#pragma unroll
+  for (int c = 0; c < kRopePre; ++c) {
+    const int u = tid + kRopeThreads * c;
+    if (u < nqk) rotate_store(u, pre[c]);
+  }
+  for (int u = tid + kRopeThreads * kRopePre; u < nqk; u += kRopeThreads) rotate_store(u, ld128(qk_src(u)));
+  if (pid >= 0) {
+    if (tid < nv) st128(vdst + 8 * tid, v0);
+    for (int u = tid + kRopeThreads; u < nv; u += kRopeThreads)
+      st128(vdst + 8 * u, ld128(a.v + (int64_t)i * a.v_stride + 8 * u));
   }
 }
 
@@ -344,7 +435,13 @@ extern "C" DELTA_EXPORT int delta_rope_append(const void *q, int64_t q_stride, c
   a.last_page_len = kv_last_page_len;
   a.batch = batch;
   a.hkv = num_kv_heads;
-  if (dtype == DELTA_BF16)
+  const bool vec = !(((uintptr_t)q | (uintptr_t)k | (uintptr_t)q_out) & 15u) && !(q_stride % 8) &&
+                   !(k_stride % 8) && !(q_out_stride % 8);
+  if (vec && dtype == DELTA_BF16)
+    hipLaunchKernelGGL(rope_append_vec_kernel<DELTA_BF16>, dim3(nnz), dim3(kRopeThreads), 0, (hipStream_t)stream, r, a);
+  else if (vec)
+    hipLaunchKernelGGL(rope_append_vec_kernel<DELTA_FP16>, dim3(nnz), dim3(kRopeThreads), 0, (hipStream_t)stream, r, a);
+  else if (dtype == DELTA_BF16)
     hipLaunchKernelGGL(rope_append_kernel<DELTA_BF16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, r, a);
   else
     hipLaunchKernelGGL(rope_append_kernel<DELTA_FP16>, dim3(nnz), dim3(256), 0, (hipStream_t)stream, r, a);

@@ -290,10 +290,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         // uniform part: first page of instruction q's slots
         const int jq = first + R * (gi0 + q * kSpi);
         float *dst = reinterpret_cast<float *>(reinterpret_cast<char *>(dump_row + (int64_t)jq * kPageSize) + f_dst);
-        dst[0] = v[0];
-        dst[1] = v[1];
-        dst[2] = v[2];
-        dst[3] = v[3];
+        // Streaming store: the scorer reads the dump once, from another kernel.
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(dst));
       }
     }
     okmask = 0;

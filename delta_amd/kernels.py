@@ -443,8 +443,8 @@ def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_append_ind
         raise ValueError("q must be [nnz, Hq, 128] with contiguous heads")
     for name, t in (("k", k), ("v", v)):
         if t.dim() != 3 or t.shape[1] != hkv or t.shape[2] != HEAD_DIM or t.stride(2) != 1 \
-                or t.stride(1) != HEAD_DIM or t.stride(0) % 8 or t.shape[0] != q.shape[0]:
-            raise ValueError(f"{name} must be [nnz, {hkv}, 128] with contiguous heads")
+                or t.stride(1) != HEAD_DIM or (name == "v" and t.stride(0) % 8) or t.shape[0] != q.shape[0]:
+            raise ValueError(f"{name} must be [nnz, {hkv}, 128] with contiguous heads (v rows 16-byte aligned)")
         if t.dtype != kv_cache.dtype or q.dtype != kv_cache.dtype:
             raise TypeError("q, k, v and kv_cache must share a dtype")
     q_out = torch.empty_like(q) if q_out is None else q_out

@@ -455,14 +455,18 @@ def test_gemm_skinny_matches_fp32_reference(dtype, M, N, Kd, bias):
     assert torch.equal(out, K.gemm_skinny(x, w, b))
 
 
-@pytest.mark.parametrize("llama31", [False, True])
-def test_rope_append_equals_rope_then_append(llama31):
+@pytest.mark.parametrize("llama31,hq,hkv,dtype,misalign,qo", [
+    (False, 16, 4, torch.bfloat16, False, [1, 2, 1, 1]),
+    (True, 16, 4, torch.bfloat16, False, [1, 2, 1, 1]),
+    (True, 64, 8, torch.float16, False, [1, 0, 2, 1]),   # > 3 chunks per thread; an empty row
+    (False, 40, 8, torch.bfloat16, True, [2, 1, 0, 1]),  # 4-byte aligned q/k: the pairwise kernel
+])
+def test_rope_append_equals_rope_then_append(llama31, hq, hkv, dtype, misalign, qo):
     """The fused launch writes the same q and the same cache bytes as delta_rope followed by
-    delta_append_kv (same per-element arithmetic), including a 2-token append and a row whose
-    append lands on a fresh page."""
+    delta_append_kv (same per-element arithmetic), including a 2-token append, a row whose
+    append lands on a fresh page and a row with nothing to append."""
     gen = torch.Generator().manual_seed(21)
-    hq, hkv, B = 16, 4, 4
-    qo = [1, 2, 1, 1]
+    B = len(qo)
     lens_after = [17, 33, 16, 300]  # tokens cached after the append
     pages = [(n + 15) // 16 for n in lens_after]
     num_pages = sum(pages) + 5
@@ -472,10 +476,12 @@ def test_rope_append_equals_rope_then_append(llama31):
     app = torch.tensor([0] + list(torch.cumsum(torch.tensor(qo), 0)), dtype=torch.int32)
     offsets = torch.tensor([n - a for n, a in zip(lens_after, qo)], dtype=torch.int32)
     nnz = sum(qo)
-    qkv = torch.randn(nnz, (hq + 2 * hkv) * 128, generator=gen).to(torch.bfloat16).to(DEV)
-    q, k, v = qkv.split([hq * 128, hkv * 128, hkv * 128], dim=-1)
+    pad = 2 if misalign else 0
+    qk = torch.randn(nnz, pad + (hq + hkv) * 128, generator=gen).to(dtype).to(DEV)
+    q, k = qk[:, pad:].split([hq * 128, hkv * 128], dim=-1)
+    v = torch.randn(nnz, hkv * 128, generator=gen).to(dtype).to(DEV)
     q, k, v = q.view(nnz, hq, 128), k.view(nnz, hkv, 128), v.view(nnz, hkv, 128)
-    cache = torch.randn(num_pages, 2, 16, hkv, 128, generator=gen).to(torch.bfloat16).to(DEV)
+    cache = torch.randn(num_pages, 2, 16, hkv, 128, generator=gen).to(dtype).to(DEV)
     cache2 = cache.clone()
     p = dict(rope_scale=8.0 if llama31 else 1.0, rope_theta=5e5)
     if llama31:

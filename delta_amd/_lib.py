@@ -14,6 +14,18 @@ DELTA_BF16 = 0
 DELTA_FP16 = 1
 
 _P = c_void_p
+
+
+class DecodeAppendC(ctypes.Structure):
+    """``delta_decode_append_t``: the new decode token's RoPE + KV append."""
+    _fields_ = [("k", c_void_p), ("k_stride", c_int64), ("v", c_void_p), ("v_stride", c_int64),
+                ("offsets", c_void_p), ("kv_indptr", c_void_p), ("kv_indices", c_void_p),
+                ("kv_indices_len", c_int64), ("rope_scale", c_float), ("rope_theta", c_float),
+                ("llama31", c_int), ("low_freq_factor", c_float), ("high_freq_factor", c_float),
+                ("old_context_len", c_float)]
+
+
+_AP = ctypes.POINTER(DecodeAppendC)
 # name -> (restype, argtypes); one entry per function declared in include/delta_hip.h
 SIGNATURES = {
     "delta_last_error": (ctypes.c_char_p, []),
@@ -32,6 +44,12 @@ SIGNATURES = {
         c_int, c_int, c_int, c_int, c_int,    # batch, hq, hkv, head_dim, dtype
         c_float, c_int,                       # sm_scale, max_pages_per_row
         _P, c_size_t, _P]),                   # workspace, bytes, stream
+    "delta_paged_decode_append": (c_int, [
+        _AP, _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int64,
+        c_int64, c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),
+    "delta_paged_decode_subset_append": (c_int, [
+        _AP, _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P,
+        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),
     "delta_paged_decode_subset": (c_int, [
         _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P,
         c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),

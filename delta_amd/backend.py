@@ -228,32 +228,46 @@ class LMBackend:
     def _decode_mode(self) -> bool:
         return self._step is not None and self._step.mode == "decode"
 
-    def attn_full(self, q, kv_cache):
+    def decode_append_ok(self) -> bool:
+        """Decode steps (one new token per row) fuse RoPE and the KV append into the attention."""
+        return self._decode_mode()
+
+    def attn_append(self, role, q, k, v, offsets, kv_cache, ap_indices, ap_indptr):
+        """A decode layer's attention with the new token's RoPE and KV append in the same launch
+        (model.py:413-418 rope -> update_kv -> attention op); q, k are un-rotated."""
+        ap = K.DecodeAppend(k, v, offsets, ap_indptr, ap_indices, **self.rope_params())
+        if role == "subset":
+            return self.attn_subset(q, kv_cache, append=ap)
+        if role == "plan":
+            return self.attn_plan(q, kv_cache, append=ap)
+        return self.attn_full(q, kv_cache, append=ap)
+
+    def attn_full(self, q, kv_cache, append=None):
         st = self._step
         if st.mode == "prefill":  # several query tokens per row: causal prefill kernel
             return K.paged_prefill(q, kv_cache, st.qo_indptr, st.kv_indptr, st.kv_indices, st.kv_last,
                                    max_qo_len=st.max_qo)
         return K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                              max_pages_per_row=st.max_pages, workspace=self.workspace)
+                              max_pages_per_row=st.max_pages, workspace=self.workspace, append=append)
 
-    def attn_subset(self, q, kv_cache):
+    def attn_subset(self, q, kv_cache, append=None):
         if not (self.enable_selective_cache and self._decode_mode()):
-            return self.attn_full(q, kv_cache)
+            return self.attn_full(q, kv_cache, append=append)
         sel = self.page_selector
         return K.paged_decode(q, kv_cache, sel.paged_subset_kv_indptr, sel.paged_subset_kv_indices,
                               self._step.kv_last, max_pages_per_row=self.k_eff, workspace=self.workspace,
-                              subset=True)
+                              subset=True, append=append)
 
-    def attn_plan(self, q, kv_cache):
+    def attn_plan(self, q, kv_cache, append=None):
         """Planner layer: full attention + logits dump, page scores, v2 selection into the subset CSR."""
         if not (self.enable_selective_cache and self._decode_mode()):
-            return self.attn_full(q, kv_cache)
+            return self.attn_full(q, kv_cache, append=append)
         st = self._step
         sel = self.page_selector
         B = q.shape[0]
         o = K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
                            max_pages_per_row=st.max_pages, lse=self.lse, logits_dump=self.dump,
-                           workspace=self.workspace)
+                           workspace=self.workspace, append=append)
         K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
                                   scores=self.page_scores, batch=B, workspace=self.workspace)
         K.select_pages(self.page_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,

@@ -133,4 +133,36 @@ __device__ __forceinline__ int wave_prefix_exclusive(bool flag, int *total) {
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------------------
+// Interleaved RoPE (FlashInfer apply_rope / apply_llama31_rope, interleave=True):
+// pair (2j, 2j+1) of a head rotates by pos * f_j, f_j = theta^(-2j/128) / rope_scale, or
+// for Llama 3.1 the blend (1 - s) f_j / rope_scale + s f_j with
+// s = clamp(f_j * smooth_a + smooth_b, 0, 1).  Every kernel that rotates (the RoPE kernels
+// and the fused decode attention) calls these two, with contraction off, so each product
+// and sum rounds the same way everywhere and the launches agree bit for bit.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void rope_cos_sin(int j, float pos, float rcp_scale, float log2_theta, float smooth_a,
+                                             float smooth_b, float *cs_sn) {
+#pragma clang fp contract(off)
+  float f = exp2f(-(2.0f * (float)j / (float)kHeadDim) * log2_theta);  // theta^(-2j/d)
+  const float s = fminf(fmaxf(f * smooth_a + smooth_b, 0.f), 1.f);
+  f = (1.f - s) * (f * rcp_scale) + s * f;
+  float sn, cs;
+  sincosf(pos * f, &sn, &cs);
+  cs_sn[0] = cs;
+  cs_sn[1] = sn;
+}
+
+// Rotates one packed pair by (cos, sin) = (cs_sn[0], cs_sn[1]); fp32 math, one rounding.
+template <int DT>
+__device__ __forceinline__ uint32_t rope_rotate(uint32_t pr, const float *cs_sn) {
+#pragma clang fp contract(off)
+  using E = Elem<DT>;
+  const float cs = cs_sn[0], sn = cs_sn[1];
+  const float x0 = E::lo(pr), x1 = E::hi(pr);
+  const float y0 = x0 * cs - x1 * sn;
+  const float y1 = x1 * cs + x0 * sn;
+  return E::from_float(y0) | (E::from_float(y1) << 16);
+}
+
 }  // namespace delta

@@ -98,31 +98,14 @@ struct RopeArgs {
 constexpr int kPairs = kHeadDim / 2;
 
 // (cos, sin) of pos * f_j for the 64 pairs j, into tab[2 j], tab[2 j + 1] (threads 0..63).
-// Contraction is off in both helpers: every kernel that inlines them then rounds each product
-// and sum the same way, so the fused and unfused launches give identical bits.
 __device__ __forceinline__ void rope_table(const RopeArgs &a, float pos, float *tab) {
-#pragma clang fp contract(off)
   const int j = threadIdx.x;
-  if (j < kPairs) {
-    float f = exp2f(-(2.0f * (float)j / (float)kHeadDim) * a.log2_theta);  // theta^(-2j/d)
-    const float s = fminf(fmaxf(f * a.smooth_a + a.smooth_b, 0.f), 1.f);
-    f = (1.f - s) * (f * a.rcp_scale) + s * f;
-    float sn, cs;
-    sincosf(pos * f, &sn, &cs);
-    tab[2 * j] = cs;
-    tab[2 * j + 1] = sn;
-  }
+  if (j < kPairs) rope_cos_sin(j, pos, a.rcp_scale, a.log2_theta, a.smooth_a, a.smooth_b, tab + 2 * j);
 }
 
 template <int DT>
 __device__ __forceinline__ uint32_t rope_pair(uint32_t pr, const float *tab, int j) {
-#pragma clang fp contract(off)
-  using E = Elem<DT>;
-  const float cs = tab[2 * j], sn = tab[2 * j + 1];
-  const float x0 = E::lo(pr), x1 = E::hi(pr);
-  const float y0 = x0 * cs - x1 * sn;
-  const float y1 = x1 * cs + x0 * sn;
-  return E::from_float(y0) | (E::from_float(y1) << 16);
+  return rope_rotate<DT>(pr, tab + 2 * j);
 }
 
 template <int DT>

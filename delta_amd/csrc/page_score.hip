@@ -24,7 +24,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
                int64_t o_stride_b, int64_t o_stride_h, float *lse, float *dump,
                int64_t dump_stride_b, int64_t dump_stride_h, int batch, int hq, int hkv,
                int head_dim, int dtype, float sm_scale, int max_pages, int mode,
-               void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who);
+               void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who,
+               const delta_decode_append_t *ap);
 int decode_num_splits(int batch, int hkv, int max_pages);
 size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc);
 
@@ -191,7 +192,7 @@ extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, 
   int rc = run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
                       kv_last_page_len, nullptr, 0, 0, lse_ws, logits_dump, dump_stride_b, dump_stride_h, batch,
                       num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale, max_pages, /*kScoreOnly*/ 2, workspace,
-                      dec, st, who);
+                      dec, st, who, nullptr);
   if (rc) return rc;
   return launch_scores(logits_dump, dump_stride_b, dump_stride_h, lse_ws, kv_indptr, kv_last_page_len, scores,
                        score_stride, batch, num_qo_heads, max_pages, st, who);

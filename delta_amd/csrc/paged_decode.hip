@@ -53,6 +53,19 @@ struct DecodeArgs {
   int chunk;        // pages per work unit (split launches)
   int hb;           // kv heads per block (hkv: page-major, 1: head-major)
   float sm_scale;
+  // Decode steps with the new token's RoPE and KV append fused in (the *_append entry
+  // points): q is the un-rotated query, row b's new token (k_new, v_new rows b) sits at
+  // kv_len_b - 1 of the append CSR (ap_indptr / ap_indices, sharing last_page_len).
+  uint16_t *kv_w;   // the cache, writable
+  const uint16_t *k_new;
+  int64_t k_new_stride;
+  const uint16_t *v_new;
+  int64_t v_new_stride;
+  const int32_t *offsets;  // [batch] the new token's position (rotation angle)
+  const int32_t *ap_indptr;
+  const int32_t *ap_indices;
+  int64_t ap_indices_len;
+  float rcp_scale, log2_theta, smooth_a, smooth_b;
 };
 
 struct RowInfo {
@@ -179,7 +192,7 @@ __device__ __forceinline__ float rows4_sum(float v) {
 //         B = V from a padded LDS tile whose row 4c + r holds token tok(r), read with
 //         ds_read_b64_tr_b16 (lane (c, j) gets tile rows 4c..4c+3 at d = 16n + j),
 //         D = O[g = 4c + r][d = 16n + lane%16].
-template <int DT, int G, bool WITH_V, bool WITH_DUMP>
+template <int DT, int G, bool WITH_V, bool WITH_DUMP, bool ROPE>
 __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
   // No FMA contraction: every instantiation (with or without the dump) rounds the softmax
   // arguments identically, so P -- rounded to the KV dtype for the P.V MFMA -- is the same.
@@ -225,6 +238,71 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     qf[1] = ld128(qp + 64);
   } else {
     qf[0] = qf[1] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // Fused RoPE + append of the row's new token (ROPE), done before the page stream starts: its
+  // few dependent loads (position, the token's k and v, the append slot's page id) then do not
+  // queue behind the page loads (measured: 2 us faster than after the first page's loads).
+  int ap_pid = -1, ap_slot = 0;
+  uint32_t kraw = 0u, vraw = 0u;
+  float rpos = 0.f;
+  if (ROPE) {
+    const int i = threadIdx.x;
+    if (i < hb * (kHeadDim / 2)) {
+      const int64_t e = (int64_t)(head0 + (i >> 6)) * kHeadDim + 2 * (i & 63);
+      kraw = *reinterpret_cast<const uint32_t *>(a.k_new + (int64_t)b * a.k_new_stride + e);
+      vraw = *reinterpret_cast<const uint32_t *>(a.v_new + (int64_t)b * a.v_new_stride + e);
+    }
+    rpos = (float)a.offsets[b];
+    // The append slot, with delta_append_kv's checks (a row without a valid slot appends
+    // nothing); the page id is checked where it is first needed.
+    const int64_t q0 = a.ap_indptr[b], q1 = a.ap_indptr[b + 1];
+    if (q0 >= 0 && q1 > q0 && q1 <= a.ap_indices_len) {
+      int lp = a.last_page_len[b];
+      lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+      const int tp = (int)(q1 - q0 - 1) * kPageSize + lp - 1;  // the new token's position
+      if (tp >= 0) {
+        ap_pid = a.ap_indices[q0 + tp / kPageSize];
+        ap_slot = tp % kPageSize;
+      }
+    }
+  }
+
+  // The token's (cos, sin) table, its rotated k and its v for the block's hb heads go to LDS
+  // past the V tiles and the dump staging; q is rotated in registers; one block per (row, kv
+  // head group) writes k and v into the cache slot, and the wave that attends that page takes
+  // the token's K and V from LDS (whatever the cache held there when the page was read).  Same
+  // rounding as delta_rope_append.
+  const int rope_off = (WITH_V ? nw * kVTile / 2 : 0) + (WITH_DUMP ? nw * dump_slots<G, WITH_V>() * G * kPageSize : 0);
+  float *const rtab = smem + rope_off;                                              // [64][cos, sin]
+  uint32_t *const knew = reinterpret_cast<uint32_t *>(smem + rope_off + kHeadDim);  // [hb][64] rotated k pairs
+  uint32_t *const vnew = knew + hb * (kHeadDim / 2);                                // [hb][64] v pairs
+  if (ROPE) {
+    const int i = threadIdx.x;
+    if (ap_pid >= (int64_t)a.num_pages) ap_pid = -1;
+    if (i < kHeadDim / 2) rope_cos_sin(i, rpos, a.rcp_scale, a.log2_theta, a.smooth_a, a.smooth_b, rtab + 2 * i);
+    __syncthreads();
+    if (i < hb * (kHeadDim / 2)) {
+      knew[i] = rope_rotate<DT>(kraw, rtab + 2 * (i & 63));
+      vnew[i] = vraw;
+    }
+    if ((t & 7) < G) {
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) qf[sp][w] = rope_rotate<DT>(qf[sp][w], rtab + 2 * (32 * sp + 16 * (t >> 3) + 4 * c + w));
+    }
+    __syncthreads();
+    if (ap_pid >= 0 && (a.nsplit == 1 || split == 0)) {
+      for (int ch = threadIdx.x; ch < 2 * hb * (kHeadDim / 8); ch += blockDim.x) {
+        const int which = ch >= hb * (kHeadDim / 8);  // 0 = K, 1 = V
+        const int r = which ? ch - hb * (kHeadDim / 8) : ch;
+        const uint32_t *src = (which ? vnew : knew) + 4 * r;  // head r / 16, 16-byte chunk r % 16
+        uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
+                        (int64_t)head0 * kHeadDim + 8 * r;
+        st128(dst, *reinterpret_cast<const u32x4 *>(src));
+      }
+    }
   }
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
@@ -321,6 +399,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       const bool more = c0 + it + 1 < count;
       const int pidn = it + 1 < cn ? __builtin_amdgcn_readlane(ids, it + 1) : __builtin_amdgcn_readlane(ids_next, 0);
       const uint16_t *nbase = page_ptr(pidn);
+      if (ROPE && ok && pid == ap_pid) {
+        // The new token's row of this page: K lanes with t / 2 == slot % 8 in steps
+        // 2 (slot / 8) + sp, V lanes with c == slot % 4 in tile row group slot / 4.
+        const int hl = h - head0;
+        if ((t >> 1) == (ap_slot & 7)) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            if ((s >> 1) == (ap_slot >> 3))
+              kf[s] = *reinterpret_cast<const u32x4 *>(knew + hl * (kHeadDim / 2) + 32 * (s & 1) + 16 * (t & 1) + 4 * c);
+        }
+        if (WITH_V && c == (ap_slot & 3)) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (i == (ap_slot >> 2)) vf[i] = *reinterpret_cast<const u32x4 *>(vnew + hl * (kHeadDim / 2) + 4 * t);
+        }
+      }
 
       if (WITH_V) {
         // Stage this page's V (loaded one iteration ago) before anything else, so the wait at
@@ -476,25 +570,26 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
 //   full  = target_decode (full CSR), subset = target_subset_decode (selected
 //   pages), plan = target_decode_plan (full CSR + logits dump),
 //   score = the standalone K-only scorer.
-template <int DT, int G>
+//   ROPE = the new decode token's RoPE and KV append fused in (the *_append entry points).
+template <int DT, int G, bool ROPE>
 __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_full_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
-  decode_split_body<DT, G, true, false>(a, smem);
+  decode_split_body<DT, G, true, false, ROPE>(a, smem);
 }
-template <int DT, int G>
+template <int DT, int G, bool ROPE>
 __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_subset_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
-  decode_split_body<DT, G, true, false>(a, smem);
+  decode_split_body<DT, G, true, false, ROPE>(a, smem);
 }
-template <int DT, int G>
+template <int DT, int G, bool ROPE>
 __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_plan_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
-  decode_split_body<DT, G, true, true>(a, smem);
+  decode_split_body<DT, G, true, true, ROPE>(a, smem);
 }
 template <int DT, int G>
 __global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
-  decode_split_body<DT, G, false, true>(a, smem);
+  decode_split_body<DT, G, false, true, false>(a, smem);
 }
 
 // Combines the unit partials of one (row, q head): thread d of the block computes
@@ -559,22 +654,35 @@ template <int DT, int G>
 void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
   dim3 grid = a.nsplit > 1 ? dim3(a.batch * a.nsplit) : dim3(a.hkv / a.hb, a.batch);
   dim3 block(64 * waves);
+  const bool rope = a.k_new != nullptr;
   const size_t merge = (size_t)waves * G * (2 + kHeadDim) * sizeof(float);
   const size_t tiles = (size_t)waves * kVTile * sizeof(uint16_t);
   const size_t dumps = (size_t)waves * dump_slots<G, true>() * G * kPageSize * sizeof(float);
   const size_t dumps_score = (size_t)waves * dump_slots<G, false>() * G * kPageSize * sizeof(float);
-  const size_t sm_attn = merge > tiles ? merge : tiles;
-  const size_t sm_plan = merge > tiles + dumps ? merge : tiles + dumps;
+  // The fused append's LDS (past the tiles and the dump staging): the (cos, sin) table, then
+  // the rotated k and the v of the block's heads.
+  const size_t rope_lds = rope ? (size_t)(kHeadDim + a.hb * kHeadDim) * sizeof(float) : 0;
+  const size_t sm_attn = merge > tiles + rope_lds ? merge : tiles + rope_lds;
+  const size_t sm_plan = merge > tiles + dumps + rope_lds ? merge : tiles + dumps + rope_lds;
   const size_t sm_score = dumps_score > (size_t)waves * G * 2 * sizeof(float) ? dumps_score : (size_t)waves * G * 2 * sizeof(float);
   switch (mode) {
     case kAttn:
-      hipLaunchKernelGGL((paged_decode_full_kernel<DT, G>), grid, block, sm_attn, stream, a);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_full_kernel<DT, G, true>), grid, block, sm_attn, stream, a);
+      else
+        hipLaunchKernelGGL((paged_decode_full_kernel<DT, G, false>), grid, block, sm_attn, stream, a);
       break;
     case kAttnSubset:
-      hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G>), grid, block, sm_attn, stream, a);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G, true>), grid, block, sm_attn, stream, a);
+      else
+        hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G, false>), grid, block, sm_attn, stream, a);
       break;
     case kAttnDump:
-      hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G>), grid, block, sm_plan, stream, a);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, true>), grid, block, sm_plan, stream, a);
+      else
+        hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, false>), grid, block, sm_plan, stream, a);
       break;
     default:
       hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, sm_score, stream, a);
@@ -664,7 +772,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
                int64_t o_stride_b, int64_t o_stride_h, float *lse, float *dump,
                int64_t dump_stride_b, int64_t dump_stride_h, int batch, int hq, int hkv,
                int head_dim, int dtype, float sm_scale, int max_pages, int mode,
-               void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who) {
+               void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who,
+               const delta_decode_append_t *ap) {
   clear_error();
   if (batch <= 0) return DELTA_OK;
   if (head_dim != kHeadDim) return set_error(DELTA_ERR_INVALID, "%s: head_dim must be 128 (got %d)", who, head_dim);
@@ -718,6 +827,40 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.part_acc = nullptr;
   a.part_ml = nullptr;
   a.unit_start = nullptr;
+  a.kv_w = nullptr;
+  a.k_new = a.v_new = nullptr;
+  a.k_new_stride = a.v_new_stride = 0;
+  a.offsets = a.ap_indptr = a.ap_indices = nullptr;
+  a.ap_indices_len = 0;
+  a.rcp_scale = a.log2_theta = a.smooth_a = a.smooth_b = 0.f;
+  if (ap) {
+    if (mode == kScoreOnly) return set_error(DELTA_ERR_INVALID, "%s: the scorer takes no append", who);
+    if (!ap->k || !ap->v || !ap->offsets || !ap->kv_indptr || !ap->kv_indices)
+      return set_error(DELTA_ERR_INVALID, "%s: null append pointer", who);
+    if ((((uintptr_t)ap->k | (uintptr_t)ap->v) & 3u) || (ap->k_stride % 2) || (ap->v_stride % 2) ||
+        ap->k_stride < 0 || ap->v_stride < 0 || ap->kv_indices_len < 0)
+      return set_error(DELTA_ERR_INVALID, "%s: append k/v must be 4-byte aligned with even row strides", who);
+    if (!(ap->rope_scale > 0.f) || !(ap->rope_theta > 0.f))
+      return set_error(DELTA_ERR_INVALID, "%s: bad rope params", who);
+    a.kv_w = (uint16_t *)kv_cache;
+    a.k_new = (const uint16_t *)ap->k;
+    a.k_new_stride = ap->k_stride;
+    a.v_new = (const uint16_t *)ap->v;
+    a.v_new_stride = ap->v_stride;
+    a.offsets = ap->offsets;
+    a.ap_indptr = ap->kv_indptr;
+    a.ap_indices = ap->kv_indices;
+    a.ap_indices_len = ap->kv_indices_len;
+    a.rcp_scale = 1.0f / ap->rope_scale;
+    a.log2_theta = log2f(ap->rope_theta);
+    if (ap->llama31) {
+      if (!(ap->high_freq_factor > ap->low_freq_factor) || !(ap->low_freq_factor > 0.f))
+        return set_error(DELTA_ERR_INVALID, "%s: bad llama3.1 frequency factors", who);
+      const float two_pi = 6.283185307179586f;
+      a.smooth_a = ap->old_context_len / (two_pi * ap->high_freq_factor - two_pi * ap->low_freq_factor);
+      a.smooth_b = -1.0f / (ap->high_freq_factor / ap->low_freq_factor - 1.0f);
+    }
+  }
 
   if (a.nsplit > 1 && a.hb != a.hkv)
     return set_error(DELTA_ERR_INVALID, "%s: split launch planned with %d of %d kv heads per block", who, a.hb, a.hkv);
@@ -781,7 +924,7 @@ extern "C" DELTA_EXPORT int delta_paged_decode(const void *q, int64_t q_stride_b
                            kv_last_page_len, o, o_stride_b, o_stride_h, lse, logits_dump, dump_stride_b,
                            dump_stride_h, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
                            max_pages_per_row, mode, workspace, workspace_bytes, (hipStream_t)stream,
-                           "delta_paged_decode");
+                           "delta_paged_decode", nullptr);
 }
 
 extern "C" DELTA_EXPORT int delta_paged_decode_subset(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -795,5 +938,41 @@ extern "C" DELTA_EXPORT int delta_paged_decode_subset(const void *q, int64_t q_s
   return delta::run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
                            kv_last_page_len, o, o_stride_b, o_stride_h, lse, nullptr, 0, 0, batch, num_qo_heads,
                            num_kv_heads, head_dim, dtype, sm_scale, max_pages_per_row, delta::kAttnSubset, workspace,
-                           workspace_bytes, (hipStream_t)stream, "delta_paged_decode_subset");
+                           workspace_bytes, (hipStream_t)stream, "delta_paged_decode_subset", nullptr);
+}
+
+extern "C" DELTA_EXPORT int delta_paged_decode_append(const delta_decode_append_t *append, const void *q,
+                                                      int64_t q_stride_b, int64_t q_stride_h, void *kv_cache,
+                                                      int64_t num_pages, const int32_t *kv_indptr,
+                                                      const int32_t *kv_indices, int64_t kv_indices_len,
+                                                      const int32_t *kv_last_page_len, void *o, int64_t o_stride_b,
+                                                      int64_t o_stride_h, float *lse, float *logits_dump,
+                                                      int64_t dump_stride_b, int64_t dump_stride_h, int batch,
+                                                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                                                      float sm_scale, int max_pages_per_row, void *workspace,
+                                                      size_t workspace_bytes, delta_stream_t stream) {
+  if (!append) return delta::set_error(DELTA_ERR_INVALID, "delta_paged_decode_append: null append");
+  const int mode = logits_dump ? delta::kAttnDump : delta::kAttn;
+  return delta::run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                           kv_last_page_len, o, o_stride_b, o_stride_h, lse, logits_dump, dump_stride_b,
+                           dump_stride_h, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
+                           max_pages_per_row, mode, workspace, workspace_bytes, (hipStream_t)stream,
+                           "delta_paged_decode_append", append);
+}
+
+extern "C" DELTA_EXPORT int delta_paged_decode_subset_append(const delta_decode_append_t *append, const void *q,
+                                                             int64_t q_stride_b, int64_t q_stride_h, void *kv_cache,
+                                                             int64_t num_pages, const int32_t *kv_indptr,
+                                                             const int32_t *kv_indices, int64_t kv_indices_len,
+                                                             const int32_t *kv_last_page_len, void *o,
+                                                             int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                                                             int batch, int num_qo_heads, int num_kv_heads,
+                                                             int head_dim, int dtype, float sm_scale,
+                                                             int max_pages_per_row, void *workspace,
+                                                             size_t workspace_bytes, delta_stream_t stream) {
+  if (!append) return delta::set_error(DELTA_ERR_INVALID, "delta_paged_decode_subset_append: null append");
+  return delta::run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                           kv_last_page_len, o, o_stride_b, o_stride_h, lse, nullptr, 0, 0, batch, num_qo_heads,
+                           num_kv_heads, head_dim, dtype, sm_scale, max_pages_per_row, delta::kAttnSubset, workspace,
+                           workspace_bytes, (hipStream_t)stream, "delta_paged_decode_subset_append", append);
 }

@@ -7,7 +7,9 @@ any graph capture; the kernels themselves never allocate or synchronise.
 """
 from __future__ import annotations
 
+import ctypes
 import math
+from dataclasses import dataclass
 from typing import Optional
 
 import torch
@@ -105,18 +107,55 @@ def decode_workspace_bytes(batch: int, hq: int, hkv: int, max_pages: int) -> int
     return int(_lib.query("delta_paged_decode_workspace_bytes", batch, hq, hkv, max_pages))
 
 
+@dataclass
+class DecodeAppend:
+    """The decode token's RoPE and KV append, fused into a ``paged_decode`` launch
+    (``delta_decode_append_t``): q is then the un-rotated query, and row b's new token (k, v
+    rows b, position ``offsets[b]`` for the rotation) is written at ``kv_len_b - 1`` of the
+    cache's full CSR ``(kv_indptr, kv_indices)``, sharing ``kv_last_page_len`` with the
+    attention.  Bit-identical to ``rope_append`` followed by the plain attention."""
+    k: torch.Tensor
+    v: torch.Tensor
+    offsets: torch.Tensor
+    kv_indptr: torch.Tensor
+    kv_indices: torch.Tensor
+    rope_scale: float = 1.0
+    rope_theta: float = 1e4
+    low_freq_factor: Optional[float] = None
+    high_freq_factor: Optional[float] = None
+    old_context_len: Optional[float] = None
+
+
+def _append_struct(ap: "DecodeAppend", B: int, hkv: int, kv_cache: torch.Tensor):
+    for name, t in (("k", ap.k), ("v", ap.v)):
+        if t.dim() != 3 or tuple(t.shape) != (B, hkv, HEAD_DIM) or t.stride(2) != 1 or t.stride(1) != HEAD_DIM \
+                or t.stride(0) % 2 or t.dtype != kv_cache.dtype or not t.is_cuda:
+            raise ValueError(f"append.{name} must be [{B}, {hkv}, 128] of the cache dtype with contiguous heads")
+    _check_i32("append.offsets", ap.offsets, B)
+    _check_i32("append.kv_indptr", ap.kv_indptr, B + 1)
+    _check_i32("append.kv_indices", ap.kv_indices)
+    llama31 = ap.low_freq_factor is not None and ap.high_freq_factor is not None
+    return _lib.DecodeAppendC(
+        ap.k.data_ptr(), ap.k.stride(0), ap.v.data_ptr(), ap.v.stride(0), ap.offsets.data_ptr(),
+        ap.kv_indptr.data_ptr(), ap.kv_indices.data_ptr(), ap.kv_indices.numel(), float(ap.rope_scale),
+        float(ap.rope_theta), int(llama31), float(ap.low_freq_factor or 0.0), float(ap.high_freq_factor or 0.0),
+        float(ap.old_context_len or 0.0))
+
+
 def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
                  kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, *,
                  max_pages_per_row: int, sm_scale: Optional[float] = None,
                  out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                  logits_dump: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None, subset: bool = False) -> torch.Tensor:
+                 workspace: Optional[torch.Tensor] = None, subset: bool = False,
+                 append: Optional[DecodeAppend] = None) -> torch.Tensor:
     """Paged decode attention (``delta_paged_decode``); returns ``out`` [B, Hq, 128].
 
     ``logits_dump`` (fp32, [B_max, Hq, S] or any view with unit last stride)
     receives the planner-layer logits for ``t < kv_len``.  ``subset=True``
     runs the same attention through ``delta_paged_decode_subset`` (selected
-    pages; no dump).
+    pages; no dump).  ``append`` fuses the decode token's RoPE and KV append in
+    (``delta_paged_decode[_subset]_append``).
     """
     if subset and logits_dump is not None:
         raise ValueError("the subset attention writes no logits dump")
@@ -155,7 +194,13 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tenso
                    out.data_ptr(), out.stride(0), out.stride(1), _ptr(lse))
     common_tail = (B, hq, hkv, HEAD_DIM, _dtype_code(q), float(sm_scale), int(max_pages_per_row),
                    workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
-    if subset:
+    if append is not None:
+        ap = ctypes.byref(_append_struct(append, B, hkv, kv_cache))
+        if subset:
+            _lib.call("delta_paged_decode_subset_append", ap, *common_head, *common_tail)
+        else:
+            _lib.call("delta_paged_decode_append", ap, *common_head, _ptr(logits_dump), dsb, dsh, *common_tail)
+    elif subset:
         _lib.call("delta_paged_decode_subset", *common_head, *common_tail)
     else:
         _lib.call("delta_paged_decode", *common_head, _ptr(logits_dump), dsb, dsh, *common_tail)

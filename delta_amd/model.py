@@ -154,6 +154,7 @@ class Transformer(nn.Module):
                 b.attention.attn_decode = torch.ops.mylib.target_subset_decode
                 self.layer_roles.append("subset")
             b.attention.rope = torch.ops.mylib.rope
+            b.attention.role = self.layer_roles[-1]
 
     def forward(self, idx: Tensor, input_pos: Tensor, kv_append_indptr: Tensor, kv_page_indices: Tensor,
                 kv_page_indptr: Tensor, kv_page_lastlen: Tensor) -> Tensor:
@@ -241,6 +242,7 @@ class Attention(nn.Module):
         self.wo = nn.Linear(config.dim, config.dim, bias=False)
         self.kv_cache: Optional[KVCache] = None
         self.attn_decode = None
+        self.role = "full"  # which attention op the layer is bound to: full / plan / subset
         self.rope = None
         self.n_head = config.n_head
         self.head_dim = config.head_dim
@@ -259,16 +261,25 @@ class Attention(nn.Module):
         q = q.view(bsz * seqlen, self.n_head, self.head_dim)
         k = k.view(bsz * seqlen, self.n_local_heads, self.head_dim)
         v = v.view(bsz * seqlen, self.n_local_heads, self.head_dim)
-        if fused:
-            # mylib::rope + mylib::update_kv in one launch (bit-identical to the two ops)
-            q = K.rope_append(q, k, v, kv_append_indptr, offsets, self.kv_cache.kv_cache, kv_page_indices,
-                              kv_page_indptr, kv_page_lastlen, **ops.active_backend().rope_params())
-            kv_cache = self.kv_cache.kv_cache
+        be = ops.active_backend()
+        if fused and be.decode_append_ok():
+            # Decode step: mylib::rope + mylib::update_kv + the layer's attention op in one launch
+            # (bit-identical to the three).
+            y = be.attn_append(self.role, q, k, v, offsets, self.kv_cache.kv_cache, kv_page_indices,
+                               kv_page_indptr)
+            if self.record is not None:  # the recorded query is the rotated one
+                q = K.rope(q, k, kv_append_indptr, offsets, **be.rope_params())[0]
         else:
-            q, k = self.rope(q, k, kv_append_indptr, offsets)
-            kv_cache = self.kv_cache.update_target(k, v, kv_append_indptr, kv_page_indices, kv_page_indptr,
-                                                   kv_page_lastlen)
-        y = self.attn_decode(q, kv_cache)
+            if fused:
+                # mylib::rope + mylib::update_kv in one launch (bit-identical to the two ops)
+                q = K.rope_append(q, k, v, kv_append_indptr, offsets, self.kv_cache.kv_cache, kv_page_indices,
+                                  kv_page_indptr, kv_page_lastlen, **be.rope_params())
+                kv_cache = self.kv_cache.kv_cache
+            else:
+                q, k = self.rope(q, k, kv_append_indptr, offsets)
+                kv_cache = self.kv_cache.update_target(k, v, kv_append_indptr, kv_page_indices, kv_page_indptr,
+                                                       kv_page_lastlen)
+            y = self.attn_decode(q, kv_cache)
         if self.record is not None:
             self.record.append((q.detach().clone(), y.detach().clone()))
         y = y.contiguous().view(bsz, seqlen, self.dim)

@@ -123,6 +123,61 @@ int delta_paged_decode_subset(const void *q, int64_t q_stride_b, int64_t q_strid
                               int dtype, float sm_scale, int max_pages_per_row,
                               void *workspace, size_t workspace_bytes, delta_stream_t stream);
 
+/* The decode step's RoPE and KV append, fused into the attention launch
+ * (Attention.forward, model.py:413-418: mylib::rope, then mylib::update_kv, then the
+ * attention op -- here one launch).  Decode steps only: one new token per row.
+ *   k, v        [batch, num_kv_heads, 128] the new token's k (before RoPE) and v, row
+ *               strides k_stride / v_stride (even), 4-byte aligned
+ *   offsets     [batch] the new token's position (its rotation angle), as delta_rope
+ *   kv_indptr / kv_indices / kv_indices_len   the cache's full CSR: row b's new token
+ *               goes to position kv_len_b - 1 of it (kv_len from kv_last_page_len), the
+ *               slot delta_append_kv uses; a row without a valid slot appends nothing
+ *   rope_scale, rope_theta, llama31, low/high_freq_factor, old_context_len   as delta_rope
+ * The attention entry points that take it treat q as the un-rotated query.  Outputs,
+ * the cache bytes, lse and the logits dump are bit-identical to delta_rope_append
+ * followed by the plain entry point. */
+typedef struct delta_decode_append {
+  const void *k;
+  int64_t k_stride;
+  const void *v;
+  int64_t v_stride;
+  const int32_t *offsets;
+  const int32_t *kv_indptr;
+  const int32_t *kv_indices;
+  int64_t kv_indices_len;
+  float rope_scale;
+  float rope_theta;
+  int llama31;
+  float low_freq_factor;
+  float high_freq_factor;
+  float old_context_len;
+} delta_decode_append_t;
+
+/* delta_paged_decode with the new token's RoPE and append fused in (see above).  No
+ * counterpart entry point in the reference: it replaces the three calls of one decode
+ * layer.  kv_cache is written (the new token's slot). */
+int delta_paged_decode_append(const delta_decode_append_t *append, const void *q, int64_t q_stride_b,
+                              int64_t q_stride_h, void *kv_cache, int64_t num_pages,
+                              const int32_t *kv_indptr, const int32_t *kv_indices,
+                              int64_t kv_indices_len, const int32_t *kv_last_page_len,
+                              void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                              float *logits_dump, int64_t dump_stride_b, int64_t dump_stride_h,
+                              int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+                              int dtype, float sm_scale, int max_pages_per_row,
+                              void *workspace, size_t workspace_bytes, delta_stream_t stream);
+
+/* delta_paged_decode_subset with the new token's RoPE and append fused in: attention over
+ * the subset CSR, the append into the full CSR of `append`. */
+int delta_paged_decode_subset_append(const delta_decode_append_t *append, const void *q,
+                                     int64_t q_stride_b, int64_t q_stride_h, void *kv_cache,
+                                     int64_t num_pages, const int32_t *kv_indptr,
+                                     const int32_t *kv_indices, int64_t kv_indices_len,
+                                     const int32_t *kv_last_page_len, void *o, int64_t o_stride_b,
+                                     int64_t o_stride_h, float *lse, int batch, int num_qo_heads,
+                                     int num_kv_heads, int head_dim, int dtype, float sm_scale,
+                                     int max_pages_per_row, void *workspace, size_t workspace_bytes,
+                                     delta_stream_t stream);
+
 /* Causal attention of several query tokens per row (prompt steps): FlashInfer
  * BatchPrefillWithPagedKVCacheWrapper.run with causal=True (backend.py:1091-1105).
  * q/o are [nnz, num_qo_heads, 128] (token stride, head stride), row b's tokens at

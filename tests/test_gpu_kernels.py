@@ -517,3 +517,80 @@ def test_paged_prefill_matches_oracle(hq, hkv, dtype):
                                                c.kv_last_page_len, c.sm_scale)
     assert_attn_close(o, o_ref, f"prefill G={hq // hkv}")
     assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("hq,hkv,dtype,llama31,batch", [
+    (32, 8, torch.bfloat16, False, 6),    # page-major split launches
+    (32, 8, torch.bfloat16, True, 36),    # head-major subset (36 rows x 8 kv heads)
+    (28, 4, torch.float16, True, 5),      # G = 7
+    (16, 2, torch.bfloat16, False, 3),    # G = 8
+])
+def test_decode_append_equals_rope_append_then_decode(hq, hkv, dtype, llama31, batch):
+    """The fused decode launch (RoPE + append + attention) against delta_rope_append followed by
+    the plain attention: o, lse, logits dump and every cache byte identical -- full, planner
+    and subset kernels; rows whose new token opens a page, fills one (trailing empty page) or
+    lands on a page the subset does not hold."""
+    gen = torch.Generator().manual_seed(41)
+    lens = [1 + (97 * i + 31) % 700 for i in range(batch)]
+    lens[0] = 16   # new token fills page 0; trailing empty page
+    lens[1] = 17   # new token opens page 1
+    c = make_case(batch=batch, hq=hq, hkv=hkv, kv_lens=lens, seed=42, page_order="randperm", k=4, L=2,
+                  trailing_empty_page=True, dtype=dtype)
+    g = gpu(c)
+    B = batch
+    mp = c.max_pages
+    q = torch.randn(B, hq, 128, generator=gen).to(dtype).to(DEV)
+    kn = torch.randn(B, hkv, 128, generator=gen).to(dtype).to(DEV)
+    vn = torch.randn(B, hkv, 128, generator=gen).to(dtype).to(DEV)
+    kv_len = torch.tensor(lens, dtype=torch.int32)
+    offsets = (kv_len - 1).to(DEV)
+    app = torch.arange(B + 1, dtype=torch.int32, device=DEV)
+    p = dict(rope_scale=8.0 if llama31 else 1.0, rope_theta=5e5)
+    if llama31:
+        p.update(low_freq_factor=1.0, high_freq_factor=4.0, old_context_len=8192.0)
+    ap = K.DecodeAppend(kn, vn, offsets, g.kv_indptr, g.kv_indices, **p)
+
+    def unfused(cache, **kw):
+        qr = K.rope_append(q, kn, vn, app, offsets, cache, g.kv_indices, g.kv_indptr, g.kv_last_page_len, **p)
+        return K.paged_decode(qr, cache, **kw)
+
+    # full + planner (dump, lse)
+    for dump_on in (False, True):
+        outs = []
+        for fused in (False, True):
+            cache = g.kv_cache.clone()
+            lse = torch.full((B, hq), 7.0, device=DEV)
+            dump = torch.full((B, hq, mp * 16), 12345.0, device=DEV) if dump_on else None
+            kw = dict(kv_indptr=g.kv_indptr, kv_indices=g.kv_indices, kv_last_page_len=g.kv_last_page_len,
+                      max_pages_per_row=mp, lse=lse, logits_dump=dump)
+            o = K.paged_decode(q, cache, append=ap, **kw) if fused else unfused(cache, **kw)
+            outs.append((o, lse, dump, cache))
+        torch.cuda.synchronize()
+        (o1, l1, d1, c1), (o2, l2, d2, c2) = outs
+        assert torch.equal(o1, o2) and torch.equal(l1, l2) and torch.equal(c1, c2)
+        if dump_on:
+            assert torch.equal(d1, d2)
+
+    # subset: every row keeps its first and last pages; row 0's new token sits on page 0
+    # (the last page is the empty trailing one), so drop page 0 there: the token is appended
+    # but not attended, as in the two-call path.
+    counts = (c.kv_indptr[1:] - c.kv_indptr[:-1]).tolist()
+    sub, sptr = [], [0]
+    for b in range(B):
+        row = c.kv_indices[int(c.kv_indptr[b]):int(c.kv_indptr[b + 1])].tolist()
+        keep = sorted({0, counts[b] - 1, counts[b] // 2}) if counts[b] > 1 else [0]
+        if b == 0:
+            keep = [j for j in keep if j != 0]
+        sub += [row[j] for j in keep]
+        sptr.append(len(sub))
+    s_idx = torch.tensor(sub, dtype=torch.int32, device=DEV)
+    s_ptr = torch.tensor(sptr, dtype=torch.int32, device=DEV)
+    outs = []
+    for fused in (False, True):
+        cache = g.kv_cache.clone()
+        kw = dict(kv_indptr=s_ptr, kv_indices=s_idx, kv_last_page_len=g.kv_last_page_len, max_pages_per_row=3,
+                  subset=True)
+        o = K.paged_decode(q, cache, append=ap, **kw) if fused else unfused(cache, **kw)
+        outs.append((o, cache))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])

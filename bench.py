@@ -78,8 +78,43 @@ def time_steps(torch, eng, warmup: int, steps: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def graph_timed(torch, calls, n_warm: int, replays: int = 3) -> float:
+    """Average device time of one of ``calls`` (kernel launches), in us.
+
+    The launches are captured in one hipGraph and replayed, with HIP events on the replay
+    stream around the replays, so host launch overhead never enters the figure (a 10 us kernel
+    launched eagerly from Python is launch-bound).  The first ``n_warm`` calls run eagerly
+    first (workspaces sized, code loaded)."""
+    for f in calls[:n_warm]:
+        f()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in calls[:n_warm]:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in calls:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e.record(stream)
+    torch.cuda.synchronize()
+    del g
+    return s.elapsed_time(e) * 1e3 / (replays * len(calls))
+
+
 def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
-    """Time each hot-path kernel at the config-3 layer shape with HIP events on its stream.
+    """Time each hot-path kernel at the config-3 layer shape (graph replays, HIP events on the
+    replay stream).
 
     Launches rotate over ``n_rot`` independent layers (own KV cache, q and selection), as
     the 30 selective layers of a step do, so no launch re-reads a working set left in the
@@ -112,17 +147,7 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
     row_kv = hkv * 128 * esz  # one token of K (or V) for all kv heads
 
     def timed(fn):
-        stream = torch.cuda.current_stream()
-        for i in range(n_rot):
-            fn(*layers[i])
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record(stream)
-        for i in range(reps):
-            fn(*layers[i % n_rot])
-        e.record(stream)
-        torch.cuda.synchronize()
-        return s.elapsed_time(e) * 1e3 / reps  # us
+        return graph_timed(torch, [lambda i=i: fn(*layers[i % n_rot]) for i in range(reps)], n_rot)
 
     res = {}
 
@@ -164,7 +189,7 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
 
 def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
     """Planner, score, selection and subset-attention kernels at one layer of BASELINE config
-    ``config`` (2, 4 or 5) at its full size, HIP-event timed over ``n_rot`` rotating layers.
+    ``config`` (2, 4 or 5) at its full size, timed in graph replays over ``n_rot`` rotating layers.
     Algorithmic bytes count each row's real pages (ragged rows, per-row budgets)."""
     from delta_amd import kernels as K
     from delta_amd.workloads import config_case
@@ -199,16 +224,7 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
     qo = 2 * B * hq * 128 * esz
 
     def timed(fn):
-        for i in range(n_rot):
-            fn(*layers[i])
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record()
-        for i in range(reps):
-            fn(*layers[i % n_rot])
-        e.record()
-        torch.cuda.synchronize()
-        return s.elapsed_time(e) * 1e3 / reps
+        return graph_timed(torch, [lambda i=i: fn(*layers[i % n_rot]) for i in range(reps)], n_rot)
 
     res = {"shape": f"B={B}, {hq}q/{hkv}kv, {ntok_full} cached tokens ({min(c.kv_lens)}-{max(c.kv_lens)} per row), "
                     f"{sum(nsel)} selected pages, {str(c.kv_cache.dtype).replace('torch.', '')}"}

@@ -20,6 +20,9 @@
 //   K and V always in flight.
 //   The block's waves merge in LDS per head; with num_splits > 1 the block writes an
 //   un-normalised partial (acc, m, l) and a merge kernel combines the splits.
+//   The ROPE instantiations (decode steps) also rotate q, rotate and append the row's new
+//   token to the cache, and take that token's K / V from LDS (mylib::rope and
+//   mylib::update_kv of Attention.forward, model.py:413-418, in the same launch).
 //
 // HBM bytes per launch (algorithmic): K and V of every attended token once,
 // q and o once, the page indices once (+ the fp32 logits when dumping).

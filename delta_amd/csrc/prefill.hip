@@ -5,24 +5,27 @@
 // cache already holds the row's new tokens (update_kv runs before attention, model.py:413-418),
 // so query i of row b sits at position kv_len_b - qo_len_b + i and attends tokens 0..position.
 //
-// Work decomposition: block = 4 waves of one (row, kv head); each wave owns TW = 16 / G
-// consecutive query tokens and puts their (token, q head) pairs in the 16 columns of its MFMA
-// tiles, then sweeps the pages up to its last token's position on its own (no merge):
-//   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows (lane%16 = token,
-//         lane/16 picks d in [32s + 8c, +8) at step s), B = the wave's query columns;
-//         D puts tokens 4c..4c+3 of column j = lane%16 in lane (c, j);
+// Work decomposition: block = 8 waves of one (row, kv head) and 8 * TW consecutive query
+// tokens; each wave owns TW = 16 / G tokens and puts their (token, q head) pairs in the 16
+// columns of its MFMA tiles.  The block sweeps the pages up to its last token's position:
+// each page's K and V (4 KiB each for one head) are loaded once per block, 16 bytes per thread,
+// into a double-buffered LDS tile, kPrefetch pages ahead in registers, and all waves read them
+// from there (a wave whose tokens end earlier skips the later pages).  No merge.
+//   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows from LDS
+//         (lane%16 = token, lane/16 picks d in [32s + 8c, +8) at step s), B = the wave's query
+//         columns; D puts tokens 4c..4c+3 of column j = lane%16 in lane (c, j);
 //   softmax: online per column in the log2 domain, causal and kv_len masks per element;
-//   P.V : v_mfma_f32_16x16x16 -- A = P (row = column j, k = tokens 4c..), B = V from a padded
-//         per-wave LDS tile read with ds_read_b64_tr_b16, D = O[column 4c + r][16n + lane%16].
-// The next page's K and V are in flight while a page is processed (page ids preloaded 64 per
-// register, as in the decode kernel).
+//   P.V : v_mfma_f32_16x16x16 -- A = P (row = column j, k = tokens 4c..), B = V from the
+//         padded LDS tile read with ds_read_b64_tr_b16, D = O[column 4c + r][16n + lane%16].
+// Page ids are preloaded 64 per register, as in the decode kernel.
 #include "delta_common.h"
 
 namespace delta {
 namespace {
 
-constexpr int kPrefillWaves = 4;
-constexpr int kVStrideP = 136;  // padded V tile row (elements)
+constexpr int kPrefillWaves = 8;  // waves per block: 8 x 16 (token, head) columns share each K/V page
+constexpr int kPrefetch = 3;      // pages in flight per thread ahead of the LDS tiles
+constexpr int kVStrideP = 136;    // padded tile row (elements)
 
 struct PrefillArgs {
   const uint16_t *q;
@@ -82,16 +85,20 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
 #pragma clang fp contract(off)
   using E = Elem<DT>;
   using M16 = PMfma<DT>;
-  constexpr int TW = 16 / G;  // query tokens per wave
-  __shared__ uint16_t vtile[kPrefillWaves][kPageSize * kVStrideP];
+  constexpr int TW = 16 / G;                  // query tokens per wave
+  constexpr int BT = kPrefillWaves * TW;      // query tokens per block
+  constexpr int kTile = kPageSize * kVStrideP;  // one K or V tile (elements)
+  // Two page buffers, each K then V (padded rows), shared by the block's waves.
+  __shared__ uint16_t tiles[2][2 * kTile];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane >> 4, t = lane & 15;
   const int b = blockIdx.z, h = blockIdx.y;
-  int64_t q0 = a.qo_indptr[b], q1 = a.qo_indptr[b + 1];
+  const int64_t q0 = a.qo_indptr[b], q1 = a.qo_indptr[b + 1];
   const int qn = q1 > q0 ? (int)(q1 - q0) : 0;
-  const int tok0 = (blockIdx.x * kPrefillWaves + wave) * TW;
-  if (tok0 >= qn) return;  // whole wave; no block-wide barrier below
+  const int btok0 = blockIdx.x * BT;
+  if (btok0 >= qn) return;  // whole block
+  const int tok0 = btok0 + wave * TW;
 
   // Row's pages and length (indptr entries clamped as in the decode kernels).
   const int64_t ilen = a.kv_indices_len;
@@ -117,26 +124,57 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
     for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  const int last_tok = (tok0 + TW < qn ? tok0 + TW : qn) - 1;
-  const int pos_max = kv_len - qn + last_tok;
-  int count = pos_max >= 0 ? pos_max / kPageSize + 1 : 0;
-  count = count > np ? np : count;
+  // Pages the block sweeps (up to its last token's position) and the ones this wave needs.
+  auto pages_upto = [&](int last_tok) {
+    const int pos = kv_len - qn + last_tok;
+    const int n = pos >= 0 ? pos / kPageSize + 1 : 0;
+    return n > np ? np : n;
+  };
+  const int count = pages_upto((btok0 + BT < qn ? btok0 + BT : qn) - 1);
+  const int wcount = tok0 < qn ? pages_upto((tok0 + TW < qn ? tok0 + TW : qn) - 1) : 0;
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
-  const int64_t k_off = (int64_t)t * row_elems + 8 * c;                        // + 32 s
-  const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;  // + 4 i rows
-  uint16_t *vt = vtile[wave];
+  // Cooperative tile load: thread i < 512 moves 16 bytes -- K (i < 256) or V row (i / 16) % 16,
+  // chunk i % 16 of head h.
+  const bool loader = threadIdx.x < 2 * kPageSize * (kHeadDim / 8);
+  const int ld_which = (threadIdx.x >> 8) & 1, ld_row = (threadIdx.x >> 4) & 15, ld_ch = threadIdx.x & 15;
+  const int64_t ld_off = (int64_t)(ld_which * kPageSize + ld_row) * row_elems + (int64_t)h * kHeadDim + 8 * ld_ch;
+  const int st_off = ld_which * kTile + ld_row * kVStrideP + 8 * ld_ch;
 
-  auto load_ids = [&](int it0) -> int {
-    const int it = it0 + lane;
+  // Page ids, 64 per register (lane i: page cbase + i), the next 64 a chunk ahead.
+  auto load_ids = [&](int base) -> int {
+    const int it = base + lane;
     int pid = -1;
     if (it < count) pid = a.kv_indices[p0 + it];
     return (pid >= 0 && (int64_t)pid < a.num_pages) ? pid : -1;
   };
-  auto page_ptr = [&](int pid) -> const uint16_t * {
-    return a.kv + (int64_t)(pid < 0 ? 0 : pid) * page_elems + (int64_t)h * kHeadDim;
+  int cbase = 0;
+  int ids = count > 0 ? load_ids(0) : -1;
+  int ids_next = count > 64 ? load_ids(64) : -1;
+  auto id_of = [&](int q) -> int {  // q in [cbase, cbase + 128)
+    return q - cbase < 64 ? __builtin_amdgcn_readlane(ids, q - cbase) : __builtin_amdgcn_readlane(ids_next, q - cbase - 64);
   };
+  // Register ring of kPrefetch pages in flight ahead of the LDS buffers.
+  auto fetch = [&](int q) -> u32x4 {
+    const int pid = id_of(q);
+    if (pid < 0 || !loader) return u32x4{0u, 0u, 0u, 0u};
+    return ld128(a.kv + (int64_t)pid * page_elems + ld_off);
+  };
+  // Store page q's chunk; V rows past kv_len (or of an invalid page) become zeros: they may
+  // hold NaN/Inf and meet p = 0.
+  auto stage = [&](int q, u32x4 v) {
+    const bool keep = ld_which == 0 || q * kPageSize + ld_row < kv_len;
+    if (loader) st128(&tiles[q & 1][st_off], keep ? v : u32x4{0u, 0u, 0u, 0u});
+  };
+
+  u32x4 ring[kPrefetch];
+  if (count > 0) {
+    stage(0, fetch(0));
+#pragma unroll
+    for (int d = 1; d <= kPrefetch; ++d)
+      if (d < count) ring[d % kPrefetch] = fetch(d);
+  }
 
   float m = -INFINITY, l = 0.f;
   f32x4 acc[8];
@@ -144,83 +182,70 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
   for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float scale2 = a.sm_scale * kLog2e;
 
-  int ids = count > 0 ? load_ids(0) : -1;
-  int pid = __builtin_amdgcn_readlane(ids, 0);
-  u32x4 kf[4], vf[4];
-  if (count > 0) {
-    const uint16_t *base = page_ptr(pid);
+  for (int j0 = 0; j0 < count; j0 += kPrefetch) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) kf[s] = ld128(base + k_off + 32 * s);
+    for (int d = 0; d < kPrefetch; ++d) {
+      const int j = j0 + d;
+      if (j < count) {
+        __syncthreads();  // page j is in tiles[j & 1]; tiles[(j + 1) & 1] is free
+        if (j > 0 && (j & 63) == 0) {  // the id window moves on
+          cbase += 64;
+          ids = ids_next;
+          ids_next = cbase + 64 < count ? load_ids(cbase + 64) : -1;
+        }
+        if (j < wcount) {
+          const uint16_t *kt = tiles[j & 1];
+          const uint16_t *vt = kt + kTile;
+          f32x4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vf[i] = ld128(base + v_off + (int64_t)(4 * i) * row_elems);
-  }
-  for (int c0 = 0; c0 < count; c0 += 64) {
-    const int cn = count - c0 < 64 ? count - c0 : 64;
-    const int ids_next = c0 + 64 < count ? load_ids(c0 + 64) : -1;
-    for (int it = 0; it < cn; ++it) {
-      const int j = c0 + it;
-      const bool ok = pid >= 0;
-      const bool more = j + 1 < count;
-      const int pidn = it + 1 < cn ? __builtin_amdgcn_readlane(ids, it + 1) : __builtin_amdgcn_readlane(ids_next, 0);
-      const uint16_t *nbase = page_ptr(pidn);
-
-      // Stage V (rows past kv_len, or of an invalid page, zeroed: they may hold NaN/Inf).
-      const int vlim = ok ? kv_len - j * kPageSize : 0;
+          for (int s = 0; s < 4; ++s)
+            S = E::mfma(*reinterpret_cast<const u32x4 *>(kt + t * kVStrideP + 32 * s + 8 * c), qf[s], S);
+          const int tk0 = j * kPageSize + 4 * c;
+          const bool ok = id_of(j) >= 0;  // an id outside the cache contributes nothing
+          float x[4], p[4];
+          float pm = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
-        st128(vt + (4 * i + c) * kVStrideP + 8 * t, vf[i] & u32x4{keep, keep, keep, keep});
-      }
-      f32x4 S = {0.f, 0.f, 0.f, 0.f};
+          for (int r = 0; r < 4; ++r) {
+            const int tk = tk0 + r;
+            x[r] = (ok && col_ok && tk <= qpos && tk < kv_len) ? S[r] * scale2 : -INFINITY;
+            pm = fmaxf(pm, x[r]);
+          }
+          const float mn = fmaxf(m, prows4_max(pm));
+          const float mref = mn == -INFINITY ? 0.f : mn;
+          const float alpha = fast_exp2(m - mref);
+          float ps = 0.f;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) S = E::mfma(kf[s], qf[s], S);
-      if (more) {
+          for (int r = 0; r < 4; ++r) {
+            p[r] = fast_exp2(x[r] - mref);
+            ps += p[r];
+          }
+          l = l * alpha + prows4_sum(ps);
+          m = mn;
+          if (__ballot(alpha != 1.f)) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kf[s] = ld128(nbase + k_off + 32 * s);
+            for (int r = 0; r < 4; ++r) {
+              const float al = shfl(alpha, 4 * c + r);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vf[i] = ld128(nbase + v_off + (int64_t)(4 * i) * row_elems);
-      }
-
-      const int tk0 = j * kPageSize + 4 * c;
-      float x[4], p[4];
-      float pm = -INFINITY;
+              for (int n = 0; n < 8; ++n) acc[n][r] *= al;
+            }
+          }
+          ps4_t pa;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tk = tk0 + r;
-        x[r] = (ok && col_ok && tk <= qpos && tk < kv_len) ? S[r] * scale2 : -INFINITY;
-        pm = fmaxf(pm, x[r]);
-      }
-      const float mn = fmaxf(m, prows4_max(pm));
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = fast_exp2(m - mref);
-      float ps = 0.f;
+          for (int r = 0; r < 4; ++r) pa[r] = M16::pack(p[r]);
+          const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStrideP + 4 * (t & 3);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = fast_exp2(x[r] - mref);
-        ps += p[r];
-      }
-      l = l * alpha + prows4_sum(ps);
-      m = mn;
-      if (__ballot(alpha != 1.f)) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float al = shfl(alpha, 4 * c + r);
-#pragma unroll
-          for (int n = 0; n < 8; ++n) acc[n][r] *= al;
+          for (int n = 0; n < 8; ++n) {
+            const ps4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 16 * n));
+            acc[n] = M16::run(pa, bv, acc[n]);
+          }
+        }
+        // Page j + 1 to LDS (it was fetched kPrefetch pages ago), page j + 1 + kPrefetch in flight.
+        if (j + 1 < count) {
+          stage(j + 1, ring[(d + 1) % kPrefetch]);
+          if (j + 1 + kPrefetch < count) ring[(d + 1) % kPrefetch] = fetch(j + 1 + kPrefetch);
         }
       }
-      ps4_t pa;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pa[r] = M16::pack(p[r]);
-      const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStrideP + 4 * (t & 3);
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const ps4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 16 * n));
-        acc[n] = M16::run(pa, bv, acc[n]);
-      }
-      pid = pidn;
     }
-    ids = ids_next;
   }
 
   // Normalise and write: lane (c, t) holds O[column 4c + r][16n + t].

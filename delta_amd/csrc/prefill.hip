@@ -9,8 +9,9 @@
 // tokens; each wave owns TW = 16 / G tokens and puts their (token, q head) pairs in the 16
 // columns of its MFMA tiles.  The block sweeps the pages up to its last token's position:
 // each page's K and V (4 KiB each for one head) are loaded once per block, 16 bytes per thread,
-// into a double-buffered LDS tile, kPrefetch pages ahead in registers, and all waves read them
-// from there (a wave whose tokens end earlier skips the later pages).  No merge.
+// into double-buffered LDS tiles kGroup pages at a time (the next group in flight in
+// registers), and all waves read them from there; a wave whose tokens end earlier skips the
+// later pages, and groups below every column's diagonal skip the element masks.  No merge.
 //   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows from LDS
 //         (lane%16 = token, lane/16 picks d in [32s + 8c, +8) at step s), B = the wave's query
 //         columns; D puts tokens 4c..4c+3 of column j = lane%16 in lane (c, j);
@@ -24,7 +25,7 @@ namespace delta {
 namespace {
 
 constexpr int kPrefillWaves = 8;  // waves per block: 8 x 16 (token, head) columns share each K/V page
-constexpr int kPrefetch = 3;      // pages in flight per thread ahead of the LDS tiles
+constexpr int kGroup = 2;         // pages per LDS buffer (and per barrier)
 constexpr int kVStrideP = 136;    // padded tile row (elements)
 
 struct PrefillArgs {
@@ -89,7 +90,7 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
   constexpr int BT = kPrefillWaves * TW;      // query tokens per block
   constexpr int kTile = kPageSize * kVStrideP;  // one K or V tile (elements)
   // Two page buffers, each K then V (padded rows), shared by the block's waves.
-  __shared__ uint16_t tiles[2][2 * kTile];
+  __shared__ uint16_t tiles[2][kGroup][2 * kTile];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane >> 4, t = lane & 15;
@@ -155,25 +156,33 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
   auto id_of = [&](int q) -> int {  // q in [cbase, cbase + 128)
     return q - cbase < 64 ? __builtin_amdgcn_readlane(ids, q - cbase) : __builtin_amdgcn_readlane(ids_next, q - cbase - 64);
   };
-  // Register ring of kPrefetch pages in flight ahead of the LDS buffers.
   auto fetch = [&](int q) -> u32x4 {
-    const int pid = id_of(q);
+    const int pid = q < count ? id_of(q) : -1;
     if (pid < 0 || !loader) return u32x4{0u, 0u, 0u, 0u};
     return ld128(a.kv + (int64_t)pid * page_elems + ld_off);
   };
-  // Store page q's chunk; V rows past kv_len (or of an invalid page) become zeros: they may
-  // hold NaN/Inf and meet p = 0.
-  auto stage = [&](int q, u32x4 v) {
-    const bool keep = ld_which == 0 || q * kPageSize + ld_row < kv_len;
-    if (loader) st128(&tiles[q & 1][st_off], keep ? v : u32x4{0u, 0u, 0u, 0u});
-  };
-
-  u32x4 ring[kPrefetch];
-  if (count > 0) {
-    stage(0, fetch(0));
+  // Pages go through LDS in groups of kGroup: one barrier, one softmax rescale and one buffer
+  // swap per group.  Group gi sits in tiles[gi & 1]; group gi + 1 waits in registers (ring),
+  // its loads issued a whole group earlier.  V rows past kv_len (or of an invalid page) are
+  // stored as zeros: they may hold NaN/Inf and meet p = 0.
+  u32x4 ring[kGroup];
+  auto fetch_group = [&](int gi) {
 #pragma unroll
-    for (int d = 1; d <= kPrefetch; ++d)
-      if (d < count) ring[d % kPrefetch] = fetch(d);
+    for (int pp = 0; pp < kGroup; ++pp) ring[pp] = fetch(gi * kGroup + pp);
+  };
+  auto stage_group = [&](int gi) {
+#pragma unroll
+    for (int pp = 0; pp < kGroup; ++pp) {
+      const int q = gi * kGroup + pp;
+      const bool keep = ld_which == 0 || q * kPageSize + ld_row < kv_len;
+      if (loader && q < count) st128(&tiles[gi & 1][pp][st_off], keep ? ring[pp] : u32x4{0u, 0u, 0u, 0u});
+    }
+  };
+  const int ngroups = (count + kGroup - 1) / kGroup;
+  if (ngroups > 0) {
+    fetch_group(0);
+    stage_group(0);
+    if (ngroups > 1) fetch_group(1);
   }
 
   float m = -INFINITY, l = 0.f;
@@ -182,69 +191,92 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
   for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float scale2 = a.sm_scale * kLog2e;
 
-  for (int j0 = 0; j0 < count; j0 += kPrefetch) {
+  for (int gi = 0; gi < ngroups; ++gi) {
+    const int j0 = gi * kGroup;
+    __syncthreads();  // group gi is in tiles[gi & 1]; tiles[(gi + 1) & 1] is free
+    if (j0 > 0 && (j0 & 63) == 0) {  // the id window moves on
+      cbase += 64;
+      ids = ids_next;
+      ids_next = cbase + 64 < count ? load_ids(cbase + 64) : -1;
+    }
+    if (j0 < wcount) {
+      f32x4 S[kGroup];
 #pragma unroll
-    for (int d = 0; d < kPrefetch; ++d) {
-      const int j = j0 + d;
-      if (j < count) {
-        __syncthreads();  // page j is in tiles[j & 1]; tiles[(j + 1) & 1] is free
-        if (j > 0 && (j & 63) == 0) {  // the id window moves on
-          cbase += 64;
-          ids = ids_next;
-          ids_next = cbase + 64 < count ? load_ids(cbase + 64) : -1;
+      for (int pp = 0; pp < kGroup; ++pp) S[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sk = 0; sk < 4; ++sk)
+#pragma unroll
+        for (int pp = 0; pp < kGroup; ++pp)
+          S[pp] = E::mfma(*reinterpret_cast<const u32x4 *>(&tiles[gi & 1][pp][t * kVStrideP + 32 * sk + 8 * c]),
+                          qf[sk], S[pp]);
+      float x[kGroup][4];
+      float pm = -INFINITY;
+      // Below the diagonal of every column and inside kv_len the group needs no element masks
+      // (columns past the wave's tokens compute on zero q and are never written).
+      bool ok[kGroup];
+      bool all_ok = (j0 + kGroup) * kPageSize <= kv_len && (j0 + kGroup) * kPageSize - 1 <= kv_len - qn + tok0;
+#pragma unroll
+      for (int pp = 0; pp < kGroup; ++pp) {
+        ok[pp] = j0 + pp < wcount && id_of(j0 + pp) >= 0;  // an id outside the cache contributes nothing
+        all_ok = all_ok && ok[pp];
+      }
+      if (all_ok) {
+#pragma unroll
+        for (int pp = 0; pp < kGroup; ++pp)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            x[pp][r] = S[pp][r] * scale2;
+            pm = fmaxf(pm, x[pp][r]);
+          }
+      } else {
+#pragma unroll
+        for (int pp = 0; pp < kGroup; ++pp)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tk = (j0 + pp) * kPageSize + 4 * c + r;
+            x[pp][r] = (ok[pp] && col_ok && tk <= qpos && tk < kv_len) ? S[pp][r] * scale2 : -INFINITY;
+            pm = fmaxf(pm, x[pp][r]);
+          }
+      }
+      const float mn = fmaxf(m, prows4_max(pm));
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = fast_exp2(m - mref);
+      float ps = 0.f;
+#pragma unroll
+      for (int pp = 0; pp < kGroup; ++pp)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[pp][r] = fast_exp2(x[pp][r] - mref);
+          ps += x[pp][r];
         }
-        if (j < wcount) {
-          const uint16_t *kt = tiles[j & 1];
-          const uint16_t *vt = kt + kTile;
-          f32x4 S = {0.f, 0.f, 0.f, 0.f};
+      l = l * alpha + prows4_sum(ps);
+      m = mn;
+      if (__ballot(alpha != 1.f)) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            S = E::mfma(*reinterpret_cast<const u32x4 *>(kt + t * kVStrideP + 32 * s + 8 * c), qf[s], S);
-          const int tk0 = j * kPageSize + 4 * c;
-          const bool ok = id_of(j) >= 0;  // an id outside the cache contributes nothing
-          float x[4], p[4];
-          float pm = -INFINITY;
+        for (int r = 0; r < 4; ++r) {
+          const float al = shfl(alpha, 4 * c + r);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tk = tk0 + r;
-            x[r] = (ok && col_ok && tk <= qpos && tk < kv_len) ? S[r] * scale2 : -INFINITY;
-            pm = fmaxf(pm, x[r]);
-          }
-          const float mn = fmaxf(m, prows4_max(pm));
-          const float mref = mn == -INFINITY ? 0.f : mn;
-          const float alpha = fast_exp2(m - mref);
-          float ps = 0.f;
+          for (int n = 0; n < 8; ++n) acc[n][r] *= al;
+        }
+      }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[r] = fast_exp2(x[r] - mref);
-            ps += p[r];
-          }
-          l = l * alpha + prows4_sum(ps);
-          m = mn;
-          if (__ballot(alpha != 1.f)) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float al = shfl(alpha, 4 * c + r);
-#pragma unroll
-              for (int n = 0; n < 8; ++n) acc[n][r] *= al;
-            }
-          }
+      for (int pp = 0; pp < kGroup; ++pp) {
+        if (j0 + pp < wcount) {  // later slots may hold a stale or unset tile
           ps4_t pa;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) pa[r] = M16::pack(p[r]);
-          const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStrideP + 4 * (t & 3);
+          for (int r = 0; r < 4; ++r) pa[r] = M16::pack(x[pp][r]);
+          const uint16_t *rd = &tiles[gi & 1][pp][kTile + (4 * c + (t >> 2)) * kVStrideP + 4 * (t & 3)];
 #pragma unroll
           for (int n = 0; n < 8; ++n) {
             const ps4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 16 * n));
             acc[n] = M16::run(pa, bv, acc[n]);
           }
         }
-        // Page j + 1 to LDS (it was fetched kPrefetch pages ago), page j + 1 + kPrefetch in flight.
-        if (j + 1 < count) {
-          stage(j + 1, ring[(d + 1) % kPrefetch]);
-          if (j + 1 + kPrefetch < count) ring[(d + 1) % kPrefetch] = fetch(j + 1 + kPrefetch);
-        }
       }
+    }
+    if (gi + 1 < ngroups) {
+      stage_group(gi + 1);
+      if (gi + 2 < ngroups) fetch_group(gi + 2);
     }
   }
 

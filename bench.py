@@ -35,6 +35,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 METRIC = "selective decode tokens/s (bs×ctx) + page-score/attn HBM GB/s vs peak"
 
 # config 3
@@ -185,6 +186,27 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
     del layers, c
     torch.cuda.empty_cache()
     return res
+
+
+def prefill_roofline(torch, n: int = 8192):
+    """The causal paged prefill kernel on one ``n``-token prompt at the Llama-3-8B layer shape
+    (32 q / 8 kv heads, bf16, shuffled pages): MFMA-bound, so reported in TFLOP/s of the two
+    attention products over the causal pairs (4 * n (n + 1) / 2 * Hq * 128 flops)."""
+    from delta_amd import kernels as K
+    from delta_amd.workloads import make_case
+    c = make_case(batch=1, hq=32, hkv=8, kv_lens=[n], dtype=torch.bfloat16, seed=0, page_order="shuffle",
+                  k=4, L=2, device="cuda:0")
+    q = torch.randn(n, 32, 128, device="cuda:0", dtype=torch.bfloat16)
+    qo = torch.tensor([0, n], dtype=torch.int32, device="cuda:0")
+    out = torch.empty_like(q)
+    us = graph_timed(torch, [lambda: K.paged_prefill(q, c.kv_cache, qo, c.kv_indptr, c.kv_indices,
+                                                     c.kv_last_page_len, max_qo_len=n, out=out)] * 4, 1)
+    flops = 4 * (n * (n + 1) / 2) * 32 * 128
+    del c, q, out
+    torch.cuda.empty_cache()
+    return {"us": round(us, 2), "tokens": n, "TFLOP_s": round(flops / us / 1e6, 1), "peak_TFLOP_s": PEAK_BF16_TFLOPS,
+            "frac": round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+            "what": f"causal prefill of one {n}-token prompt, 32q/8kv heads, bf16 (MFMA-bound)"}
 
 
 def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
@@ -422,6 +444,10 @@ def main():
     for k, v in kern.items():
         log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s ({100 * v['frac']:.1f}% of peak)")
     dom = kern["paged_decode_subset_kernel"]
+    log("prefill kernel")
+    prefill = prefill_roofline(torch)
+    log(f"  paged_prefill_kernel: {prefill['us']} us, {prefill['TFLOP_s']} TFLOP/s "
+        f"({100 * prefill['frac']:.1f}% of bf16 MFMA peak)")
     others = None
     if not args.no_other_configs:
         others = {}
@@ -465,6 +491,7 @@ def main():
         "full_cache": full,
         "speedup_vs_full_cache": round(tok_s / full["tokens_per_s"], 3) if full else None,
         "kernels": kern,
+        "prefill": prefill,
         "kernels_other_configs": others,
     }
     print(json.dumps(line), flush=True)

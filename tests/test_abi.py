@@ -86,6 +86,24 @@ def test_argument_errors_reported_without_launch(lib):
         _lib.call("delta_select_pages", 8, 4, 8, 8, 4, 1, 4, 5, None, 1, 1e-7, 0, None, 8, 4, 8, None)
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="stand-in addresses: validation-only, run where no GPU is visible")
+def test_append_descriptor_errors_reported_without_launch(lib):
+    from delta_amd import _lib
+    # The fused decode entry points check their append descriptor before any launch; the
+    # non-null 16-byte-aligned stand-in addresses below are never dereferenced.
+    with pytest.raises(_lib.DeltaHipError, match="null append"):
+        _lib.call("delta_paged_decode_append", None, 16, 0, 0, 16, 1, 16, 16, 0, 16, 16, 0, 0, None, None, 0, 0,
+                  1, 8, 8, 128, 0, 1.0, 1, None, 0, None)
+    bad_theta = _lib.DecodeAppendC(16, 1024, 16, 1024, 16, 16, 16, 1, 1.0, -1.0, 0, 0.0, 0.0, 0.0)
+    with pytest.raises(_lib.DeltaHipError, match="rope"):
+        _lib.call("delta_paged_decode_subset_append", ctypes.byref(bad_theta), 16, 0, 0, 16, 1, 16, 16, 0, 16, 16,
+                  0, 0, None, 1, 8, 8, 128, 0, 1.0, 1, None, 0, None)
+    odd_stride = _lib.DecodeAppendC(16, 1023, 16, 1024, 16, 16, 16, 1, 1.0, 1e4, 0, 0.0, 0.0, 0.0)
+    with pytest.raises(_lib.DeltaHipError, match="even row strides"):
+        _lib.call("delta_paged_decode_append", ctypes.byref(odd_stride), 16, 0, 0, 16, 1, 16, 16, 0, 16, 16, 0, 0,
+                  None, None, 0, 0, 1, 8, 8, 128, 0, 1.0, 1, None, 0, None)
+
+
 def test_wrappers_reject_cpu_tensors():
     from delta_amd import kernels
     q = torch.zeros(1, 8, 128, dtype=torch.bfloat16)

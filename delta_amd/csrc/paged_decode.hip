@@ -513,10 +513,13 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     ids = ids_next;
   }
 
-  // Merge the block's waves in LDS (the V tiles are dead once every wave left the loop).
-  __syncthreads();
-  float *s_ml = smem;                  // [nw][G][2]
-  float *s_acc = smem + nw * G * 2;    // [nw][G][128]
+  // Merge the block's waves in LDS.  Attention launches have a merge area of their own past
+  // the V tiles (and the append's LDS), so each wave stores its (m, l, acc) as soon as it
+  // leaves the loop; the dump launches reuse the V tiles' space once every wave left it.
+  constexpr bool kOwnMerge = WITH_V && !WITH_DUMP;
+  float *const s_ml = smem + (kOwnMerge ? rope_off + (ROPE ? kHeadDim + hb * kHeadDim : 0) : 0);  // [nw][G][2]
+  float *const s_acc = s_ml + nw * G * 2;                                                          // [nw][G][128]
+  if (!kOwnMerge) __syncthreads();
   if (c == 0 && t < G) {
     s_ml[(wave * G + t) * 2 + 0] = m;
     s_ml[(wave * G + t) * 2 + 1] = l;
@@ -540,15 +543,36 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     const int hh = head0 + hl;
     const int g = WITH_V ? (idx / kHeadDim) % G : idx % G;
     const int dd = WITH_V ? idx % kHeadDim : 0;
-    float M = -INFINITY;
-    for (int r = 0; r < R; ++r) M = fmaxf(M, s_ml[((r * hb + hl) * G + g) * 2]);
-    const float Mr = M == -INFINITY ? 0.f : M;
-    float L = 0.f, A = 0.f;
-    for (int r = 0; r < R; ++r) {
-      const int w = r * hb + hl;
-      const float sc = fast_exp2(s_ml[(w * G + g) * 2] - Mr);
-      L = fmaf(s_ml[(w * G + g) * 2 + 1], sc, L);
-      if (WITH_V) A = fmaf(s_acc[(w * G + g) * kHeadDim + dd], sc, A);
+    float M = -INFINITY, L = 0.f, A = 0.f;
+    if (kOwnMerge && R == kMaxWaves) {
+      // Head-major launch (one head, 16 waves): unrolled, so all the LDS reads issue
+      // together (same sums in the same order as the loop below).
+      float mw[kMaxWaves], lw[kMaxWaves], aw[kMaxWaves];
+#pragma unroll
+      for (int r = 0; r < kMaxWaves; ++r) {
+        const int w = r * hb + hl;
+        mw[r] = s_ml[(w * G + g) * 2];
+        lw[r] = s_ml[(w * G + g) * 2 + 1];
+        aw[r] = s_acc[(w * G + g) * kHeadDim + dd];
+      }
+#pragma unroll
+      for (int r = 0; r < kMaxWaves; ++r) M = fmaxf(M, mw[r]);
+      const float Mr = M == -INFINITY ? 0.f : M;
+#pragma unroll
+      for (int r = 0; r < kMaxWaves; ++r) {
+        const float sc = fast_exp2(mw[r] - Mr);
+        L = fmaf(lw[r], sc, L);
+        A = fmaf(aw[r], sc, A);
+      }
+    } else {
+      for (int r = 0; r < R; ++r) M = fmaxf(M, s_ml[((r * hb + hl) * G + g) * 2]);
+      const float Mr = M == -INFINITY ? 0.f : M;
+      for (int r = 0; r < R; ++r) {
+        const int w = r * hb + hl;
+        const float sc = fast_exp2(s_ml[(w * G + g) * 2] - Mr);
+        L = fmaf(s_ml[(w * G + g) * 2 + 1], sc, L);
+        if (WITH_V) A = fmaf(s_acc[(w * G + g) * kHeadDim + dd], sc, A);
+      }
     }
     const int hq = hh * G + g;
     if (a.nsplit == 1) {
@@ -665,7 +689,7 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
   // The fused append's LDS (past the tiles and the dump staging): the (cos, sin) table, then
   // the rotated k and the v of the block's heads.
   const size_t rope_lds = rope ? (size_t)(kHeadDim + a.hb * kHeadDim) * sizeof(float) : 0;
-  const size_t sm_attn = merge > tiles + rope_lds ? merge : tiles + rope_lds;
+  const size_t sm_attn = tiles + rope_lds + merge;  // own merge area past the tiles
   const size_t sm_plan = merge > tiles + dumps + rope_lds ? merge : tiles + dumps + rope_lds;
   const size_t sm_score = dumps_score > (size_t)waves * G * 2 * sizeof(float) ? dumps_score : (size_t)waves * G * 2 * sizeof(float);
   switch (mode) {

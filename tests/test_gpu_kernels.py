@@ -108,10 +108,14 @@ def test_page_scores(name):
     s_lse = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
     s_2pass = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp)
     s_kv = K.page_score(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, mp)
+    # A dump at a 4-byte offset with odd row strides (no alignment assumed by the scorer).
+    dump_u = torch.full((B, hq, mp * 16 + 1), float("nan"), device=DEV)[:, :, 1:]
+    dump_u.copy_(dump)
+    s_unal = K.page_scores_from_logits(dump_u, g.kv_indptr, g.kv_last_page_len, mp, lse=lse)
     torch.cuda.synchronize()
     x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, c.sm_scale, mp * 16)
     ref = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
-    for what, s in (("planner", s_lse), ("two-pass", s_2pass), ("kv-only", s_kv)):
+    for what, s in (("planner", s_lse), ("two-pass", s_2pass), ("kv-only", s_kv), ("unaligned dump", s_unal)):
         s = s.cpu().double()
         rel = ((s - ref).abs() / ref.abs().clamp_min(1e-30))
         rel[ref == 0] = s[ref == 0].abs()

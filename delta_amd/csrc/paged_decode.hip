@@ -206,8 +206,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   const int nw = blockDim.x >> 6;
   const int hb = a.hb;
   const int R = nw / hb;  // waves per kv head
-  const int hgroups = a.hkv / hb;
-  const int head0 = (blockIdx.x % hgroups) * hb;
+  // Head group: blockIdx.y of a split launch (blockIdx.x = work unit), blockIdx.x otherwise.
+  const int head0 = (a.nsplit > 1 ? (int)blockIdx.y : (int)blockIdx.x) * hb;
   const int wave = uniform(threadIdx.x >> 6);
   const int h = head0 + wave % hb;
   const int rslot = wave / hb;
@@ -622,8 +622,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArg
 // Combines the unit partials of one (row, q head): thread d of the block computes
 //   M = max_s m_s,  o[d] = sum_s A_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M),
 //   lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2
-// in two passes (the maxima, then independent scaled loads), so the loads of all units are in
-// flight together instead of one online-merge step at a time.
+// with the units' loads issued 16 at a time (all in flight together).
 template <int DT>
 __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
   using E = Elem<DT>;
@@ -635,17 +634,38 @@ __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, in
   const int nu = units_of(a, b);
   const int64_t stride = (int64_t)a.hkv * G;  // partial rows per unit
   const int64_t p0 = ((int64_t)u0 * a.hkv + h) * G + g;
-  float M = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < nu; ++s) M = fmaxf(M, a.part_ml[(p0 + s * stride) * 2]);
-  const float Mr = M == -INFINITY ? 0.f : M;
-  float L = 0.f, A = 0.f;
-#pragma unroll 8
-  for (int s = 0; s < nu; ++s) {
-    const int64_t pidx = p0 + s * stride;
-    const float sc = fast_exp2(a.part_ml[pidx * 2] - Mr);
-    L = fmaf(a.part_ml[pidx * 2 + 1], sc, L);
-    A = fmaf(a.part_acc[pidx * kHeadDim + dd], sc, A);
+  // Units in batches of 16 whose loads all issue together (clamped to the last unit, weight 0
+  // past it); the running sums move to a new maximum between batches.  One batch (<= 16
+  // units) is exactly the two-pass merge.
+  float M = -INFINITY, L = 0.f, A = 0.f;
+  for (int s0 = 0; s0 < nu; s0 += 16) {
+    float mv[16], lv[16], av[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t pidx = p0 + (int64_t)(s0 + i < nu ? s0 + i : nu - 1) * stride;
+      mv[i] = a.part_ml[pidx * 2];
+      lv[i] = a.part_ml[pidx * 2 + 1];
+      av[i] = a.part_acc[pidx * kHeadDim + dd];
+    }
+    float cm = M;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (s0 + i < nu) cm = fmaxf(cm, mv[i]);
+    const float cmr = cm == -INFINITY ? 0.f : cm;
+    if (s0 > 0) {
+      const float al = fast_exp2(M - cmr);
+      L *= al;
+      A *= al;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (s0 + i < nu) {
+        const float sc = fast_exp2(mv[i] - cmr);
+        L = fmaf(lv[i], sc, L);
+        A = fmaf(av[i], sc, A);
+      }
+    }
+    M = cm;
   }
   a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(L > 0.f ? A / L : 0.f);
   if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
@@ -679,7 +699,7 @@ enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
 
 template <int DT, int G>
 void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
-  dim3 grid = a.nsplit > 1 ? dim3(a.batch * a.nsplit) : dim3(a.hkv / a.hb, a.batch);
+  dim3 grid = a.nsplit > 1 ? dim3(a.batch * a.nsplit, a.hkv / a.hb) : dim3(a.hkv / a.hb, a.batch);
   dim3 block(64 * waves);
   const bool rope = a.k_new != nullptr;
   const size_t merge = (size_t)waves * G * (2 + kHeadDim) * sizeof(float);
@@ -743,16 +763,23 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   head-major (hb = 1) when the (row, kv head) pairs alone give >= 256 blocks and the
 //     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
 //     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
-//     faster page-major gather repays the merge.
+//     faster page-major gather repays the merge;
+//   head-major with splits (grid (units, Hkv)) for attention launches of fewer than 256
+//     pairs (small batches): the launch still reaches 256 blocks, down to one page per
+//     wave, and each unit's partials cover one kv head, so the partials and the merge's
+//     reads are 1/Hkv of page-major's (config 4 subset: 20.6 -> 15.5 us).  Dump launches
+//     (planner, scorer) keep page-major, which measured faster for them.
 //   Work units hold at most kMaxChunk pages (64 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
 constexpr int64_t kHeadMajorPageHeads = 65536;
 constexpr int kMaxChunk = 128;
 
-void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int *hb, int *chunk) {
+void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int *waves, int *hb, int *chunk) {
   int h = hkv;
   if ((int64_t)batch * hkv >= kHeadMajorPairs && (int64_t)batch * hkv * max_pages <= kHeadMajorPageHeads) h = 1;
+  const bool small = !dump && (int64_t)batch * hkv < kHeadMajorPairs;
+  if (small) h = 1;
   int R = h > 0 ? kMaxWaves / h : 1;
   if (R < 1) R = 1;
   const int w = h * R;
@@ -760,7 +787,7 @@ void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int
   int64_t ns = 1;
   if (batch > 0 && max_pages > 0) {
     ns = ceil_div(256 * 4 * 4, (int64_t)batch * groups * w);
-    int64_t cap = max_pages / (2 * R);
+    int64_t cap = max_pages / ((small ? 1 : 2) * R);
     if (cap < 1) cap = 1;
     if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;
@@ -778,9 +805,10 @@ void decode_plan(int batch, int hkv, int max_pages, int *nsplit, int *waves, int
 }
 
 int decode_num_splits(int batch, int hkv, int max_pages) {
-  int ns, w, hb, ch;
-  decode_plan(batch, hkv, max_pages, &ns, &w, &hb, &ch);
-  return ns;
+  int ns, w, hb, ch, ns_dump;
+  decode_plan(batch, hkv, max_pages, false, &ns, &w, &hb, &ch);
+  decode_plan(batch, hkv, max_pages, true, &ns_dump, &w, &hb, &ch);
+  return ns > ns_dump ? ns : ns_dump;
 }
 
 // Workspace of a split launch: (m, l) for every (unit, q head), then acc, then each row's
@@ -849,7 +877,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.hq = hq;
   a.hkv = hkv;
   int waves;
-  decode_plan(batch, hkv, max_pages, &a.nsplit, &waves, &a.hb, &a.chunk);
+  decode_plan(batch, hkv, max_pages, dump != nullptr, &a.nsplit, &waves, &a.hb, &a.chunk);
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;
@@ -889,8 +917,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
     }
   }
 
-  if (a.nsplit > 1 && a.hb != a.hkv)
-    return set_error(DELTA_ERR_INVALID, "%s: split launch planned with %d of %d kv heads per block", who, a.hb, a.hkv);
+  if (a.hb < 1 || a.hkv % a.hb != 0)
+    return set_error(DELTA_ERR_INVALID, "%s: launch planned with %d of %d kv heads per block", who, a.hb, a.hkv);
   const bool with_acc = mode != kScoreOnly;
   const size_t need = decode_workspace_bytes(batch, hq, a.nsplit, with_acc);
   if (need > 0) {

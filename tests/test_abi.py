@@ -51,10 +51,11 @@ def test_no_undeclared_exports(lib):
 def test_queries_without_gpu(lib):
     assert lib.delta_abi_version() == 100
     assert lib.delta_last_error() == b""
-    # split heuristic: deterministic, >= 1, and >= 2 pages per wave.
-    # Page-major blocks (Hkv heads x R waves = 16) split up to 4096 waves in total;
-    # head-major blocks (one kv head, 16 waves) when batch*Hkv >= 256 and
-    # batch*Hkv*max_pages <= 65536 never split.
+    # split heuristic: deterministic, >= 1; the larger of the attention and the dump plans.
+    # Page-major blocks (Hkv heads x R waves = 16) split up to 4096 waves in total, >= 2 pages
+    # per wave; head-major blocks (one kv head, 16 waves) when batch*Hkv >= 256 and
+    # batch*Hkv*max_pages <= 65536 never split; attention launches with batch*Hkv < 256 use
+    # head-major blocks split to 256 blocks, >= 1 page per wave (fewer splits than page-major).
     assert lib.delta_decode_num_splits(32, 8, 128) == 1        # config 3 subset: head-major
     assert lib.delta_decode_num_splits(64, 4, 128) == 1        # head-major
     assert lib.delta_decode_num_splits(32, 8, 513) == 8        # config 3 full: page-major, 256 blocks

@@ -50,12 +50,17 @@ def gpu(c):
     return c.to(DEV)
 
 
-def assert_ulp_close(a, b):
-    """Two kernel variants (with / without the logits dump) round the same math
-    differently by a few ulp at most (P is rounded to the KV dtype for the P.V MFMA)."""
+def assert_variant_close(a, b):
+    """Launches with and without the logits dump compute the same math but may cut a row's
+    pages into different work units (small attention launches split head-major, dump
+    launches page-major), so the fp32 sums run in another order and P (rounded to the KV
+    dtype for the P.V MFMA, +-2^-8 relative) can round the other way.  The output then moves
+    by ~2^-8 of its typical magnitude: allowed, a few ulp of each output plus two ulp of the
+    largest output of its (row, head)."""
     ulp = torch.finfo(a.dtype).eps
     a, b = a.float(), b.float()
-    assert ((a - b).abs() <= 4 * ulp * b.abs() + 1e-5).all()
+    scale = b.abs().amax(dim=-1, keepdim=True)
+    assert ((a - b).abs() <= 4 * ulp * b.abs() + 2 * ulp * scale + 1e-6).all()
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -88,11 +93,11 @@ def test_decode_attention_and_dump(name):
         assert torch.all(d[b, :, end:] == 12345.0), f"row {b}: dump wrote past the last page"
     err = (d[valid] - x_ref[valid]).abs() / (1 + x_ref[valid].abs())
     assert err.max().item() < 1e-4
-    # the no-dump variant agrees to an ulp and each variant is deterministic
+    # the no-dump variant agrees to rounding and each variant is deterministic
     o2 = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
     o3 = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
     assert torch.equal(o2, o3)
-    assert_ulp_close(o, o2)
+    assert_variant_close(o, o2)
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -256,7 +261,8 @@ def test_ragged_work_units(plan_pages):
     o_ref, lse_ref = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
                                               c.kv_last_page_len, c.sm_scale)
     assert_attn_close(o, o_ref, "ragged units")
-    assert torch.equal(o, o2)
+    assert_attn_close(o2, o_ref, "ragged units, no dump")
+    assert_variant_close(o, o2)
     assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
     x_ref = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
                           c.sm_scale, c.max_pages * 16)
@@ -283,7 +289,7 @@ def test_sparse_equals_full_when_budget_covers_all():
     o_sp = K.paged_decode(g.q, g.kv_cache, ip, idx, g.kv_last_page_len, max_pages_per_row=mp, subset=True)
     o_nd = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
     assert torch.equal(o_sp, o_nd)
-    assert_ulp_close(o_sp, o_full)
+    assert_variant_close(o_sp, o_full)
 
 
 def test_pack_page_indices():

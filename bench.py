@@ -15,6 +15,8 @@ Also measured, in the same process:
     K-only scorer, each timed with HIP events on its launch stream; achieved
     GB/s from algorithmic bytes (K/V of the attended tokens once, q, o, the
     page indices, + the logits for the scorers);
+  * the decode step of BASELINE config 4 end to end (Qwen2.5-7B shape, batch 4,
+    64 k context), selective and full cache;
   * a CPU baseline: the oracle's PyTorch-CPU restatement of the same math,
     composed per step from per-op timings on a bounded sample.
 
@@ -64,6 +66,40 @@ def build_engine(torch, steps_budget: int):
     eng.setup_caches(max_batch_size=BATCH, max_seq_length=CONTEXT + steps_budget + 16)
     eng.prepare_synthetic_decode(CONTEXT, decode_budget=steps_budget, seed=0)
     return eng
+
+
+def engine_config4(torch, warmup: int, steps: int) -> dict:
+    """BASELINE config 4 end to end: a random-init Qwen2.5-7B-shaped model (28 layers, 28 q / 4
+    kv heads, qkv bias, bf16), batch 4, 65536-token context, 4096-token budget (256 pages) behind
+    the compression-ratio-16 gate, L = 8, layers 0-1 full, 4 K channels scaled x8 in every
+    layer; one hipGraph per step, selective and full-cache decode in turn."""
+    from delta_amd.backend import LMBackend
+    from delta_amd import ops
+    B, ctx, budget_pages = 4, 65536, 256
+    extra = 2 * (warmup + steps) + 16
+    eng = LMBackend(dtype=torch.bfloat16, device="cuda:0", cuda_graph_decode=True)
+    eng.load_model("random:Qwen2.5-7b", seed=0)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = [0, 1]
+    cfg.subset_cache_size = budget_pages
+    cfg.compression_ratio = 16.0
+    cfg.L = 8
+    eng.setup_caches(max_batch_size=B, max_seq_length=ctx + extra + 16)
+    eng.prepare_synthetic_decode(ctx, decode_budget=extra, seed=0, k_outlier_channels=4)
+    ms = time_steps(torch, eng, warmup, steps)
+    eng.enable_selective_cache = False
+    eng._decode_graph = None
+    ms_full = time_steps(torch, eng, warmup, steps)
+    ops.set_active_backend(None)
+    del eng
+    torch.cuda.empty_cache()
+    return {"workload": "config4: Qwen2.5-7B-shaped decode step, B=4, 65536-token context, 4096-token budget "
+                        "(256 pages, compression ratio 16, L=8), full layers [0,1], K outlier channels, "
+                        "one hipGraph per step",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 2),
+            "full_cache_ms_per_step": round(ms_full, 4), "full_cache_tokens_per_s": round(B / ms_full * 1e3, 2),
+            "speedup_vs_full_cache": round(ms_full / ms, 3)}
 
 
 def time_steps(torch, eng, warmup: int, steps: int) -> float:
@@ -398,6 +434,8 @@ def main():
     ap.add_argument("--no-full-compare", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the kernel-level measurements at BASELINE configs 2, 4 and 5")
+    ap.add_argument("--no-engine-config4", action="store_true",
+                    help="skip the end-to-end decode step at BASELINE config 4")
     ap.add_argument("--kernel-reps", type=int, default=48)
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel roofline loop and a copy of known size (for rocprofv3 --pmc runs)")
@@ -462,6 +500,17 @@ def main():
                 others[f"config{cfg}"] = {"error": repr(exc)}
                 log(f"  failed: {exc!r}")
             torch.cuda.empty_cache()
+    eng4 = None
+    if not args.no_engine_config4:
+        log("engine at config 4 (Qwen2.5-7B shape, B=4, 64k context)")
+        try:
+            eng4 = engine_config4(torch, args.warmup, args.steps)
+            log(f"  selective {eng4['ms_per_step']:.3f} ms/step ({eng4['tokens_per_s']} tokens/s), full cache "
+                f"{eng4['full_cache_ms_per_step']:.3f} ms/step: {eng4['speedup_vs_full_cache']}x")
+        except Exception as exc:  # reported in the line, never fatal for the headline number
+            eng4 = {"error": repr(exc)}
+            log(f"  failed: {exc!r}")
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
@@ -493,6 +542,7 @@ def main():
         "kernels": kern,
         "prefill": prefill,
         "kernels_other_configs": others,
+        "engine_config4": eng4,
     }
     print(json.dumps(line), flush=True)
 

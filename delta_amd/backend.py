@@ -357,11 +357,14 @@ class LMBackend:
     # --------------------------------------------------- synthetic contexts
     @torch.inference_mode()
     def prepare_synthetic_decode(self, kv_len, decode_budget: int = 256, seed: int = 0,
-                                 fill_std: float = 1.0):
+                                 fill_std: float = 1.0, k_outlier_channels: int = 0,
+                                 k_outlier_scale: float = 8.0):
         """Put every slot in the state "``kv_len`` tokens cached, decoding" (``kv_len`` an int
         or one length per slot): pages for ``kv_len + decode_budget`` tokens from the page
-        pool, seeded N(0, fill_std) K/V in every layer, random current tokens.  Used by the
-        benchmark and tests (no prompts, no prefill)."""
+        pool, seeded N(0, fill_std) K/V in every layer, random current tokens.  With
+        ``k_outlier_channels`` = n, n seeded head-dim channels of every layer's K are scaled by
+        ``k_outlier_scale`` (per-channel outliers).  Used by the benchmark and tests (no
+        prompts, no prefill)."""
         B = self.batch_size
         lens = [int(kv_len)] * B if isinstance(kv_len, int) else [int(x) for x in kv_len]
         if len(lens) != B:
@@ -375,9 +378,16 @@ class LMBackend:
         self.slot_block_table.copy_(bt)
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
+        outl = None
+        if k_outlier_channels:
+            g2 = torch.Generator()
+            g2.manual_seed(seed + 2)
+            outl = torch.randperm(self.model.config.head_dim, generator=g2)[:k_outlier_channels].to(self.device)
         for layer in self.model.layers:
             cache = layer.attention.kv_cache.kv_cache
             cache.normal_(0.0, fill_std, generator=gen)
+            if outl is not None:
+                cache[:, 0, :, :, outl] *= k_outlier_scale
         self.cachelens.copy_(torch.tensor(lens, dtype=torch.int32))
         self.active.fill_(1)
         vocab = self.model.config.vocab_size

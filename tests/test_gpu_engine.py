@@ -241,3 +241,19 @@ def test_fused_dense_path_matches_reference_structure():
     cos = torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0).item()
     assert cos > 0.999, cos
     assert (a - b).abs().max().item() < 0.05 * b.abs().max().item()
+
+
+def test_synthetic_fill_outlier_channels():
+    """prepare_synthetic_decode(k_outlier_channels=n): n channels of every layer's K scaled by
+    k_outlier_scale, V and the other K channels untouched (config 4's per-channel outliers)."""
+    eng = make_engine()
+    eng.prepare_synthetic_decode([200, 200, 200], decode_budget=16, seed=3)
+    ref = [l.attention.kv_cache.kv_cache.clone() for l in eng.model.layers]
+    eng.prepare_synthetic_decode([200, 200, 200], decode_budget=16, seed=3, k_outlier_channels=2,
+                                 k_outlier_scale=8.0)
+    for layer, r in zip(eng.model.layers, ref):
+        c = layer.attention.kv_cache.kv_cache
+        assert torch.equal(c[:, 1], r[:, 1])                    # V untouched
+        ratio = (c[:, 0].float().abs().sum(dim=(0, 1, 2)) / r[:, 0].float().abs().sum(dim=(0, 1, 2))).cpu()
+        scaled = (ratio - 8.0).abs() < 1e-2
+        assert int(scaled.sum()) == 2 and bool(((ratio - 1.0).abs() < 1e-6)[~scaled].all())

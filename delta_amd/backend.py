@@ -37,6 +37,7 @@ import torch
 
 from . import kernels as K
 from . import ops
+from . import model as model_mod
 from .model import Transformer, build_random_model
 from .page_selector_v2 import PageSelectorV2
 from .public_config import FINAL_PUBLIC_DELTA_BACKEND_CONFIG as _CFG
@@ -173,6 +174,10 @@ class LMBackend:
         dev = self.device
         self.max_length = max_seq_length
         self.batch_size = max_batch_size
+        if max_batch_size <= model_mod._SKINNY_ROWS_ANY:
+            # every decode GEMM of this engine runs on delta_gemm_skinny, the gate|up one too
+            for layer in self.model.layers:
+                layer.feed_forward.use_row_major_w13()
         self.page_size = PAGE_SIZE
         self.pages_per_slot = (max_seq_length + PAGE_SIZE - 1) // PAGE_SIZE + 1  # +1: trailing empty page
         self.max_num_pages = self.pages_per_slot * max_batch_size

@@ -6,8 +6,9 @@
 // smaller weights at 1.7-3.7 TB/s (few, large tiles); this kernel is built to stream W once at
 // HBM rate:
 //
-//   grid = (N / (8 * NB), ceil(M / 32)), block = 8 waves splitting K; wave w owns k in
-//   [w * kper, (w + 1) * kper) for the block's 8 * NB output columns and 32 token rows.
+//   grid = (N / (8 * NB), ceil(M / (8 TG))), block = 8 waves splitting K; wave w owns k in
+//   [w * kper, (w + 1) * kper) for the block's 8 * NB output columns and 8 TG token rows
+//   (TG = 1 at M <= 8, else 4), with 1 or 2 k steps of loads in flight.
 //   Per 64-wide k step and 8-column block, one v_mfma_f32_16x16x32 per 8 token rows:
 //     A = W: row i = 2u + e is column n0 + u restricted to k in 32 e + [0, 32); lane (c, t)
 //         loads W[n0 + t/2][k + 32 (t%2) + 8c, +8), so one load instruction covers 8 weight
@@ -20,8 +21,9 @@
 //   added before the one rounding).
 //
 // HBM bytes per launch (algorithmic): W once (N * K * 2) + x and out (small).  Measured on
-// MI355X against hipBLASLt (torch.nn.functional.linear): at M = 4 this kernel streams the
-// Llama-3-8B projections at 4.2-6.0 TB/s (hipBLASLt 1.8-5.6).  At M = 32 it is faster standalone
+// MI355X against hipBLASLt (x @ W.T, graph replays over rotating weights): at M = 4 this kernel
+// streams the Llama-3-8B projections at 4.5-6.0 TB/s (hipBLASLt 2.1-4.7) and the Qwen2.5-7B ones at
+// 3.3-6.6 TB/s (hipBLASLt 2.1-5.1; merged w1|w3 41 vs 53 us).  At M = 32 it is faster standalone
 // for weights up to ~48 MB (wo: 12.5 vs 19.7 us) and slower for the large ones: every block
 // re-reads the x fragments of its k range (as many load instructions as for W), which costs
 // most inside a decode step, where x was just written across all 8 XCDs' L2s.
@@ -31,7 +33,6 @@ namespace delta {
 namespace {
 
 constexpr int kGemmWaves = 8;  // 2-3 blocks per CU overlap one block's reduction with another's loads
-constexpr int kGemmRows = 32;  // token rows per block
 
 struct GemmArgs {
   const uint16_t *x;
@@ -44,91 +45,124 @@ struct GemmArgs {
   int M, N, K, kper;
 };
 
-template <int DT, int NB>
+// TG groups of 8 token rows per block (TG = 1 for M <= 8, else 4); each wave keeps D k steps of
+// W and x in flight (a ring of D fragment sets), so the launch has enough bytes in flight to
+// stream W at HBM rate even when the N / 16 blocks barely cover the CUs.
+template <int DT, int NB, int TG, int D>
 __global__ void __launch_bounds__(kGemmWaves * 64) gemm_skinny_kernel(GemmArgs a) {
   using E = Elem<DT>;
-  extern __shared__ float red[];  // [wave][32 token rows][8 * NB columns]
+  extern __shared__ float red[];  // [wave][8 TG token rows][8 NB columns]
   constexpr int kCols = 8 * NB;
+  constexpr int kRows = 8 * TG;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane >> 4, t = lane & 15;
   const int n0 = blockIdx.x * kCols;
-  const int m0 = blockIdx.y * kGemmRows;
+  const int m0 = blockIdx.y * kRows;
   const int kb = wave * a.kper;
   const int ke = min(a.K, kb + a.kper);
+  const int S = ke > kb ? (ke - kb) / 64 : 0;  // this wave's k steps
 
-  const uint16_t *wp = a.w + (int64_t)(n0 + (t >> 1)) * a.ldw + 32 * (t & 1) + 8 * c;
-  const uint16_t *xp[4];
-  bool xok[4];
+  const uint16_t *wp = a.w + (int64_t)(n0 + (t >> 1)) * a.ldw + 32 * (t & 1) + 8 * c + kb;
+  const uint16_t *xp[TG];
+  bool xok[TG];
 #pragma unroll
-  for (int tg = 0; tg < 4; ++tg) {
+  for (int tg = 0; tg < TG; ++tg) {
     const int r = m0 + 8 * tg + (t & 7);
     xok[tg] = r < a.M;
-    xp[tg] = a.x + (int64_t)(xok[tg] ? r : 0) * a.ldx + 32 * (t >> 3) + 8 * c;
+    xp[tg] = a.x + (int64_t)(xok[tg] ? r : 0) * a.ldx + 32 * (t >> 3) + 8 * c + kb;
   }
 
-  f32x4 acc[NB][4];
+  f32x4 acc[NB][TG];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int tg = 0; tg < 4; ++tg) acc[nb][tg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int tg = 0; tg < TG; ++tg) acc[nb][tg] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 wf[NB], xf[4];
-  if (kb < ke) {
+  u32x4 wf[D][NB], xf[D][TG];
+  auto load = [&](int d, int s) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) wf[nb] = ld128_stream(wp + (int64_t)nb * 8 * a.ldw + kb);
+    for (int nb = 0; nb < NB; ++nb) wf[d][nb] = ld128_stream(wp + (int64_t)nb * 8 * a.ldw + 64 * s);
 #pragma unroll
-    for (int tg = 0; tg < 4; ++tg) xf[tg] = xok[tg] ? ld128(xp[tg] + kb) : u32x4{0u, 0u, 0u, 0u};
-  }
-  for (int k = kb; k < ke; k += 64) {
+    for (int tg = 0; tg < TG; ++tg) xf[d][tg] = xok[tg] ? ld128(xp[tg] + 64 * s) : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto step = [&](int d) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int tg = 0; tg < 4; ++tg) acc[nb][tg] = E::mfma(wf[nb], xf[tg], acc[nb][tg]);
-    // The next k step's fragments are in flight while the other waves compute.
-    if (k + 64 < ke) {
+      for (int tg = 0; tg < TG; ++tg) acc[nb][tg] = E::mfma(wf[d][nb], xf[d][tg], acc[nb][tg]);
+  };
+  // Step s lives in slot s % D.  Prologue: the first D steps; steady state: use slot d, refill
+  // it D steps ahead (no branch while 2 D steps remain); then the last 1..2 D steps.
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) wf[nb] = ld128_stream(wp + (int64_t)nb * 8 * a.ldw + k + 64);
+  for (int d = 0; d < D; ++d)
+    if (d < S) load(d, d);
+  int s0 = 0;
+  for (; s0 + 2 * D <= S; s0 += D) {
 #pragma unroll
-      for (int tg = 0; tg < 4; ++tg) xf[tg] = xok[tg] ? ld128(xp[tg] + k + 64) : u32x4{0u, 0u, 0u, 0u};
+    for (int d = 0; d < D; ++d) {
+      step(d);
+      load(d, s0 + d + D);
     }
   }
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (s0 + d < S) {
+      step(d);
+      if (s0 + d + D < S) load(d, s0 + d + D);
+    }
+  }
+  s0 += D;
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (s0 + d < S) step(d);
 
   // Join the k slices and park this wave's partials: lane (c, v < 8) holds columns
   // n0 + 8 nb + 2c + {0, 1} of token row 8 tg + v.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int tg = 0; tg < 4; ++tg) {
-      const float s0 = acc[nb][tg][0] + dpp_f<0x128>(acc[nb][tg][1]);
-      const float s1 = acc[nb][tg][2] + dpp_f<0x128>(acc[nb][tg][3]);
+    for (int tg = 0; tg < TG; ++tg) {
+      const float s0v = acc[nb][tg][0] + dpp_f<0x128>(acc[nb][tg][1]);
+      const float s1v = acc[nb][tg][2] + dpp_f<0x128>(acc[nb][tg][3]);
       if (t < 8) {
-        float *r = red + ((int64_t)wave * kGemmRows + 8 * tg + t) * kCols + 8 * nb + 2 * c;
-        r[0] = s0;
-        r[1] = s1;
+        float *r = red + ((int64_t)wave * kRows + 8 * tg + t) * kCols + 8 * nb + 2 * c;
+        r[0] = s0v;
+        r[1] = s1v;
       }
     }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < kGemmRows * kCols; idx += kGemmWaves * 64) {
+  for (int idx = threadIdx.x; idx < kRows * kCols; idx += kGemmWaves * 64) {
     const int row = idx / kCols, col = idx % kCols;
-    float s = 0.f;
+    float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kGemmWaves; ++w) s += red[(w * kGemmRows + row) * kCols + col];
+    for (int w = 0; w < kGemmWaves; ++w) sum += red[(w * kRows + row) * kCols + col];
     if (m0 + row < a.M) {
-      if (a.bias) s += (float)E::lo(a.bias[n0 + col]);
-      a.out[(int64_t)(m0 + row) * a.ldo + n0 + col] = (uint16_t)E::from_float(s);
+      if (a.bias) sum += (float)E::lo(a.bias[n0 + col]);
+      a.out[(int64_t)(m0 + row) * a.ldo + n0 + col] = (uint16_t)E::from_float(sum);
     }
   }
 }
 
+template <int DT, int NB, int TG, int D>
+void launch_nb(const GemmArgs &a, hipStream_t stream) {
+  const dim3 grid(a.N / (8 * NB), (a.M + 8 * TG - 1) / (8 * TG));
+  hipLaunchKernelGGL((gemm_skinny_kernel<DT, NB, TG, D>), grid, dim3(kGemmWaves * 64),
+                     kGemmWaves * 8 * TG * 8 * NB * sizeof(float), stream, a);
+}
+
+// At M <= 8 a wave keeps two k steps in flight when the launch has at most one block per CU
+// (the bytes in flight must come from depth there), one otherwise.  Measured at 4 token rows
+// (graph replays, rotating weights): Qwen2.5-7B w2 30.7 -> 22.8 us, wo 8.3 -> 6.5 us; a depth
+// of 4 or 8 was slower again, and so was depth 2 with more than 256 blocks.
 template <int DT>
 int launch_gemm(const GemmArgs &a, int nb, hipStream_t stream) {
-  const dim3 block(kGemmWaves * 64);
-  if (nb == 4) {
-    const dim3 grid(a.N / 32, (a.M + kGemmRows - 1) / kGemmRows);
-    hipLaunchKernelGGL((gemm_skinny_kernel<DT, 4>), grid, block, kGemmWaves * kGemmRows * 32 * sizeof(float), stream, a);
+  if (a.M <= 8) {
+    const bool deep = a.N / (8 * nb) <= 256;
+    if (nb == 4) deep ? launch_nb<DT, 4, 1, 2>(a, stream) : launch_nb<DT, 4, 1, 1>(a, stream);
+    else deep ? launch_nb<DT, 2, 1, 2>(a, stream) : launch_nb<DT, 2, 1, 1>(a, stream);
   } else {
-    const dim3 grid(a.N / 16, (a.M + kGemmRows - 1) / kGemmRows);
-    hipLaunchKernelGGL((gemm_skinny_kernel<DT, 2>), grid, block, kGemmWaves * kGemmRows * 16 * sizeof(float), stream, a);
+    if (nb == 4) launch_nb<DT, 4, 4, 1>(a, stream);
+    else launch_nb<DT, 2, 4, 1>(a, stream);
   }
   return check_launch("delta_gemm_skinny");
 }

@@ -257,3 +257,24 @@ def test_synthetic_fill_outlier_channels():
         ratio = (c[:, 0].float().abs().sum(dim=(0, 1, 2)) / r[:, 0].float().abs().sum(dim=(0, 1, 2))).cpu()
         scaled = (ratio - 8.0).abs() < 1e-2
         assert int(scaled.sum()) == 2 and bool(((ratio - 1.0).abs() < 1e-6)[~scaled].all())
+
+
+def test_row_major_gate_up_matches_transposed():
+    """use_row_major_w13 (small-batch engines: the gate|up GEMM on delta_gemm_skinny) keeps the
+    FFN's values: same output as the transposed layout on hipBLASLt, to bf16 rounding."""
+    from delta_amd.model import FeedForward, ModelArgs
+    torch.manual_seed(5)
+    ff = FeedForward(ModelArgs(dim=512, intermediate_size=1024, n_head=4, n_local_heads=2))
+    with torch.no_grad():
+        ff.w13_t.normal_(0, 0.05)
+        ff.w2.weight.normal_(0, 0.05)
+    ff = ff.to(device=DEV, dtype=torch.bfloat16)
+    x = torch.randn(3, 512, device=DEV, dtype=torch.bfloat16)
+    with torch.inference_mode():
+        y_t = ff.forward_fused(x).float()
+        ff.use_row_major_w13()
+        assert not hasattr(ff, "w13_t") and tuple(ff.w13.shape) == (2048, 512)
+        y_r = ff.forward_fused(x).float()
+        y_plain = ff(x).float()
+    for y in (y_r, y_plain):
+        assert (y - y_t).abs().max().item() <= 2e-2 * y_t.abs().max().item()

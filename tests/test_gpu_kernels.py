@@ -446,7 +446,8 @@ def test_dense_step_helpers_match_torch(dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N,Kd,bias", [(32, 4096, 4096, False), (1, 48, 64, True), (5, 6144, 4160, True),
-                                        (32, 272, 14336, False), (40, 64, 1024, False)])
+                                        (32, 272, 14336, False), (40, 64, 1024, False), (4, 3584, 18944, False),
+                                        (8, 4608, 3584, True), (2, 152064, 3584, False), (3, 16, 640, True)])
 def test_gemm_skinny_matches_fp32_reference(dtype, M, N, Kd, bias):
     """delta_gemm_skinny against x.float() @ w.float().T (+ b): fp32 accumulation then one
     rounding, so the error is one output ulp plus fp32 summation-order noise."""

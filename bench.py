@@ -436,6 +436,8 @@ def main():
                     help="skip the kernel-level measurements at BASELINE configs 2, 4 and 5")
     ap.add_argument("--no-engine-config4", action="store_true",
                     help="skip the end-to-end decode step at BASELINE config 4")
+    ap.add_argument("--engine-config4-only", action="store_true",
+                    help="only the config-4 decode step (selective and full cache; for kernel traces)")
     ap.add_argument("--kernel-reps", type=int, default=48)
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel roofline loop and a copy of known size (for rocprofv3 --pmc runs)")
@@ -450,6 +452,13 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     torch.manual_seed(0)
+    if args.engine_config4_only:
+        log("engine at config 4 (Qwen2.5-7B shape, B=4, 64k context)")
+        eng4 = engine_config4(torch, args.warmup, args.steps)
+        log(f"  selective {eng4['ms_per_step']:.3f} ms/step ({eng4['tokens_per_s']} tokens/s), full cache "
+            f"{eng4['full_cache_ms_per_step']:.3f} ms/step: {eng4['speedup_vs_full_cache']}x")
+        print(json.dumps({"engine_config4": eng4}), flush=True)
+        return
     if args.kernels_only:
         kern = kernel_roofline(torch, args.kernel_reps)
         kern["copy_calibration"] = copy_calibration(torch)

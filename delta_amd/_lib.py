@@ -75,8 +75,12 @@ SIGNATURES = {
     "delta_argmax_rows": (c_int, [_P, c_int64, c_int, c_int, c_int, _P, c_int64, _P, c_size_t, _P]),
     "delta_add_rmsnorm": (c_int, [_P, c_int64, _P, c_int64, _P, c_float, _P, c_int64, _P, c_int64, c_int, c_int,
                                   c_int, _P]),
+    "delta_add_rmsnorm_partials": (c_int, [_P, c_int64, _P, c_int, _P, c_float, _P, c_int64, _P, c_int64, c_int,
+                                           c_int, c_int, _P]),
     "delta_silu_mul": (c_int, [_P, c_int64, _P, c_int64, c_int, c_int, c_int, _P]),
     "delta_gemm_skinny": (c_int, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int, c_int, c_int, c_int, _P]),
+    "delta_gemm_rows32_splits": (c_int, [c_int, c_int, c_int]),
+    "delta_gemm_rows32": (c_int, [_P, c_int64, _P, c_int64, _P, _P, c_int64, _P, c_int, c_int, c_int, c_int, _P]),
     "delta_rope": (c_int, [
         _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_float, c_int, c_float, c_float, c_float, _P]),

@@ -167,6 +167,166 @@ int launch_gemm(const GemmArgs &a, int nb, hipStream_t stream) {
   return check_launch("delta_gemm_skinny");
 }
 
+// ---------------------------------------------------------------------------------------------
+// Decode GEMM at up to 32 token rows: x staged in LDS once per block and shared by its 8 waves.
+//
+// The kernel above splits K across the waves of a block, so every wave reads its own slice of
+// x, as many load instructions as for W at 32 rows.  Here the 8 waves of a block own different
+// columns (8 NB each, 64 NB per block) over the same k range, and the block stages x through
+// LDS in chunks of kChunk k, already in MFMA fragment order (lane l of (k step, token group)
+// at 16 l bytes: conflict-free 16-byte reads).  Enough blocks come from splitting K across the
+// grid's y dimension (S splits); with S > 1 every split writes fp32 partials [S][M][N] that the
+// consumer sums (bias added by split 0), with S = 1 the block writes the rounded output.
+//   A = W as in gemm_skinny_kernel (8 weight rows x 128 contiguous bytes per load, streaming);
+//   B = x^T token group tg (rows 8 tg + v), read from LDS; D joined by one DPP rotate.
+// W keeps four k steps in flight per wave; a load past the block's last step is pointed at x
+// (resident in L2) and never used, so the ring's waits stay static.  Measured at 32 rows
+// (graph replays, rotating weights) against hipBLASLt: Llama-3-8B wo 9.5 vs 14.0 us, w2 24.6 vs
+// 32.8, wqkv 13.7 vs 15.3, merged w1|w3 45.4 vs 45.6 (its transposed layout); depth 2 left
+// HBM idle (wo 11.1, w2 31.9) and depth 8 spilled.
+constexpr int kChunk = 512;                   // k per staged x chunk
+constexpr int kChunkSteps = kChunk / 64;      // 64-wide k steps per chunk
+constexpr int kXFrag = kChunkSteps * 4 * 64;  // u32x4 fragments per chunk buffer (32 rows)
+static_assert(kChunkSteps % 4 == 0, "the W ring's slots follow the chunk's steps");
+
+struct SplitArgs {
+  const uint16_t *x;
+  int64_t ldx;
+  const uint16_t *w;
+  int64_t ldw;
+  const uint16_t *bias;
+  uint16_t *out;    // S == 1
+  int64_t ldo;
+  float *part;      // S > 1: [S][M][N]
+  int M, N, K, ksplit;  // ksplit: k per split (multiple of 64)
+};
+
+template <int DT, int NB>
+__global__ void __launch_bounds__(kGemmWaves * 64) gemm_rows32_kernel(SplitArgs a) {
+  using E = Elem<DT>;
+  __shared__ u32x4 xs[2][kXFrag];  // 2 x 32 KiB
+  constexpr int D = 4;  // k steps of W in flight per wave (8 slots spill, 2 leave HBM idle)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane >> 4, t = lane & 15;
+  const int ncol = blockIdx.x * (64 * NB) + wave * (8 * NB);
+  const int kb = blockIdx.y * a.ksplit;
+  const int ke = min(a.K, kb + a.ksplit);
+  const int total = ke > kb ? (ke - kb) / 64 : 0;  // k steps of this split
+  const int nchunks = (total + kChunkSteps - 1) / kChunkSteps;
+
+  // x staging: thread i moves 16-byte units u = i + 512 j of the chunk: row u / 64, k8 u % 64.
+  u32x4 xr[4];
+  auto load_chunk = [&](int ch) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = threadIdx.x + 512 * j;
+      const int row = u >> 6, k8 = u & 63;
+      const int k = kb + ch * kChunk + 8 * k8;
+      xr[j] = (row < a.M && k < ke) ? ld128(a.x + (int64_t)row * a.ldx + k) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = threadIdx.x + 512 * j;
+      const int row = u >> 6, k8 = u & 63;
+      const int s = k8 >> 3, half = (k8 >> 2) & 1, cc = k8 & 3;
+      const int l = 16 * cc + (row & 7) + 8 * half;
+      xs[buf][(s * 4 + (row >> 3)) * 64 + l] = xr[j];
+    }
+  };
+
+  const uint16_t *wp = a.w + (int64_t)(ncol + (t >> 1)) * a.ldw + 32 * (t & 1) + 8 * c + kb;
+  u32x4 wf[D][NB];
+  auto load_w = [&](int d, int g) {
+    const bool in = g < total;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      wf[d][nb] = ld128_stream(in ? wp + (int64_t)nb * 8 * a.ldw + 64 * g : a.x);
+  };
+
+  f32x4 acc[NB][4];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) acc[nb][tg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nchunks > 0) {
+    load_chunk(0);
+    store_chunk(0);
+    if (nchunks > 1) load_chunk(1);
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_w(d, d);
+  __syncthreads();
+
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int buf = ch & 1;
+    const int steps = min(kChunkSteps, total - ch * kChunkSteps);
+    auto step = [&](int d, int sl) {
+      u32x4 xf[4];
+#pragma unroll
+      for (int tg = 0; tg < 4; ++tg) xf[tg] = xs[buf][(sl * 4 + tg) * 64 + lane];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int tg = 0; tg < 4; ++tg) acc[nb][tg] = E::mfma(wf[d][nb], xf[tg], acc[nb][tg]);
+    };
+    // Slot d holds step g with g % D == d (a chunk's kChunkSteps is a multiple of D).
+    int s0 = 0;
+    for (; s0 + D <= steps; s0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        step(d, s0 + d);
+        load_w(d, ch * kChunkSteps + s0 + d + D);
+      }
+    }
+    for (int d = 0; s0 + d < steps; ++d) step(d, s0 + d);  // the split's last steps
+    if (ch + 1 < nchunks) {
+      store_chunk(buf ^ 1);  // its last reader was chunk ch - 1, behind the barrier below
+      if (ch + 2 < nchunks) load_chunk(ch + 2);
+      __syncthreads();
+    }
+  }
+
+  // Join the k slices: lane (c, v < 8) holds columns ncol + 8 nb + 2c + {0, 1} of row 8 tg + v.
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) {
+      const float s0v = acc[nb][tg][0] + dpp_f<0x128>(acc[nb][tg][1]);
+      const float s1v = acc[nb][tg][2] + dpp_f<0x128>(acc[nb][tg][3]);
+      const int row = 8 * tg + t;
+      const int col = ncol + 8 * nb + 2 * c;
+      if (t < 8 && row < a.M) {
+        float v0 = s0v, v1 = s1v;
+        if (a.bias && blockIdx.y == 0) {
+          v0 += (float)E::lo(a.bias[col]);
+          v1 += (float)E::lo(a.bias[col + 1]);
+        }
+        if (gridDim.y == 1) {
+          const uint32_t pk = E::from_float(v0) | (E::from_float(v1) << 16);
+          *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.ldo + col) = pk;
+        } else {
+          float *pp = a.part + ((int64_t)blockIdx.y * a.M + row) * a.N + col;
+          *reinterpret_cast<float2 *>(pp) = float2{v0, v1};
+        }
+      }
+    }
+}
+
+// Splits of a 32-row launch: enough blocks for every CU (N / 64 NB column blocks times S), S a
+// divisor of K / 64 so every split holds whole k steps.  Two column groups per wave for the very
+// wide (lm_head) and the deep (w2: K >= 8192) weights.
+void rows32_plan(int N, int K, int *nb, int *splits) {
+  *nb = (N % 128 == 0 && (N / 128 >= 256 || K >= 8192)) ? 2 : 1;
+  const int cblocks = N / (64 * *nb);
+  const int steps = K / 64;
+  int s = 1;
+  while (cblocks * s < 256 && s < 16 && steps % (2 * s) == 0) s *= 2;
+  *splits = s;
+}
+
 }  // namespace
 }  // namespace delta
 
@@ -200,4 +360,58 @@ extern "C" DELTA_EXPORT int delta_gemm_skinny(const void *x, int64_t ldx, const 
   const int nb = (N % 32 == 0 && N / 32 >= 256) ? 4 : 2;
   return dtype == DELTA_BF16 ? launch_gemm<DELTA_BF16>(a, nb, (hipStream_t)stream)
                              : launch_gemm<DELTA_FP16>(a, nb, (hipStream_t)stream);
+}
+
+extern "C" DELTA_EXPORT int delta_gemm_rows32_splits(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N % 64) return 0;
+  int nb, sp;
+  delta::rows32_plan(N, K, &nb, &sp);
+  return sp;
+}
+
+extern "C" DELTA_EXPORT int delta_gemm_rows32(const void *x, int64_t ldx, const void *w, int64_t ldw,
+                                              const void *bias, void *out, int64_t ldo, float *partials,
+                                              int M, int N, int K, int dtype, delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_gemm_rows32";
+  if (M <= 0 || N <= 0) return DELTA_OK;
+  if (!x || !w) return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (M > 32) return set_error(DELTA_ERR_INVALID, "%s: M (%d) must be <= 32", who, M);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
+  if (K <= 0 || K % 64) return set_error(DELTA_ERR_INVALID, "%s: K (%d) must be a positive multiple of 64", who, K);
+  if (N % 64) return set_error(DELTA_ERR_INVALID, "%s: N (%d) must be a multiple of 64", who, N);
+  if (ldx < K || ldw < K) return set_error(DELTA_ERR_INVALID, "%s: leading dimensions too small", who);
+  if ((ldx % 8) || (ldw % 8) || (((uintptr_t)x | (uintptr_t)w) & 15u))
+    return set_error(DELTA_ERR_INVALID, "%s: x and W rows must be 16-byte aligned", who);
+  int nb, sp;
+  rows32_plan(N, K, &nb, &sp);
+  if (sp == 1) {
+    if (!out || ldo < N || (ldo % 2) || ((uintptr_t)out & 3u))
+      return set_error(DELTA_ERR_INVALID, "%s: out must be [M, >= N] with 4-byte aligned rows", who);
+  } else if (!partials || ((uintptr_t)partials & 7u)) {
+    return set_error(DELTA_ERR_INVALID, "%s: this shape needs fp32 partials [%d][M][N] (8-byte aligned)", who, sp);
+  }
+  SplitArgs a;
+  a.x = (const uint16_t *)x;
+  a.ldx = ldx;
+  a.w = (const uint16_t *)w;
+  a.ldw = ldw;
+  a.bias = (const uint16_t *)bias;
+  a.out = (uint16_t *)out;
+  a.ldo = ldo;
+  a.part = partials;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ksplit = K / sp;
+  const dim3 grid(N / (64 * nb), sp), block(kGemmWaves * 64);
+  if (dtype == DELTA_BF16) {
+    if (nb == 2) hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 2>), grid, block, 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 1>), grid, block, 0, (hipStream_t)stream, a);
+  } else {
+    if (nb == 2) hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 2>), grid, block, 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 1>), grid, block, 0, (hipStream_t)stream, a);
+  }
+  return check_launch(who);
 }

@@ -17,15 +17,22 @@ namespace {
 
 constexpr int kNormThreads = 256;
 
-template <int DT>
+// PART: the residual is the sum of S fp32 partials (a split-K GEMM's, [S][rows][dim] with
+// split stride ps), rounded to the dtype once -- the value the unsplit GEMM would have written.
+template <int DT, bool PART>
 __global__ void __launch_bounds__(kNormThreads)
     add_rmsnorm_kernel(const uint16_t *x, int64_t xs, const uint16_t *r, int64_t rs, const uint16_t *w,
-                       float eps, uint16_t *h_out, int64_t hs, uint16_t *y, int64_t ys, int dim) {
+                       float eps, uint16_t *h_out, int64_t hs, uint16_t *y, int64_t ys, int dim,
+                       const float *part, int nsplit, int64_t ps) {
+  // No contraction: every product is rounded where the reference's ops round it (a fused
+  // multiply-round would also differ between the two instantiations).
+#pragma clang fp contract(off)
   using E = Elem<DT>;
   __shared__ float red[kNormThreads / 64];
   const int row = blockIdx.x;
   const uint16_t *xr = x + (int64_t)row * xs;
-  const uint16_t *rr = r ? r + (int64_t)row * rs : nullptr;
+  const uint16_t *rr = PART ? nullptr : (r ? r + (int64_t)row * rs : nullptr);
+  const float *pr = PART ? part + (int64_t)row * dim : nullptr;
   constexpr int kMaxChunks = 4;  // 8 elements per chunk -> dim <= 8192
   float hv[kMaxChunks][8];
   float ss = 0.f;
@@ -35,7 +42,27 @@ __global__ void __launch_bounds__(kNormThreads)
     if (c0 < dim) {
       const u32x4 a = ld128(xr + c0);
       u32x4 o;
-      if (rr) {
+      if (PART) {
+        float rs8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rs8[e] = 0.f;
+        for (int sp = 0; sp < nsplit; ++sp) {
+          const f32x4 p0 = *reinterpret_cast<const f32x4 *>(pr + sp * ps + c0);
+          const f32x4 p1 = *reinterpret_cast<const f32x4 *>(pr + sp * ps + c0 + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            rs8[e] += p0[e];
+            rs8[4 + e] += p1[e];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float r0 = E::lo(E::from_float(rs8[2 * q])), r1 = E::lo(E::from_float(rs8[2 * q + 1]));
+          const uint32_t lo = E::from_float(E::lo(a[q]) + r0);
+          const uint32_t hi = E::from_float(E::hi(a[q]) + r1);
+          o[q] = lo | (hi << 16);
+        }
+      } else if (rr) {
         const u32x4 bb = ld128(rr + c0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -53,7 +80,7 @@ __global__ void __launch_bounds__(kNormThreads)
         ss = fmaf(hv[k][2 * q], hv[k][2 * q], ss);
         ss = fmaf(hv[k][2 * q + 1], hv[k][2 * q + 1], ss);
       }
-      if (h_out && rr) st128(h_out + (int64_t)row * hs + c0, o);
+      if (h_out && (PART || rr)) st128(h_out + (int64_t)row * hs + c0, o);
     }
   }
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
@@ -71,8 +98,13 @@ __global__ void __launch_bounds__(kNormThreads)
       u32x4 o;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float n0 = E::lo(E::from_float(hv[k][2 * q] * inv));
-        const float n1 = E::lo(E::from_float(hv[k][2 * q + 1] * inv));
+        // h * inv is rounded to fp32 and then to the dtype, as the reference's fp32 RMSNorm
+        // followed by type_as does; the empty asm keeps the fp16 conversion from being folded
+        // into one mixed-precision fma (a single rounding, taken for some elements only).
+        float m0 = hv[k][2 * q] * inv, m1 = hv[k][2 * q + 1] * inv;
+        asm volatile("" : "+v"(m0), "+v"(m1));
+        const float n0 = E::lo(E::from_float(m0));
+        const float n1 = E::lo(E::from_float(m1));
         o[q] = E::from_float(n0 * E::lo(wv[q])) | (E::from_float(n1 * E::hi(wv[q])) << 16);
       }
       st128(y + (int64_t)row * ys + c0, o);
@@ -230,15 +262,15 @@ extern "C" DELTA_EXPORT int delta_add_rmsnorm(const void *x, int64_t x_stride, c
       (x_stride | r_stride | s_stride | out_stride) & 7)
     return set_error(DELTA_ERR_INVALID, "delta_add_rmsnorm: 16-byte aligned rows required");
   if (dtype == DELTA_BF16)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<DELTA_BF16>, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_BF16, false>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
                        (const uint16_t *)x, x_stride, (const uint16_t *)residual, r_stride,
                        (const uint16_t *)weight, eps, (uint16_t *)sum_out, s_stride, (uint16_t *)out, out_stride,
-                       dim);
+                       dim, nullptr, 0, 0);
   else if (dtype == DELTA_FP16)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<DELTA_FP16>, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_FP16, false>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
                        (const uint16_t *)x, x_stride, (const uint16_t *)residual, r_stride,
                        (const uint16_t *)weight, eps, (uint16_t *)sum_out, s_stride, (uint16_t *)out, out_stride,
-                       dim);
+                       dim, nullptr, 0, 0);
   else
     return set_error(DELTA_ERR_INVALID, "delta_add_rmsnorm: bad dtype");
   return check_launch("delta_add_rmsnorm");
@@ -262,4 +294,31 @@ extern "C" DELTA_EXPORT int delta_silu_mul(const void *gate_up, int64_t gu_strid
   else
     return set_error(DELTA_ERR_INVALID, "delta_silu_mul: bad dtype");
   return check_launch("delta_silu_mul");
+}
+
+extern "C" DELTA_EXPORT int delta_add_rmsnorm_partials(const void *x, int64_t x_stride, const float *partials,
+                                                       int nsplit, const void *weight, float eps, void *sum_out,
+                                                       int64_t s_stride, void *out, int64_t out_stride, int rows,
+                                                       int dim, int dtype, delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_add_rmsnorm_partials";
+  if (rows <= 0) return DELTA_OK;
+  if (!x || !partials || !weight || !out || nsplit <= 0 || dim <= 0 || dim % 8 || dim > 8 * 4 * kNormThreads)
+    return set_error(DELTA_ERR_INVALID, "%s: bad arguments (nsplit >= 1, dim %% 8 == 0, dim <= 8192)", who);
+  if (((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)sum_out | (uintptr_t)partials) & 15u ||
+      (x_stride | s_stride | out_stride) & 7)
+    return set_error(DELTA_ERR_INVALID, "%s: 16-byte aligned rows required", who);
+  const int64_t ps = (int64_t)rows * dim;
+  if (dtype == DELTA_BF16)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_BF16, true>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+                       (const uint16_t *)x, x_stride, nullptr, 0, (const uint16_t *)weight, eps, (uint16_t *)sum_out,
+                       s_stride, (uint16_t *)out, out_stride, dim, partials, nsplit, ps);
+  else if (dtype == DELTA_FP16)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_FP16, true>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+                       (const uint16_t *)x, x_stride, nullptr, 0, (const uint16_t *)weight, eps, (uint16_t *)sum_out,
+                       s_stride, (uint16_t *)out, out_stride, dim, partials, nsplit, ps);
+  else
+    return set_error(DELTA_ERR_INVALID, "%s: bad dtype", who);
+  return check_launch(who);
 }

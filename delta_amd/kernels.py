@@ -543,6 +543,8 @@ def add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch
                 out: Optional[torch.Tensor] = None):
     """(x + residual, RMSNorm(x + residual) * weight) in one kernel (``delta_add_rmsnorm``).
 
+    ``residual`` may also be the fp32 partials ``[S, rows, dim]`` of a split-K
+    ``gemm_rows32`` (``delta_add_rmsnorm_partials``: summed and rounded to x's dtype first).
     Returns ``(h, y)``; ``h`` is ``x`` itself when ``residual`` is None."""
     dev = _check_cuda(x, residual, weight, out)
     dim = x.shape[-1]
@@ -551,6 +553,18 @@ def add_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch
         raise ValueError("weight must be a contiguous [dim] tensor of x's dtype")
     x2 = _rows2d("x", x, dim)
     rows = x2.shape[0]
+    if residual is not None and residual.dtype == torch.float32 and x.dtype != torch.float32:
+        if residual.dim() != 3 or tuple(residual.shape[1:]) != (rows, dim) or not residual.is_contiguous():
+            raise ValueError(f"partials must be contiguous fp32 [S, {rows}, {dim}]")
+        h = torch.empty_like(x)
+        h2 = _rows2d("h", h, dim)
+        if out is None:
+            out = torch.empty_like(x)
+        o2 = _rows2d("out", out, dim)
+        _lib.call("delta_add_rmsnorm_partials", x2.data_ptr(), x2.stride(0), residual.data_ptr(),
+                  int(residual.shape[0]), weight.data_ptr(), float(eps), h2.data_ptr(), h2.stride(0),
+                  o2.data_ptr(), o2.stride(0), int(rows), int(dim), _dtype_code(x), _stream(dev))
+        return h, out
     h = x if residual is None else torch.empty_like(x)
     r2 = None if residual is None else _rows2d("residual", residual, dim)
     h2 = None if residual is None else _rows2d("h", h, dim)
@@ -585,6 +599,49 @@ def gemm_skinny_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
     rows = x.numel() // max(x.shape[-1], 1)
     return (x.shape[-1] == Kd and Kd % 64 == 0 and N % 16 == 0 and 0 < rows <= 32
             and weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def gemm_rows32_splits(M: int, N: int, K: int) -> int:
+    """K splits ``delta_gemm_rows32`` uses for this shape (1: rounded output; > 1: fp32 partials)."""
+    return int(_lib.query("delta_gemm_rows32_splits", int(M), int(N), int(K)))
+
+
+def gemm_rows32(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None, partials: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x @ weight.T (+ bias)`` for <= 32 token rows on ``delta_gemm_rows32``.
+
+    Returns the rounded output ``[..., N]`` when the shape runs unsplit, else the fp32 partials
+    ``[S, M, N]`` whose sum over S is the product (bias included once)."""
+    dev = _check_cuda(x, weight, bias, out, partials)
+    N, Kd = weight.shape
+    if x.shape[-1] != Kd:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects {Kd}")
+    if weight.dtype != x.dtype or (bias is not None and (bias.dtype != x.dtype or bias.numel() != N
+                                                         or not bias.is_contiguous())):
+        raise TypeError("x, weight and bias must share a dtype; bias must be contiguous [N]")
+    if weight.stride(1) != 1:
+        raise ValueError("weight rows must be contiguous")
+    x2 = _rows2d("x", x, Kd)
+    M = x2.shape[0]
+    S = gemm_rows32_splits(M, N, Kd)
+    if S < 1:
+        raise ValueError(f"delta_gemm_rows32 does not take [{M}, {Kd}] x [{N}, {Kd}]^T")
+    o2 = None
+    if S == 1:
+        if out is None:
+            out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
+        o2 = out.reshape(-1, N)
+        if o2.stride(1) != 1 or o2.shape[0] != M:
+            raise ValueError("out must be [..., N] with contiguous rows")
+    else:
+        if partials is None:
+            partials = torch.empty(S, M, N, dtype=torch.float32, device=dev)
+        if partials.dtype != torch.float32 or not partials.is_contiguous() or tuple(partials.shape) != (S, M, N):
+            raise ValueError(f"partials must be contiguous fp32 [{S}, {M}, {N}]")
+    _lib.call("delta_gemm_rows32", x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _ptr(bias),
+              o2.data_ptr() if o2 is not None else None, o2.stride(0) if o2 is not None else 0,
+              partials.data_ptr() if S > 1 else None, int(M), int(N), int(Kd), _dtype_code(x), _stream(dev))
+    return out if S == 1 else partials
 
 
 def gemm_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,

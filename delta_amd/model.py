@@ -209,6 +209,25 @@ def dense(x: Tensor, layer: nn.Linear) -> Tensor:
     return layer(x)
 
 
+# Projections whose only consumer is the next fused add + RMSNorm (wo, w2) go to delta_gemm_rows32
+# at 9-32 token rows: it stages x in LDS per block and splits K across the grid, handing the
+# norm fp32 partials to sum (Llama-3-8B at 32 rows: wo 9.5 vs 14.0 us, w2 24.6 vs 32.8 on
+# hipBLASLt).  wqkv and the merged w1|w3 stay on hipBLASLt there (no gain without a consumer
+# that sums partials, the same time for w1|w3).
+_ROWS32_MAX = 32
+
+
+def dense_to_norm(x: Tensor, layer: nn.Linear):
+    """``layer(x)`` for a consumer that is ``K.add_rmsnorm``: the output, or the fp32 partials
+    ``[S, rows, N]`` of a split-K ``delta_gemm_rows32`` that the norm sums."""
+    w = layer.weight
+    rows = x.numel() // x.shape[-1]
+    if rows > _SKINNY_ROWS_ANY and rows <= _ROWS32_MAX and K.gemm_skinny_ok(x, w) and w.shape[0] % 64 == 0:
+        r = K.gemm_rows32(x, w, layer.bias)
+        return r if r.dtype == torch.float32 else r.view(*x.shape[:-1], w.shape[0])
+    return dense(x, layer)
+
+
 class TransformerBlock(nn.Module):
     def __init__(self, config: ModelArgs) -> None:
         super().__init__()
@@ -283,7 +302,7 @@ class Attention(nn.Module):
         if self.record is not None:
             self.record.append((q.detach().clone(), y.detach().clone()))
         y = y.contiguous().view(bsz, seqlen, self.dim)
-        return lin(y, self.wo)
+        return dense_to_norm(y, self.wo) if fused else lin(y, self.wo)
 
 
 class FeedForward(nn.Module):
@@ -328,8 +347,9 @@ class FeedForward(nn.Module):
         g, u = self._gate_up(x).split(self.inter, dim=-1)
         return self.w2(F.silu(g) * u)
 
-    def forward_fused(self, x: Tensor) -> Tensor:
-        return dense(K.silu_mul(self._gate_up(x)), self.w2)
+    def forward_fused(self, x: Tensor):
+        """The block's FFN output for the next fused add + norm (maybe as fp32 partials)."""
+        return dense_to_norm(K.silu_mul(self._gate_up(x)), self.w2)
 
 
 class RMSNorm(nn.Module):

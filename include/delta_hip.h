@@ -364,6 +364,13 @@ int delta_add_rmsnorm(const void *x, int64_t x_stride, const void *residual, int
                       const void *weight, float eps, void *sum_out, int64_t s_stride, void *out,
                       int64_t out_stride, int rows, int dim, int dtype, delta_stream_t stream);
 
+/* delta_add_rmsnorm with the residual given as nsplit fp32 partials [nsplit][rows][dim]
+ * (contiguous, a split-K delta_gemm_rows32's output): residual = dtype(sum of the partials in
+ * split order), then the same h and out.  Same limits; partials 16-byte aligned. */
+int delta_add_rmsnorm_partials(const void *x, int64_t x_stride, const float *partials, int nsplit,
+                               const void *weight, float eps, void *sum_out, int64_t s_stride, void *out,
+                               int64_t out_stride, int rows, int dim, int dtype, delta_stream_t stream);
+
 /* out[r, i] = dtype(dtype(silu(g)) * u) with g = gate_up[r, i], u = gate_up[r, inter + i]:
  * FeedForward's silu(w1 x) * w3 x (model.py:509-514) on the merged w1|w3 GEMM output. */
 int delta_silu_mul(const void *gate_up, int64_t gu_stride, void *out, int64_t out_stride, int rows,
@@ -377,6 +384,21 @@ int delta_silu_mul(const void *gate_up, int64_t gu_stride, void *out, int64_t ou
  * rows 16-byte aligned.  Built for M <= 32 (larger M works, re-reading w per 32 rows). */
 int delta_gemm_skinny(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *bias,
                       void *out, int64_t ldo, int M, int N, int K, int dtype, delta_stream_t stream);
+
+/* K splits delta_gemm_rows32 uses for an [M, K] x [N, K]^T product (depends only on the
+ * shape): 1 = it writes the rounded output, S > 1 = it writes fp32 partials [S][M][N];
+ * 0 = the shape is not taken (M, K % 64 or N % 64). */
+int delta_gemm_rows32_splits(int M, int N, int K);
+
+/* The same decode projections as delta_gemm_skinny for M <= 32 token rows, with x staged in
+ * LDS once per block and K split across the grid so that narrow weights still fill the GPU.
+ * With delta_gemm_rows32_splits(M, N, K) == 1: out [M, N] (row stride ldo, even, 4-byte
+ * aligned rows) = dtype(x w^T + bias).  With S > 1: partials [S][M][N] fp32 (contiguous,
+ * 8-byte aligned), sum over S = x w^T + bias (bias in split 0 only), for a consumer that sums
+ * them (delta_add_rmsnorm_partials); out is unused.  K % 64 == 0,
+ * N % 64 == 0, x and w rows 16-byte aligned. */
+int delta_gemm_rows32(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *bias, void *out,
+                      int64_t ldo, float *partials, int M, int N, int K, int dtype, delta_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -605,3 +605,52 @@ def test_decode_append_equals_rope_append_then_decode(hq, hkv, dtype, llama31, b
         outs.append((o, cache))
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,Kd,bias", [(32, 4096, 4096, False), (32, 6144, 4096, True), (17, 4096, 14336, False),
+                                        (32, 28672, 4096, False), (1, 64, 64, True), (32, 128256, 1024, False),
+                                        (9, 192, 640, True)])
+def test_gemm_rows32_matches_fp32_reference(dtype, M, N, Kd, bias):
+    """delta_gemm_rows32 (x staged in LDS, K split across the grid) against x.float() @ w.float().T
+    (+ b): the fp32 partials sum to the product; the unsplit output is it rounded once."""
+    gen = torch.Generator(device=DEV).manual_seed(M * 3 + N + Kd)
+    x = torch.randn(M, Kd, generator=gen, device=DEV).to(dtype)
+    w = (torch.randn(N, Kd, generator=gen, device=DEV) * 0.05).to(dtype)
+    b = (torch.randn(N, generator=gen, device=DEV) * 0.1).to(dtype) if bias else None
+    S = K.gemm_rows32_splits(M, N, Kd)
+    r = K.gemm_rows32(x, w, b)
+    r2 = K.gemm_rows32(x, w, b)
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().T + (b.float() if bias else 0.0)
+    mag = x.float().abs() @ w.float().abs().T
+    if S == 1:
+        assert r.dtype == dtype and tuple(r.shape) == (M, N)
+        err = (r.float() - ref).abs()
+        assert torch.all(err <= torch.finfo(dtype).eps * ref.abs() + 1e-5 * mag + 1e-6), f"max err {err.max().item()}"
+    else:
+        assert r.dtype == torch.float32 and tuple(r.shape) == (S, M, N)
+        err = (r.sum(0) - ref).abs()
+        assert torch.all(err <= 1e-5 * mag + 1e-6), f"max err {err.max().item()}"
+    assert torch.equal(r, r2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_add_rmsnorm_over_partials_equals_rounded_sum(dtype):
+    """delta_add_rmsnorm_partials (the norm after a split-K projection) gives bit for bit what
+    delta_add_rmsnorm gives on the partials' sum (split order) rounded to the dtype."""
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    M, N, Kd = 32, 4096, 4096
+    xin = torch.randn(M, Kd, generator=gen, device=DEV).to(dtype)
+    w = (torch.randn(N, Kd, generator=gen, device=DEV) * 0.02).to(dtype)
+    x = torch.randn(M, N, generator=gen, device=DEV).to(dtype)
+    nw = (1 + 0.1 * torch.randn(N, generator=gen, device=DEV)).to(dtype)
+    parts = K.gemm_rows32(xin, w)
+    assert parts.dtype == torch.float32 and parts.shape[0] > 1
+    h, y = K.add_rmsnorm(x, parts, nw, 1e-5)
+    r = parts[0].clone()
+    for s in range(1, parts.shape[0]):
+        r += parts[s]
+    h2, y2 = K.add_rmsnorm(x, r.to(dtype), nw, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2) and torch.equal(y, y2)

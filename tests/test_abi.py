@@ -87,6 +87,25 @@ def test_argument_errors_reported_without_launch(lib):
         _lib.call("delta_select_pages", 8, 4, 8, 8, 4, 1, 4, 5, None, 1, 1e-7, 0, None, 8, 4, 8, None)
 
 
+def test_gemm_rows32_plan_and_errors_without_launch(lib):
+    from delta_amd import _lib
+    # splits: enough (N / 64 NB) x S blocks for 256 CUs, S dividing K / 64; 0 = shape not taken
+    assert lib.delta_gemm_rows32_splits(32, 4096, 4096) == 4      # Llama-3-8B wo
+    assert lib.delta_gemm_rows32_splits(32, 4096, 14336) == 8     # w2: two column groups per wave
+    assert lib.delta_gemm_rows32_splits(32, 28672, 4096) == 1     # w1|w3: 448 blocks, unsplit
+    assert lib.delta_gemm_rows32_splits(32, 4100, 4096) == 0      # N % 64
+    assert lib.delta_gemm_rows32_splits(32, 4096, 4000) == 0      # K % 64
+    # rejected before any launch (null x / w are checked after the shape)
+    with pytest.raises(_lib.DeltaHipError, match="M .* must be <= 32"):
+        _lib.call("delta_gemm_rows32", 16, 4096, 16, 4096, None, 16, 4096, 16, 33, 4096, 4096, 0, None)
+    with pytest.raises(_lib.DeltaHipError, match="multiple of 64"):
+        _lib.call("delta_gemm_rows32", 16, 4096, 16, 4096, None, 16, 4100, 16, 32, 4100, 4096, 0, None)
+    with pytest.raises(_lib.DeltaHipError, match="fp32 partials"):
+        _lib.call("delta_gemm_rows32", 16, 4096, 16, 4096, None, 16, 4096, None, 32, 4096, 4096, 0, None)
+    with pytest.raises(_lib.DeltaHipError, match="nsplit >= 1"):
+        _lib.call("delta_add_rmsnorm_partials", 16, 4096, 16, 0, 16, 1e-5, 16, 4096, 16, 4096, 32, 4096, 0, None)
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="stand-in addresses: validation-only, run where no GPU is visible")
 def test_append_descriptor_errors_reported_without_launch(lib):
     from delta_amd import _lib

@@ -10,6 +10,8 @@
 //   argmax_rows : torch.argmax(logits, -1) of _finalize_logits (model.py:320-323), two
 //                 passes (row chunks, then per row), no memset.
 // Each kernel rounds where the reference's bf16 tensor ops round.
+#include <type_traits>
+
 #include "delta_common.h"
 
 namespace delta {
@@ -17,16 +19,18 @@ namespace {
 
 constexpr int kNormThreads = 256;
 
-// PART: the residual is the sum of S fp32 partials (a split-K GEMM's, [S][rows][dim] with
+// PS > 0: the residual is the sum of PS fp32 partials (a split-K GEMM's, [PS][rows][dim] with
 // split stride ps), rounded to the dtype once -- the value the unsplit GEMM would have written.
-template <int DT, bool PART>
+// All PS loads of a chunk are issued before the first add (one round trip, not PS).
+template <int DT, int PS>
 __global__ void __launch_bounds__(kNormThreads)
     add_rmsnorm_kernel(const uint16_t *x, int64_t xs, const uint16_t *r, int64_t rs, const uint16_t *w,
                        float eps, uint16_t *h_out, int64_t hs, uint16_t *y, int64_t ys, int dim,
-                       const float *part, int nsplit, int64_t ps) {
+                       const float *part, int64_t ps) {
   // No contraction: every product is rounded where the reference's ops round it (a fused
-  // multiply-round would also differ between the two instantiations).
+  // multiply-round would also differ between the instantiations).
 #pragma clang fp contract(off)
+  constexpr bool PART = PS > 0;
   using E = Elem<DT>;
   __shared__ float red[kNormThreads / 64];
   const int row = blockIdx.x;
@@ -43,18 +47,22 @@ __global__ void __launch_bounds__(kNormThreads)
       const u32x4 a = ld128(xr + c0);
       u32x4 o;
       if (PART) {
+        f32x4 pv[PS > 0 ? PS : 1][2];
+#pragma unroll
+        for (int sp = 0; sp < PS; ++sp) {
+          pv[sp][0] = *reinterpret_cast<const f32x4 *>(pr + sp * ps + c0);
+          pv[sp][1] = *reinterpret_cast<const f32x4 *>(pr + sp * ps + c0 + 4);
+        }
         float rs8[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) rs8[e] = 0.f;
-        for (int sp = 0; sp < nsplit; ++sp) {
-          const f32x4 p0 = *reinterpret_cast<const f32x4 *>(pr + sp * ps + c0);
-          const f32x4 p1 = *reinterpret_cast<const f32x4 *>(pr + sp * ps + c0 + 4);
+#pragma unroll
+        for (int sp = 0; sp < PS; ++sp)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            rs8[e] += p0[e];
-            rs8[4 + e] += p1[e];
+            rs8[e] += pv[sp][0][e];
+            rs8[4 + e] += pv[sp][1][e];
           }
-        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float r0 = E::lo(E::from_float(rs8[2 * q])), r1 = E::lo(E::from_float(rs8[2 * q + 1]));
@@ -262,15 +270,15 @@ extern "C" DELTA_EXPORT int delta_add_rmsnorm(const void *x, int64_t x_stride, c
       (x_stride | r_stride | s_stride | out_stride) & 7)
     return set_error(DELTA_ERR_INVALID, "delta_add_rmsnorm: 16-byte aligned rows required");
   if (dtype == DELTA_BF16)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_BF16, false>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_BF16, 0>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
                        (const uint16_t *)x, x_stride, (const uint16_t *)residual, r_stride,
                        (const uint16_t *)weight, eps, (uint16_t *)sum_out, s_stride, (uint16_t *)out, out_stride,
-                       dim, nullptr, 0, 0);
+                       dim, nullptr, 0);
   else if (dtype == DELTA_FP16)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_FP16, false>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_FP16, 0>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
                        (const uint16_t *)x, x_stride, (const uint16_t *)residual, r_stride,
                        (const uint16_t *)weight, eps, (uint16_t *)sum_out, s_stride, (uint16_t *)out, out_stride,
-                       dim, nullptr, 0, 0);
+                       dim, nullptr, 0);
   else
     return set_error(DELTA_ERR_INVALID, "delta_add_rmsnorm: bad dtype");
   return check_launch("delta_add_rmsnorm");
@@ -304,21 +312,30 @@ extern "C" DELTA_EXPORT int delta_add_rmsnorm_partials(const void *x, int64_t x_
   clear_error();
   const char *who = "delta_add_rmsnorm_partials";
   if (rows <= 0) return DELTA_OK;
-  if (!x || !partials || !weight || !out || nsplit <= 0 || dim <= 0 || dim % 8 || dim > 8 * 4 * kNormThreads)
-    return set_error(DELTA_ERR_INVALID, "%s: bad arguments (nsplit >= 1, dim %% 8 == 0, dim <= 8192)", who);
+  if (!x || !partials || !weight || !out || dim <= 0 || dim % 8 || dim > 8 * 4 * kNormThreads)
+    return set_error(DELTA_ERR_INVALID, "%s: bad arguments (dim %% 8 == 0, dim <= 8192)", who);
+  if (nsplit != 2 && nsplit != 4 && nsplit != 8 && nsplit != 16)
+    return set_error(DELTA_ERR_INVALID, "%s: nsplit must be 2, 4, 8 or 16 (delta_gemm_rows32's splits)", who);
   if (((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)sum_out | (uintptr_t)partials) & 15u ||
       (x_stride | s_stride | out_stride) & 7)
     return set_error(DELTA_ERR_INVALID, "%s: 16-byte aligned rows required", who);
   const int64_t ps = (int64_t)rows * dim;
-  if (dtype == DELTA_BF16)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_BF16, true>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+  auto launch = [&](auto dt_tag, auto ps_tag) {
+    constexpr int DT = decltype(dt_tag)::value, PSN = decltype(ps_tag)::value;
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DT, PSN>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
                        (const uint16_t *)x, x_stride, nullptr, 0, (const uint16_t *)weight, eps, (uint16_t *)sum_out,
-                       s_stride, (uint16_t *)out, out_stride, dim, partials, nsplit, ps);
-  else if (dtype == DELTA_FP16)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<DELTA_FP16, true>), dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
-                       (const uint16_t *)x, x_stride, nullptr, 0, (const uint16_t *)weight, eps, (uint16_t *)sum_out,
-                       s_stride, (uint16_t *)out, out_stride, dim, partials, nsplit, ps);
-  else
-    return set_error(DELTA_ERR_INVALID, "%s: bad dtype", who);
+                       s_stride, (uint16_t *)out, out_stride, dim, partials, ps);
+  };
+  auto by_splits = [&](auto dt_tag) {
+    switch (nsplit) {
+      case 2: launch(dt_tag, std::integral_constant<int, 2>{}); break;
+      case 4: launch(dt_tag, std::integral_constant<int, 4>{}); break;
+      case 8: launch(dt_tag, std::integral_constant<int, 8>{}); break;
+      default: launch(dt_tag, std::integral_constant<int, 16>{}); break;
+    }
+  };
+  if (dtype == DELTA_BF16) by_splits(std::integral_constant<int, DELTA_BF16>{});
+  else if (dtype == DELTA_FP16) by_splits(std::integral_constant<int, DELTA_FP16>{});
+  else return set_error(DELTA_ERR_INVALID, "%s: bad dtype", who);
   return check_launch(who);
 }

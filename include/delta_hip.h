@@ -366,7 +366,8 @@ int delta_add_rmsnorm(const void *x, int64_t x_stride, const void *residual, int
 
 /* delta_add_rmsnorm with the residual given as nsplit fp32 partials [nsplit][rows][dim]
  * (contiguous, a split-K delta_gemm_rows32's output): residual = dtype(sum of the partials in
- * split order), then the same h and out.  Same limits; partials 16-byte aligned. */
+ * split order), then the same h and out.  nsplit is 2, 4, 8 or 16 (the splits
+ * delta_gemm_rows32 makes).  Same limits; partials 16-byte aligned. */
 int delta_add_rmsnorm_partials(const void *x, int64_t x_stride, const float *partials, int nsplit,
                                const void *weight, float eps, void *sum_out, int64_t s_stride, void *out,
                                int64_t out_stride, int rows, int dim, int dtype, delta_stream_t stream);

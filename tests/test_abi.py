@@ -102,7 +102,7 @@ def test_gemm_rows32_plan_and_errors_without_launch(lib):
         _lib.call("delta_gemm_rows32", 16, 4096, 16, 4096, None, 16, 4100, 16, 32, 4100, 4096, 0, None)
     with pytest.raises(_lib.DeltaHipError, match="fp32 partials"):
         _lib.call("delta_gemm_rows32", 16, 4096, 16, 4096, None, 16, 4096, None, 32, 4096, 4096, 0, None)
-    with pytest.raises(_lib.DeltaHipError, match="nsplit >= 1"):
+    with pytest.raises(_lib.DeltaHipError, match="nsplit must be 2, 4, 8 or 16"):
         _lib.call("delta_add_rmsnorm_partials", 16, 4096, 16, 0, 16, 1e-5, 16, 4096, 16, 4096, 32, 4096, 0, None)
 
 

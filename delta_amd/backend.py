@@ -174,8 +174,9 @@ class LMBackend:
         dev = self.device
         self.max_length = max_seq_length
         self.batch_size = max_batch_size
-        if max_batch_size <= model_mod._SKINNY_ROWS_ANY:
-            # every decode GEMM of this engine runs on delta_gemm_skinny, the gate|up one too
+        if max_batch_size <= model_mod._ROWS32_MAX:
+            # the gate|up GEMM of this engine's decode steps runs on delta_gemm_skinny (<= 8
+            # rows) or delta_gemm_rows32_silu, both on the row-major merged weight
             for layer in self.model.layers:
                 layer.feed_forward.use_row_major_w13()
         self.page_size = PAGE_SIZE

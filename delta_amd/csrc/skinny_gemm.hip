@@ -199,16 +199,23 @@ struct SplitArgs {
   int64_t ldo;
   float *part;      // S > 1: [S][M][N]
   int M, N, K, ksplit;  // ksplit: k per split (multiple of 64)
+  int inter;        // GLU: out [M][inter] = silu(gate) * up of W = [gate rows; up rows]
 };
 
-template <int DT, int NB>
+// GLU (the merged w1|w3 GEMM and SiLU-mul, FeedForward model.py:509-514): NB = 1, unsplit; waves
+// 0-3 of block b own gate columns 32 b + [0, 32), waves 4-7 the up columns inter + 32 b + [0, 32),
+// and the block writes dtype(dtype(silu(g)) * u) with g and u rounded to the dtype first (what
+// the GEMM and then delta_silu_mul compute).
+template <int DT, int NB, bool GLU>
 __global__ void __launch_bounds__(kGemmWaves * 64) gemm_rows32_kernel(SplitArgs a) {
   using E = Elem<DT>;
   __shared__ u32x4 xs[2][kXFrag];  // 2 x 32 KiB
   constexpr int D = 4;  // k steps of W in flight per wave (8 slots spill, 2 leave HBM idle)
+  static_assert(!GLU || NB == 1, "the GLU epilogue pairs one 8-column group per wave");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane >> 4, t = lane & 15;
-  const int ncol = blockIdx.x * (64 * NB) + wave * (8 * NB);
+  const int ncol = GLU ? (wave >= 4 ? a.inter : 0) + blockIdx.x * 32 + (wave & 3) * 8
+                       : blockIdx.x * (64 * NB) + wave * (8 * NB);
   const int kb = blockIdx.y * a.ksplit;
   const int ke = min(a.K, kb + a.ksplit);
   const int total = ke > kb ? (ke - kb) / 64 : 0;  // k steps of this split
@@ -290,6 +297,40 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm_rows32_kernel(SplitArgs 
   }
 
   // Join the k slices: lane (c, v < 8) holds columns ncol + 8 nb + 2c + {0, 1} of row 8 tg + v.
+  if (GLU) {
+    // Up waves park dtype(up) in LDS ([32 rows][32 columns], the x buffers are free once every
+    // wave left the loop); gate waves finish silu(g) * u and write the block's 32 columns.
+    float *upv = reinterpret_cast<float *>(&xs[0][0]);
+    __syncthreads();
+#pragma unroll
+    for (int tg = 0; tg < 4; ++tg) {
+      const float s0v = acc[0][tg][0] + dpp_f<0x128>(acc[0][tg][1]);
+      const float s1v = acc[0][tg][2] + dpp_f<0x128>(acc[0][tg][3]);
+      if (wave >= 4 && t < 8) {
+        float *u = upv + (8 * tg + t) * 32 + (wave & 3) * 8 + 2 * c;
+        u[0] = E::lo(E::from_float(s0v));
+        u[1] = E::lo(E::from_float(s1v));
+      }
+    }
+    __syncthreads();
+    if (wave < 4) {
+#pragma unroll
+      for (int tg = 0; tg < 4; ++tg) {
+        const float s0v = acc[0][tg][0] + dpp_f<0x128>(acc[0][tg][1]);
+        const float s1v = acc[0][tg][2] + dpp_f<0x128>(acc[0][tg][3]);
+        const int row = 8 * tg + t;
+        if (t < 8 && row < a.M) {
+          const float *u = upv + row * 32 + wave * 8 + 2 * c;
+          const float g0 = E::lo(E::from_float(s0v)), g1 = E::lo(E::from_float(s1v));
+          const float h0 = E::lo(E::from_float(g0 / (1.f + expf(-g0))));
+          const float h1 = E::lo(E::from_float(g1 / (1.f + expf(-g1))));
+          const uint32_t pk = E::from_float(h0 * u[0]) | (E::from_float(h1 * u[1]) << 16);
+          *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.ldo + ncol + 2 * c) = pk;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -405,13 +446,52 @@ extern "C" DELTA_EXPORT int delta_gemm_rows32(const void *x, int64_t ldx, const 
   a.N = N;
   a.K = K;
   a.ksplit = K / sp;
+  a.inter = 0;
   const dim3 grid(N / (64 * nb), sp), block(kGemmWaves * 64);
   if (dtype == DELTA_BF16) {
-    if (nb == 2) hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 2>), grid, block, 0, (hipStream_t)stream, a);
-    else hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 1>), grid, block, 0, (hipStream_t)stream, a);
+    if (nb == 2) hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 2, false>), grid, block, 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 1, false>), grid, block, 0, (hipStream_t)stream, a);
   } else {
-    if (nb == 2) hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 2>), grid, block, 0, (hipStream_t)stream, a);
-    else hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 1>), grid, block, 0, (hipStream_t)stream, a);
+    if (nb == 2) hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 2, false>), grid, block, 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 1, false>), grid, block, 0, (hipStream_t)stream, a);
   }
+  return check_launch(who);
+}
+
+extern "C" DELTA_EXPORT int delta_gemm_rows32_silu(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out,
+                                                   int64_t ldo, int M, int inter, int K, int dtype,
+                                                   delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_gemm_rows32_silu";
+  if (M <= 0 || inter <= 0) return DELTA_OK;
+  if (!x || !w13 || !out) return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (M > 32) return set_error(DELTA_ERR_INVALID, "%s: M (%d) must be <= 32", who, M);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
+  if (K <= 0 || K % 64) return set_error(DELTA_ERR_INVALID, "%s: K (%d) must be a positive multiple of 64", who, K);
+  if (inter % 32) return set_error(DELTA_ERR_INVALID, "%s: inter (%d) must be a multiple of 32", who, inter);
+  if (ldx < K || ldw < K || ldo < inter || (ldo % 2) || ((uintptr_t)out & 3u))
+    return set_error(DELTA_ERR_INVALID, "%s: leading dimensions too small or out rows not 4-byte aligned", who);
+  if ((ldx % 8) || (ldw % 8) || (((uintptr_t)x | (uintptr_t)w13) & 15u))
+    return set_error(DELTA_ERR_INVALID, "%s: x and W rows must be 16-byte aligned", who);
+  SplitArgs a;
+  a.x = (const uint16_t *)x;
+  a.ldx = ldx;
+  a.w = (const uint16_t *)w13;
+  a.ldw = ldw;
+  a.bias = nullptr;
+  a.out = (uint16_t *)out;
+  a.ldo = ldo;
+  a.part = nullptr;
+  a.M = M;
+  a.N = 2 * inter;
+  a.K = K;
+  a.ksplit = K;
+  a.inter = inter;
+  const dim3 grid(inter / 32, 1), block(kGemmWaves * 64);
+  if (dtype == DELTA_BF16)
+    hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 1, true>), grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 1, true>), grid, block, 0, (hipStream_t)stream, a);
   return check_launch(who);
 }

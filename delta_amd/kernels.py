@@ -644,6 +644,28 @@ def gemm_rows32(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tens
     return out if S == 1 else partials
 
 
+def gemm_rows32_silu(x: torch.Tensor, w13: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``silu(x @ w1.T) * (x @ w3.T)`` for <= 32 token rows in one launch (``delta_gemm_rows32_silu``);
+    ``w13`` is the row-major merged ``[2 * inter, dim]`` weight (w1 rows, then w3 rows)."""
+    dev = _check_cuda(x, w13, out)
+    N2, Kd = w13.shape
+    inter = N2 // 2
+    if x.shape[-1] != Kd or N2 % 2:
+        raise ValueError("x must be [..., dim] and w13 [2 * inter, dim]")
+    if w13.dtype != x.dtype or w13.stride(1) != 1:
+        raise ValueError("w13 must share x's dtype and have contiguous rows")
+    x2 = _rows2d("x", x, Kd)
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(*x.shape[:-1], inter, dtype=x.dtype, device=dev)
+    o2 = out.reshape(-1, inter)
+    if o2.stride(1) != 1 or o2.shape[0] != M:
+        raise ValueError("out must be [..., inter] with contiguous rows")
+    _lib.call("delta_gemm_rows32_silu", x2.data_ptr(), x2.stride(0), w13.data_ptr(), w13.stride(0), o2.data_ptr(),
+              o2.stride(0), int(M), int(inter), int(Kd), _dtype_code(x), _stream(dev))
+    return out
+
+
 def gemm_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``F.linear(x, weight, bias)`` for decode-sized x on ``delta_gemm_skinny``."""

@@ -309,9 +309,10 @@ class FeedForward(nn.Module):
     """SwiGLU FFN.  ``w1`` and ``w3`` live in one weight stored transposed, ``w13_t``
     ``[dim, 2 * inter]``, so the gate and up projections are one GEMM ``x @ w13_t``: at
     32-row decode batches hipBLASLt streams this layout at ~5.2 TB/s against ~4.4 TB/s for
-    ``x @ w13.T``.  An engine set up for at most 8 rows per step re-lays it out row-major
-    (``w13`` ``[2 * inter, dim]``, ``use_row_major_w13``) for ``delta_gemm_skinny``, which streams
-    it faster still (Qwen2.5-7B, 4 rows: 41 vs 53 us).  Checkpoints with separate ``w1`` /
+    ``x @ w13.T``.  An engine set up for at most 32 rows per step re-lays it out row-major
+    (``w13`` ``[2 * inter, dim]``, ``use_row_major_w13``): ``delta_gemm_skinny`` streams it faster
+    still at <= 8 rows (Qwen2.5-7B, 4 rows: 41 vs 53 us) and ``delta_gemm_rows32_silu`` fuses the
+    SiLU-mul into the GEMM at 9-32 rows.  Checkpoints with separate ``w1`` /
     ``w3`` (the reference's names, ``[inter, dim]`` each) are merged and transposed on load."""
 
     def __init__(self, config: ModelArgs) -> None:
@@ -349,6 +350,11 @@ class FeedForward(nn.Module):
 
     def forward_fused(self, x: Tensor):
         """The block's FFN output for the next fused add + norm (maybe as fp32 partials)."""
+        rows = x.numel() // x.shape[-1]
+        if (hasattr(self, "w13") and _SKINNY_ROWS_ANY < rows <= _ROWS32_MAX and self.inter % 32 == 0
+                and K.gemm_skinny_ok(x, self.w13)):
+            # gate/up GEMM and SiLU-mul in one launch (same bits as the two)
+            return dense_to_norm(K.gemm_rows32_silu(x, self.w13), self.w2)
         return dense_to_norm(K.silu_mul(self._gate_up(x)), self.w2)
 
 

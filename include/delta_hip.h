@@ -401,6 +401,14 @@ int delta_gemm_rows32_splits(int M, int N, int K);
 int delta_gemm_rows32(const void *x, int64_t ldx, const void *w, int64_t ldw, const void *bias, void *out,
                       int64_t ldo, float *partials, int M, int N, int K, int dtype, delta_stream_t stream);
 
+/* FeedForward's gate/up projections and SiLU-mul (model.py:509-514) in one launch for M <= 32
+ * rows: w13 [2 * inter, K] row-major (row stride ldw) holds w1's rows then w3's; out [M, inter]
+ * (row stride ldo, even, 4-byte aligned rows) = dtype(dtype(silu(g)) * u) with g = dtype(x w1^T),
+ * u = dtype(x w3^T): bit for bit delta_gemm_rows32 (unsplit) followed by delta_silu_mul.
+ * inter % 32 == 0, K % 64 == 0, x and w13 rows 16-byte aligned. */
+int delta_gemm_rows32_silu(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out, int64_t ldo,
+                           int M, int inter, int K, int dtype, delta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -654,3 +654,21 @@ def test_add_rmsnorm_over_partials_equals_rounded_sum(dtype):
     h2, y2 = K.add_rmsnorm(x, r.to(dtype), nw, 1e-5)
     torch.cuda.synchronize()
     assert torch.equal(h, h2) and torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,inter,Kd", [(32, 14336, 4096), (13, 1024, 640), (32, 18944, 3584)])
+def test_gemm_rows32_silu_equals_gemm_then_silu_mul(dtype, M, inter, Kd):
+    """The fused gate/up GEMM + SiLU-mul writes the bits of delta_gemm_rows32 (unsplit, the same
+    per-column sums) followed by delta_silu_mul."""
+    gen = torch.Generator(device=DEV).manual_seed(M + inter + Kd)
+    x = torch.randn(M, Kd, generator=gen, device=DEV).to(dtype)
+    w13 = (torch.randn(2 * inter, Kd, generator=gen, device=DEV) * 0.03).to(dtype)
+    fused = K.gemm_rows32_silu(x, w13)
+    gu = K.gemm_rows32(x, w13) if K.gemm_rows32_splits(M, 2 * inter, Kd) == 1 else None
+    ref = K.silu_mul((x.float() @ w13.float().T).to(dtype))
+    torch.cuda.synchronize()
+    if gu is not None:
+        assert torch.equal(fused, K.silu_mul(gu))
+    err = (fused.float() - ref.float()).abs()
+    assert err.max().item() <= 0.02 * ref.float().abs().max().item() + 1e-3

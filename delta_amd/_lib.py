@@ -82,6 +82,7 @@ SIGNATURES = {
     "delta_gemm_rows32_splits": (c_int, [c_int, c_int, c_int]),
     "delta_gemm_rows32": (c_int, [_P, c_int64, _P, c_int64, _P, _P, c_int64, _P, c_int, c_int, c_int, c_int, _P]),
     "delta_gemm_rows32_silu": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, _P]),
+    "delta_gemm_skinny_silu": (c_int, [_P, c_int64, _P, c_int64, _P, c_int64, c_int, c_int, c_int, c_int, _P]),
     "delta_rope": (c_int, [
         _P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int, c_int,
         c_int, c_int, c_float, c_float, c_int, c_float, c_float, c_float, _P]),

@@ -43,12 +43,16 @@ struct GemmArgs {
   uint16_t *out;
   int64_t ldo;
   int M, N, K, kper;
+  int inter;  // GLU: W = [gate rows; up rows], out [M][inter]
 };
 
 // TG groups of 8 token rows per block (TG = 1 for M <= 8, else 4); each wave keeps D k steps of
 // W and x in flight (a ring of D fragment sets), so the launch has enough bytes in flight to
 // stream W at HBM rate even when the N / 16 blocks barely cover the CUs.
-template <int DT, int NB, int TG, int D>
+// GLU (FeedForward's gate/up GEMM and SiLU-mul, model.py:509-514): column groups nb < NB / 2 are
+// gate columns n0 + 8 nb, the others the matching up columns inter + n0 + 8 (nb - NB / 2); the
+// block writes dtype(dtype(silu(g)) * u) of its 4 NB columns, g and u rounded to the dtype first.
+template <int DT, int NB, int TG, int D, bool GLU = false>
 __global__ void __launch_bounds__(kGemmWaves * 64) gemm_skinny_kernel(GemmArgs a) {
   using E = Elem<DT>;
   extern __shared__ float red[];  // [wave][8 TG token rows][8 NB columns]
@@ -56,7 +60,11 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm_skinny_kernel(GemmArgs a
   constexpr int kRows = 8 * TG;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane >> 4, t = lane & 15;
-  const int n0 = blockIdx.x * kCols;
+  const int n0 = blockIdx.x * (GLU ? kCols / 2 : kCols);
+  // row offset of column group nb in W
+  auto grp = [&](int nb) -> int64_t {
+    return GLU && nb >= NB / 2 ? (int64_t)a.inter + 8 * (nb - NB / 2) : (int64_t)8 * nb;
+  };
   const int m0 = blockIdx.y * kRows;
   const int kb = wave * a.kper;
   const int ke = min(a.K, kb + a.kper);
@@ -81,7 +89,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm_skinny_kernel(GemmArgs a
   u32x4 wf[D][NB], xf[D][TG];
   auto load = [&](int d, int s) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) wf[d][nb] = ld128_stream(wp + (int64_t)nb * 8 * a.ldw + 64 * s);
+    for (int nb = 0; nb < NB; ++nb) wf[d][nb] = ld128_stream(wp + grp(nb) * a.ldw + 64 * s);
 #pragma unroll
     for (int tg = 0; tg < TG; ++tg) xf[d][tg] = xok[tg] ? ld128(xp[tg] + 64 * s) : u32x4{0u, 0u, 0u, 0u};
   };
@@ -131,6 +139,24 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm_skinny_kernel(GemmArgs a
       }
     }
   __syncthreads();
+  if (GLU) {
+    constexpr int kOut = kCols / 2;
+    for (int idx = threadIdx.x; idx < kRows * kOut; idx += kGemmWaves * 64) {
+      const int row = idx / kOut, col = idx % kOut;
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGemmWaves; ++w) {
+        g += red[(w * kRows + row) * kCols + col];
+        u += red[(w * kRows + row) * kCols + kOut + col];
+      }
+      if (m0 + row < a.M) {
+        const float gr = E::lo(E::from_float(g)), ur = E::lo(E::from_float(u));
+        const float h = E::lo(E::from_float(gr / (1.f + expf(-gr))));
+        a.out[(int64_t)(m0 + row) * a.ldo + n0 + col] = (uint16_t)E::from_float(h * ur);
+      }
+    }
+    return;
+  }
   for (int idx = threadIdx.x; idx < kRows * kCols; idx += kGemmWaves * 64) {
     const int row = idx / kCols, col = idx % kCols;
     float sum = 0.f;
@@ -397,6 +423,7 @@ extern "C" DELTA_EXPORT int delta_gemm_skinny(const void *x, int64_t ldx, const 
   a.N = N;
   a.K = K;
   a.kper = (int)(ceil_div(K / 64, kGemmWaves) * 64);
+  a.inter = 0;
   // 32 columns per block when that still gives every CU a block, else 16.
   const int nb = (N % 32 == 0 && N / 32 >= 256) ? 4 : 2;
   return dtype == DELTA_BF16 ? launch_gemm<DELTA_BF16>(a, nb, (hipStream_t)stream)
@@ -493,5 +520,43 @@ extern "C" DELTA_EXPORT int delta_gemm_rows32_silu(const void *x, int64_t ldx, c
     hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_BF16, 1, true>), grid, block, 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL((gemm_rows32_kernel<DELTA_FP16, 1, true>), grid, block, 0, (hipStream_t)stream, a);
+  return check_launch(who);
+}
+
+extern "C" DELTA_EXPORT int delta_gemm_skinny_silu(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out,
+                                                   int64_t ldo, int M, int inter, int K, int dtype,
+                                                   delta_stream_t stream) {
+  using namespace delta;
+  clear_error();
+  const char *who = "delta_gemm_skinny_silu";
+  if (M <= 0 || inter <= 0) return DELTA_OK;
+  if (!x || !w13 || !out) return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
+  if (M > 8) return set_error(DELTA_ERR_INVALID, "%s: M (%d) must be <= 8", who, M);
+  if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
+  if (K <= 0 || K % 64) return set_error(DELTA_ERR_INVALID, "%s: K (%d) must be a positive multiple of 64", who, K);
+  if (inter % 16) return set_error(DELTA_ERR_INVALID, "%s: inter (%d) must be a multiple of 16", who, inter);
+  if (ldx < K || ldw < K || ldo < inter) return set_error(DELTA_ERR_INVALID, "%s: leading dimensions too small", who);
+  if ((ldx % 8) || (ldw % 8) || (((uintptr_t)x | (uintptr_t)w13) & 15u))
+    return set_error(DELTA_ERR_INVALID, "%s: x and W rows must be 16-byte aligned", who);
+  GemmArgs a;
+  a.x = (const uint16_t *)x;
+  a.ldx = ldx;
+  a.w = (const uint16_t *)w13;
+  a.ldw = ldw;
+  a.bias = nullptr;
+  a.out = (uint16_t *)out;
+  a.ldo = ldo;
+  a.M = M;
+  a.N = 2 * inter;
+  a.K = K;
+  a.kper = (int)(ceil_div(K / 64, kGemmWaves) * 64);
+  a.inter = inter;
+  // 16 gate + 16 up columns per block, one k step in flight (the launch has inter / 16 blocks)
+  const dim3 grid(inter / 16, 1), block(kGemmWaves * 64);
+  const size_t lds = kGemmWaves * 8 * 32 * sizeof(float);
+  if (dtype == DELTA_BF16)
+    hipLaunchKernelGGL((gemm_skinny_kernel<DELTA_BF16, 4, 1, 1, true>), grid, block, lds, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((gemm_skinny_kernel<DELTA_FP16, 4, 1, 1, true>), grid, block, lds, (hipStream_t)stream, a);
   return check_launch(who);
 }

@@ -644,7 +644,8 @@ def gemm_rows32(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tens
     return out if S == 1 else partials
 
 
-def gemm_rows32_silu(x: torch.Tensor, w13: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+def gemm_rows32_silu(x: torch.Tensor, w13: torch.Tensor, out: Optional[torch.Tensor] = None,
+                     _entry: str = "delta_gemm_rows32_silu") -> torch.Tensor:
     """``silu(x @ w1.T) * (x @ w3.T)`` for <= 32 token rows in one launch (``delta_gemm_rows32_silu``);
     ``w13`` is the row-major merged ``[2 * inter, dim]`` weight (w1 rows, then w3 rows)."""
     dev = _check_cuda(x, w13, out)
@@ -661,9 +662,14 @@ def gemm_rows32_silu(x: torch.Tensor, w13: torch.Tensor, out: Optional[torch.Ten
     o2 = out.reshape(-1, inter)
     if o2.stride(1) != 1 or o2.shape[0] != M:
         raise ValueError("out must be [..., inter] with contiguous rows")
-    _lib.call("delta_gemm_rows32_silu", x2.data_ptr(), x2.stride(0), w13.data_ptr(), w13.stride(0), o2.data_ptr(),
+    _lib.call(_entry, x2.data_ptr(), x2.stride(0), w13.data_ptr(), w13.stride(0), o2.data_ptr(),
               o2.stride(0), int(M), int(inter), int(Kd), _dtype_code(x), _stream(dev))
     return out
+
+
+def gemm_skinny_silu(x: torch.Tensor, w13: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The same fused gate/up GEMM + SiLU-mul for <= 8 token rows (``delta_gemm_skinny_silu``)."""
+    return gemm_rows32_silu(x, w13, out, _entry="delta_gemm_skinny_silu")
 
 
 def gemm_skinny(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,

@@ -351,10 +351,12 @@ class FeedForward(nn.Module):
     def forward_fused(self, x: Tensor):
         """The block's FFN output for the next fused add + norm (maybe as fp32 partials)."""
         rows = x.numel() // x.shape[-1]
-        if (hasattr(self, "w13") and _SKINNY_ROWS_ANY < rows <= _ROWS32_MAX and self.inter % 32 == 0
-                and K.gemm_skinny_ok(x, self.w13)):
+        if hasattr(self, "w13") and self.inter % 32 == 0 and K.gemm_skinny_ok(x, self.w13):
             # gate/up GEMM and SiLU-mul in one launch (same bits as the two)
-            return dense_to_norm(K.gemm_rows32_silu(x, self.w13), self.w2)
+            if rows <= _SKINNY_ROWS_ANY:
+                return dense_to_norm(K.gemm_skinny_silu(x, self.w13), self.w2)
+            if rows <= _ROWS32_MAX:
+                return dense_to_norm(K.gemm_rows32_silu(x, self.w13), self.w2)
         return dense_to_norm(K.silu_mul(self._gate_up(x)), self.w2)
 
 

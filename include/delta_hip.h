@@ -409,6 +409,12 @@ int delta_gemm_rows32(const void *x, int64_t ldx, const void *w, int64_t ldw, co
 int delta_gemm_rows32_silu(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out, int64_t ldo,
                            int M, int inter, int K, int dtype, delta_stream_t stream);
 
+/* The same fused gate/up GEMM + SiLU-mul for M <= 8 rows on delta_gemm_skinny's kernel: bit
+ * for bit delta_gemm_skinny over w13 followed by delta_silu_mul.  inter % 16 == 0; out rows
+ * any alignment (row stride ldo >= inter). */
+int delta_gemm_skinny_silu(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out, int64_t ldo,
+                           int M, int inter, int K, int dtype, delta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

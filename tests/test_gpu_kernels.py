@@ -672,3 +672,17 @@ def test_gemm_rows32_silu_equals_gemm_then_silu_mul(dtype, M, inter, Kd):
         assert torch.equal(fused, K.silu_mul(gu))
     err = (fused.float() - ref.float()).abs()
     assert err.max().item() <= 0.02 * ref.float().abs().max().item() + 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,inter,Kd", [(4, 18944, 3584), (1, 64, 128), (8, 14336, 4096), (3, 1040, 640)])
+def test_gemm_skinny_silu_equals_gemm_then_silu_mul(dtype, M, inter, Kd):
+    """The fused gate/up GEMM + SiLU-mul at <= 8 rows writes the bits of delta_gemm_skinny over the
+    merged weight followed by delta_silu_mul."""
+    gen = torch.Generator(device=DEV).manual_seed(M * 5 + inter + Kd)
+    x = torch.randn(M, Kd, generator=gen, device=DEV).to(dtype)
+    w13 = (torch.randn(2 * inter, Kd, generator=gen, device=DEV) * 0.03).to(dtype)
+    fused = K.gemm_skinny_silu(x, w13)
+    two = K.silu_mul(K.gemm_skinny(x, w13))
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two)

@@ -212,9 +212,9 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
         ntok_full * hq * 4 + B * mp * 4, "reads the logits dump once, writes page scores")
     add("page_score_kv (standalone scorer)",
         timed(lambda c, d, l, s, i, p: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
-                                                     c.kv_last_page_len, mp, logits_dump=d, scores=s)),
+                                                     c.kv_last_page_len, mp, scores=s)),
         ntok_full * row_kv + B * hq * 128 * esz + B * mp * 4 + B * mp * 4,
-        "K read once + q + page table + scores (logit spill not counted)")
+        "K read once + q + page table + scores (logits on chip where they fit, else a spilled dump)")
     add("select_pages_kernel",
         timed(lambda c, d, l, s, i, p: K.select_pages(s, c.kv_indptr, c.block_table, c.k, c.L, out_indices=i,
                                                        out_indptr=p)),
@@ -310,7 +310,7 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
         ntok_sub * 2 * row_kv + qo + sum(nsel) * 4)
     add("page_score_kv (standalone scorer)",
         timed(lambda c, d, l, s, i, p: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
-                                                     c.kv_last_page_len, mp, logits_dump=d, scores=s)),
+                                                     c.kv_last_page_len, mp, scores=s)),
         ntok_full * row_kv + B * hq * 128 * esz + sum(npages) * 4 + B * mp * 4)
     del layers, c
     torch.cuda.empty_cache()

@@ -57,6 +57,7 @@ SIGNATURES = {
     "delta_page_scores_from_logits": (c_int, [
         _P, c_int64, c_int64, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, _P, c_size_t, _P]),
     "delta_page_score_kv_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "delta_page_score_needs_dump": (c_int, [c_int, c_int, c_int, c_int]),
     "delta_page_score": (c_int, [
         _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P,
         _P, c_int64, c_int64, _P, c_int64,

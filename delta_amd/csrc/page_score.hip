@@ -27,11 +27,13 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
                void *workspace, size_t workspace_bytes, hipStream_t stream, const char *who,
                const delta_decode_append_t *ap);
 int decode_num_splits(int batch, int hkv, int max_pages);
+bool tokmax_fits(int batch, int hkv, int G, int max_pages);
 size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc);
 
 namespace {
 
 constexpr int kScoreThreads = 256;
+constexpr int kMaxWaves = 16;  // kv heads a launch takes (the decode kernel's block limit)
 constexpr int kMaxHeads = 256;
 
 __device__ __forceinline__ int row_kv_len(const int32_t *kv_indptr, const int32_t *last, int b) {
@@ -105,6 +107,29 @@ __global__ void __launch_bounds__(kScoreThreads)
   if ((threadIdx.x & 15) == 0 && page < max_pages) scores[(int64_t)b * score_stride + page] = page_sum;
 }
 
+// Page scores from the LDS scorer's per-(kv head, token) maxima tm [batch][hkv][sh]: one token per
+// thread, the max over the hkv values (the max over all q heads of the token's probability),
+// then the same 16-lane page sum as legacy_softmax_score_kernel.
+__global__ void __launch_bounds__(kScoreThreads)
+    tokmax_score_kernel(const float *tm, int64_t sb, int64_t sh, int hkv, const int32_t *kv_indptr,
+                        const int32_t *last, float *scores, int64_t score_stride, int max_pages) {
+  const int b = blockIdx.y;
+  const int n = min(row_kv_len(kv_indptr, last, b), max_pages * kPageSize);
+  const int tok = blockIdx.x * kScoreThreads + threadIdx.x;
+  const float *col = tm + (int64_t)b * sb + tok;
+  float best = 0.f;
+  if (tok < n) {
+    float v[kMaxWaves];
+#pragma unroll
+    for (int kh = 0; kh < kMaxWaves; ++kh) v[kh] = kh < hkv ? __builtin_nontemporal_load(col + kh * sh) : 0.f;
+#pragma unroll
+    for (int kh = 0; kh < kMaxWaves; ++kh) best = fmaxf(best, v[kh]);
+  }
+  const float page_sum = row16_sum(best);
+  const int page = tok >> 4;
+  if ((threadIdx.x & 15) == 0 && page < max_pages) scores[(int64_t)b * score_stride + page] = page_sum;
+}
+
 int launch_scores(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
                   const int32_t *kv_indptr, const int32_t *last, float *scores, int64_t score_stride,
                   int batch, int hq, int max_pages, hipStream_t stream, const char *who) {
@@ -158,10 +183,23 @@ extern "C" DELTA_EXPORT int delta_page_scores_from_logits(const float *logits_du
 
 extern "C" DELTA_EXPORT size_t delta_page_score_kv_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                                                    int max_pages_per_row) {
-  // [partials of the K-only decode][lse]
+  // [partials of the K-only decode][lse], or, for the LDS scorer, its per-(kv head, token)
+  // maxima [batch][hkv][max_pages * 16] (the larger of the two).
   const int ns = delta::decode_num_splits(batch, num_kv_heads, max_pages_per_row);
   const size_t lse_bytes = ((size_t)batch * num_qo_heads * sizeof(float) + 255) & ~(size_t)255;
-  return delta::decode_workspace_bytes(batch, num_qo_heads, ns, false) + lse_bytes;
+  const size_t dump_path = delta::decode_workspace_bytes(batch, num_qo_heads, ns, false) + lse_bytes;
+  if (num_kv_heads <= 0 || num_qo_heads % num_kv_heads ||
+      !delta::tokmax_fits(batch, num_kv_heads, num_qo_heads / num_kv_heads, max_pages_per_row))
+    return dump_path;
+  const size_t tm = ((size_t)batch * num_kv_heads * max_pages_per_row * delta::kPageSize * sizeof(float) + 255) &
+                    ~(size_t)255;
+  return tm > dump_path ? tm : dump_path;
+}
+
+extern "C" DELTA_EXPORT int delta_page_score_needs_dump(int batch, int num_qo_heads, int num_kv_heads,
+                                                        int max_pages_per_row) {
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads) return 1;
+  return delta::tokmax_fits(batch, num_kv_heads, num_qo_heads / num_kv_heads, max_pages_per_row) ? 0 : 1;
 }
 
 extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -176,16 +214,34 @@ extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, 
   clear_error();
   const char *who = "delta_page_score";
   if (batch <= 0 || max_pages <= 0) return DELTA_OK;
-  if (!scores || !logits_dump) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
+  if (!scores) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
   if (num_qo_heads > kMaxHeads) return set_error(DELTA_ERR_INVALID, "%s: too many heads", who);
+  if (num_kv_heads <= 0 || num_qo_heads % num_kv_heads)
+    return set_error(DELTA_ERR_INVALID, "%s: num_qo_heads must be a multiple of num_kv_heads", who);
   if (score_stride < max_pages) return set_error(DELTA_ERR_INVALID, "%s: score_stride < max_pages", who);
-  if (dump_stride_h < (int64_t)max_pages * kPageSize)
+  if (logits_dump && dump_stride_h < (int64_t)max_pages * kPageSize)
     return set_error(DELTA_ERR_INVALID, "%s: dump rows shorter than max_pages*16", who);
+  const bool lds_path = !logits_dump && tokmax_fits(batch, num_kv_heads, num_qo_heads / num_kv_heads, max_pages);
+  if (!logits_dump && !lds_path)
+    return set_error(DELTA_ERR_INVALID, "%s: this shape needs a logits dump buffer", who);
   const size_t need = delta_page_score_kv_workspace_bytes(batch, num_qo_heads, num_kv_heads, max_pages);
   if (!workspace || workspace_bytes < need)
     return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
   if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
   hipStream_t st = (hipStream_t)stream;
+  if (lds_path) {
+    // One launch streams K once and leaves per-(kv head, token) maxima; a second sums pages.
+    float *tm = (float *)workspace;
+    const int64_t sh = (int64_t)max_pages * kPageSize, sb = (int64_t)num_kv_heads * sh;
+    int rc = run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                        kv_last_page_len, nullptr, 0, 0, nullptr, tm, sb, sh, batch, num_qo_heads, num_kv_heads,
+                        head_dim, dtype, sm_scale, max_pages, /*kScoreTokmax*/ 4, nullptr, 0, st, who, nullptr);
+    if (rc) return rc;
+    dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
+    hipLaunchKernelGGL(tokmax_score_kernel, grid, dim3(kScoreThreads), 0, st, tm, sb, sh, num_kv_heads, kv_indptr,
+                       kv_last_page_len, scores, score_stride, max_pages);
+    return check_launch(who);
+  }
   const int ns = decode_num_splits(batch, num_kv_heads, max_pages);
   const size_t dec = decode_workspace_bytes(batch, num_qo_heads, ns, false);
   float *lse_ws = (float *)((char *)workspace + dec);

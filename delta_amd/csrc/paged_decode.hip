@@ -69,6 +69,10 @@ struct DecodeArgs {
   const int32_t *ap_indices;
   int64_t ap_indices_len;
   float rcp_scale, log2_theta, smooth_a, smooth_b;
+  // K-only scorer with the row's logits kept in LDS (TOKMAX): per (row, kv head, token) the
+  // largest softmax probability over the head's G q heads, [batch][hkv][tokmax_stride_h].
+  float *tokmax;
+  int64_t tokmax_stride_b, tokmax_stride_h;
 };
 
 struct RowInfo {
@@ -166,6 +170,12 @@ constexpr int dump_slots() {
   return WITH_V ? (G <= 4 ? 16 : 8) : (G <= 4 ? 32 : 16);
 }
 
+// TOKMAX LDS: the waves' (m, l) [16][G][2], 16 floats of per-head lse2, then the logits.
+template <int G>
+constexpr int tokmax_lds_header() {
+  return kMaxWaves * G * 2 + 16;
+}
+
 // max / sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950 permlane swaps.
 __device__ __forceinline__ float rows4_max(float v) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -195,11 +205,16 @@ __device__ __forceinline__ float rows4_sum(float v) {
 //         B = V from a padded LDS tile whose row 4c + r holds token tok(r), read with
 //         ds_read_b64_tr_b16 (lane (c, j) gets tile rows 4c..4c+3 at d = 16n + j),
 //         D = O[g = 4c + r][d = 16n + lane%16].
-template <int DT, int G, bool WITH_V, bool WITH_DUMP, bool ROPE>
+// TOKMAX (K-only, head-major, unsplit, the row's logits fit in LDS): every page's logits stay
+// in LDS ([page][g][16], past a small merge header); once the block's waves have merged, the
+// block knows each head's final lse and writes, per token, max_g 2^(x_g log2 e - lse2_g) --
+// del3_legacy_softmax's per-token max over this kv head's q heads -- instead of a logits dump.
+template <int DT, int G, bool WITH_V, bool WITH_DUMP, bool ROPE, bool TOKMAX = false>
 __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
   // No FMA contraction: every instantiation (with or without the dump) rounds the softmax
   // arguments identically, so P -- rounded to the KV dtype for the P.V MFMA -- is the same.
 #pragma clang fp contract(off)
+  static_assert(!TOKMAX || (!WITH_V && !WITH_DUMP && !ROPE), "TOKMAX is the K-only scorer");
   using E = Elem<DT>;
   using M16 = Mfma16<DT>;
 
@@ -458,6 +473,11 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       for (int r = 0; r < 4; ++r)
         x[r] = (ok && tok0 + 8 * (r >> 1) + (r & 1) < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
       const int slot = (c0 + it) % kDumpSlots;
+      if (TOKMAX && t < G && j < a.dump_pages) {
+        float *dl = smem + tokmax_lds_header<G>() + (j * G + t) * kPageSize + 2 * c;
+        *reinterpret_cast<float2 *>(dl) = float2{x[0], x[1]};
+        *reinterpret_cast<float2 *>(dl + 8) = float2{x[2], x[3]};
+      }
       if (WITH_DUMP) {
         // Logits staged in LDS, one slot per page of a kDumpSlots-page window.
         if (t < G) {
@@ -582,6 +602,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       }
       if (dd == 0 && a.lse != nullptr)
         a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+      if (TOKMAX) smem[tokmax_lds_header<G>() - 16 + g] = L > 0.f ? M + log2f(L) : -INFINITY;
     } else {
       const int64_t pidx = ((int64_t)unit * a.hkv + hh) * G + g;
       if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
@@ -589,6 +610,21 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         a.part_ml[pidx * 2 + 0] = M;
         a.part_ml[pidx * 2 + 1] = L;
       }
+    }
+  }
+  if (TOKMAX) {
+    __syncthreads();
+    const float *lse2 = smem + tokmax_lds_header<G>() - 16;
+    const float *lg = smem + tokmax_lds_header<G>();
+    float *outp = a.tokmax + (int64_t)b * a.tokmax_stride_b + (int64_t)head0 * a.tokmax_stride_h;
+    const int np_out = ri.np < a.dump_pages ? ri.np : a.dump_pages;
+    for (int tk = threadIdx.x; tk < np_out * kPageSize; tk += blockDim.x) {
+      const int j = tk >> 4, tok = tk & 15;
+      float mx = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (lse2[g] != -INFINITY) mx = fmaxf(mx, fast_exp2(lg[(j * G + g) * kPageSize + tok] * kLog2e - lse2[g]));
+      __builtin_nontemporal_store(mx, outp + tk);
     }
   }
 }
@@ -617,6 +653,11 @@ template <int DT, int G>
 __global__ void __launch_bounds__(kMaxWaves * 64) page_score_kv_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
   decode_split_body<DT, G, false, true, false>(a, smem);
+}
+template <int DT, int G>
+__global__ void __launch_bounds__(kMaxWaves * 64) page_score_tokmax_kernel(DecodeArgs a) {
+  extern __shared__ float smem[];
+  decode_split_body<DT, G, false, false, false, true>(a, smem);
 }
 
 // Combines the unit partials of one (row, q head): thread d of the block computes
@@ -695,7 +736,7 @@ __global__ void __launch_bounds__(256) decode_merge_lse_kernel(DecodeArgs a, int
   if (lane == 0) a.lse[idx] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
 
-enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3 };
+enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3, kScoreTokmax = 4 };
 
 template <int DT, int G>
 void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
@@ -731,11 +772,16 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
       else
         hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, false>), grid, block, sm_plan, stream, a);
       break;
+    case kScoreTokmax:
+      hipLaunchKernelGGL((page_score_tokmax_kernel<DT, G>), grid, block,
+                         (size_t)(tokmax_lds_header<G>() + a.dump_pages * G * kPageSize) * sizeof(float), stream, a);
+      break;
     default:
       hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, sm_score, stream, a);
       break;
   }
 }
+
 
 template <int DT>
 void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t stream) {
@@ -804,6 +850,14 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
   *chunk = (int)(ch < 1 ? 1 : ch);
 }
 
+// The K-only scorer keeps the row's logits in LDS (no dump, no merge launch) when a head-major
+// unsplit launch fills the GPU (>= 256 (row, kv head) blocks) and max_pages * G * 16 logits fit
+// beside the merge header in 160 KiB.
+bool tokmax_fits(int batch, int hkv, int G, int max_pages) {
+  const int64_t lds = ((int64_t)kMaxWaves * G * 2 + 16 + (int64_t)max_pages * G * kPageSize) * (int64_t)sizeof(float);
+  return (int64_t)batch * hkv >= kHeadMajorPairs && lds <= 160 * 1024;
+}
+
 int decode_num_splits(int batch, int hkv, int max_pages) {
   int ns, w, hb, ch, ns_dump;
   decode_plan(batch, hkv, max_pages, false, &ns, &w, &hb, &ch);
@@ -840,9 +894,12 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
   if (!q || !kv_cache || !kv_indptr || !kv_indices || !kv_last_page_len)
     return set_error(DELTA_ERR_INVALID, "%s: null input pointer", who);
-  if (mode != kScoreOnly && !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
-  if ((mode == kAttnDump || mode == kScoreOnly) && !dump)
+  const bool tokmax = mode == kScoreTokmax;  // `dump` is then the [batch][hkv][stride_h] output
+  if (mode != kScoreOnly && !tokmax && !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
+  if ((mode == kAttnDump || mode == kScoreOnly || tokmax) && !dump)
     return set_error(DELTA_ERR_INVALID, "%s: null logits dump", who);
+  if (tokmax && !tokmax_fits(batch, hkv, G, max_pages))
+    return set_error(DELTA_ERR_INVALID, "%s: this shape does not fit the LDS scorer", who);
   if (((uintptr_t)q | (uintptr_t)kv_cache) & 15u)
     return set_error(DELTA_ERR_INVALID, "%s: q and kv_cache must be 16-byte aligned", who);
   if ((q_stride_h % 8) || (q_stride_b % 8))
@@ -869,15 +926,24 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.o_stride_b = o_stride_b;
   a.o_stride_h = o_stride_h;
   a.lse = lse;
-  a.dump = dump;
+  a.dump = tokmax ? nullptr : dump;
   a.dump_stride_b = dump_stride_b;
   a.dump_stride_h = dump_stride_h;
   a.dump_pages = max_pages;
+  a.tokmax = tokmax ? dump : nullptr;
+  a.tokmax_stride_b = dump_stride_b;
+  a.tokmax_stride_h = dump_stride_h;
   a.batch = batch;
   a.hq = hq;
   a.hkv = hkv;
   int waves;
   decode_plan(batch, hkv, max_pages, dump != nullptr, &a.nsplit, &waves, &a.hb, &a.chunk);
+  if (tokmax) {  // head-major, unsplit: each block ends with its head's final lse
+    a.nsplit = 1;
+    a.hb = 1;
+    waves = kMaxWaves;
+    a.chunk = max_pages;
+  }
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;
@@ -919,7 +985,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
 
   if (a.hb < 1 || a.hkv % a.hb != 0)
     return set_error(DELTA_ERR_INVALID, "%s: launch planned with %d of %d kv heads per block", who, a.hb, a.hkv);
-  const bool with_acc = mode != kScoreOnly;
+  const bool with_acc = mode != kScoreOnly && !tokmax;
   const size_t need = decode_workspace_bytes(batch, hq, a.nsplit, with_acc);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)

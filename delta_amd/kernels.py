@@ -276,7 +276,10 @@ def page_score(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
                sm_scale: Optional[float] = None, logits_dump: Optional[torch.Tensor] = None,
                scores: Optional[torch.Tensor] = None,
                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Standalone scorer (K read once): returns fp32 page scores [B, max_pages]."""
+    """Standalone scorer (K read once): returns fp32 page scores [B, max_pages].
+
+    Without ``logits_dump`` the scorer keeps each row's logits on chip when the shape allows
+    (``delta_page_score_needs_dump`` == 0: no dump written); otherwise a dump buffer is used."""
     dev = _check_cuda(q, kv_cache, kv_indptr, kv_indices, kv_last_page_len, logits_dump, scores)
     _check_cache(kv_cache)
     hq, hkv = _check_heads(q, kv_cache)
@@ -284,11 +287,12 @@ def page_score(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
     _check_i32("kv_indptr", kv_indptr, B + 1)
     _check_i32("kv_indices", kv_indices)
     _check_i32("kv_last_page_len", kv_last_page_len, B)
-    if logits_dump is None:
+    if logits_dump is None and int(_lib.query("delta_page_score_needs_dump", B, hq, hkv, max_pages)):
         logits_dump = torch.empty((B, hq, max_pages * PAGE_SIZE), dtype=torch.float32, device=dev)
-    if logits_dump.dtype != torch.float32 or logits_dump.dim() != 3 or logits_dump.stride(2) != 1 \
-            or logits_dump.shape[0] < B or logits_dump.shape[1] != hq \
-            or logits_dump.shape[2] < max_pages * PAGE_SIZE:
+    if logits_dump is not None and (
+            logits_dump.dtype != torch.float32 or logits_dump.dim() != 3 or logits_dump.stride(2) != 1
+            or logits_dump.shape[0] < B or logits_dump.shape[1] != hq
+            or logits_dump.shape[2] < max_pages * PAGE_SIZE):
         raise ValueError("logits_dump must be fp32 [>=B, Hq, >=max_pages*16] with unit last stride")
     if scores is None:
         scores = torch.empty((B, max_pages), dtype=torch.float32, device=dev)
@@ -303,8 +307,8 @@ def page_score(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
     _lib.call("delta_page_score",
               q.data_ptr(), q.stride(0), q.stride(1), kv_cache.data_ptr(), kv_cache.shape[0],
               kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_indices.numel(),
-              kv_last_page_len.data_ptr(), logits_dump.data_ptr(), logits_dump.stride(0),
-              logits_dump.stride(1), scores.data_ptr(), scores.stride(0),
+              kv_last_page_len.data_ptr(), _ptr(logits_dump), 0 if logits_dump is None else logits_dump.stride(0),
+              0 if logits_dump is None else logits_dump.stride(1), scores.data_ptr(), scores.stride(0),
               B, hq, hkv, HEAD_DIM, _dtype_code(q), float(sm_scale), int(max_pages),
               workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
     return scores

@@ -216,13 +216,17 @@ int delta_page_scores_from_logits(const float *logits_dump, int64_t dump_stride_
                                   int num_qo_heads, int max_pages, void *workspace,
                                   size_t workspace_bytes, delta_stream_t stream);
 
-/* Standalone scorer: reads the paged K cache once (no V), writes the fp32
- * logits into logits_dump (caller-provided, layout as above, >= max_pages*16
- * per (b,h) row) and the page scores.  Replaces the dump attention kernel +
- * legacy-softmax torch ops for a caller that only needs scores
- * (backend.py:561-577 + 887-904). */
+/* Standalone scorer: reads the paged K cache once (no V) and writes the page
+ * scores.  Replaces the dump attention kernel + legacy-softmax torch ops for a
+ * caller that only needs scores (backend.py:561-577 + 887-904).  With a
+ * logits_dump (caller-provided, layout as above, >= max_pages*16 per (b,h)
+ * row) the fp32 logits are written there too.  With logits_dump == NULL the
+ * scorer keeps each row's logits on chip -- allowed when
+ * delta_page_score_needs_dump(...) == 0 (batch * num_kv_heads >= 256 and the
+ * row's logits fit in LDS), else an error -- and writes no logits. */
 size_t delta_page_score_kv_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                            int max_pages_per_row);
+int delta_page_score_needs_dump(int batch, int num_qo_heads, int num_kv_heads, int max_pages_per_row);
 int delta_page_score(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                      const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr,
                      const int32_t *kv_indices, int64_t kv_indices_len,

@@ -72,8 +72,13 @@ def test_queries_without_gpu(lib):
     # config 5 (ragged up to 2049 pages): units of at most 128 pages, 17 for the longest row
     assert lib.delta_decode_num_splits(128, 8, 2049) == 17
     assert lib.delta_page_score_workspace_bytes(32, 32) == 32 * 32 * 4
-    # (m, l) per (unit, q head) + each row's first unit + the lse buffer, each 256-byte aligned
-    assert lib.delta_page_score_kv_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 2 * 4 + 256 + 32 * 32 * 4
+    # the larger of: (m, l) per (unit, q head) + each row's first unit + the lse buffer (dump path),
+    # and the LDS scorer's per-(kv head, token) maxima [B][Hkv][max_pages*16] (config 3 fits)
+    assert lib.delta_page_score_needs_dump(32, 32, 8, 513) == 0
+    assert lib.delta_page_score_kv_workspace_bytes(32, 32, 8, 513) == 32 * 8 * 513 * 16 * 4
+    assert lib.delta_page_score_needs_dump(8, 32, 8, 1024) == 1      # config 2: 64 (row, head) pairs
+    assert lib.delta_page_score_needs_dump(32, 64, 8, 513) == 1      # G = 8: 263 KB of logits per row
+    assert lib.delta_page_score_kv_workspace_bytes(8, 32, 8, 1024) == 8 * 32 * 32 * 2 * 4 + 256 + 8 * 32 * 4
     assert lib.delta_page_score_kv_workspace_bytes(1024, 32, 8, 2048) == 1024 * 32 * 4
 
 

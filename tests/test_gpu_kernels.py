@@ -686,3 +686,27 @@ def test_gemm_skinny_silu_equals_gemm_then_silu_mul(dtype, M, inter, Kd):
     two = K.silu_mul(K.gemm_skinny(x, w13))
     torch.cuda.synchronize()
     assert torch.equal(fused, two)
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_page_score_on_chip_matches_oracle_and_dump_path(ragged):
+    """The K-only scorer without a dump (the row's logits kept in LDS, per-(kv head, token) maxima,
+    then page sums) against the oracle's del3_legacy_softmax scores (1e-4 relative) and the dump
+    path on the same inputs.  B * Hkv = 256 (row, head) blocks, rows of up to 300 pages."""
+    lens = [300 * 16] * 32 if not ragged else [16 * (1 + (37 * i) % 300) + (i % 16) for i in range(32)]
+    c = make_case(batch=32, hq=32, hkv=8, kv_lens=lens, seed=5, page_order="randperm", k=4, L=2,
+                  trailing_empty_page=ragged)
+    g = gpu(c)
+    mp = c.max_pages
+    assert K._lib.query("delta_page_score_needs_dump", 32, 32, 8, mp) == 0
+    s_chip = K.page_score(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, mp)
+    dump = torch.empty((32, 32, mp * 16), device=DEV)
+    s_dump = K.page_score(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, mp, logits_dump=dump)
+    torch.cuda.synchronize()
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, c.sm_scale, mp * 16)
+    ref = O.legacy_softmax_page_scores(x, 32, mp, compute_dtype=torch.float64).double()
+    for what, s in (("on chip", s_chip), ("dump", s_dump)):
+        s = s.cpu().double()
+        rel = (s - ref).abs() / ref.abs().clamp_min(1e-30)
+        rel[ref == 0] = s[ref == 0].abs()
+        assert rel.max().item() < 1e-4, f"{what}: rel err {rel.max().item()}"

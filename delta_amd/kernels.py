@@ -83,10 +83,13 @@ def _check_heads(q: torch.Tensor, kv_cache: torch.Tensor):
 
 
 class Workspace:
-    """Grow-only device scratch buffer (allocate before any graph capture)."""
+    """Grow-only device scratch buffer (allocate before any graph capture).  A buffer that a
+    larger request replaces is kept alive, not freed: a graph captured earlier still holds its
+    address and may be replayed."""
 
     def __init__(self):
         self._buf: dict = {}
+        self._retired: list = []
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
         nbytes = max(int(nbytes), 256)
@@ -95,6 +98,8 @@ class Workspace:
         if buf is None or buf.numel() < nbytes:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("workspace must be sized before graph capture")
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
             self._buf[key] = buf
         return buf

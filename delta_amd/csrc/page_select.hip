@@ -13,8 +13,10 @@
 // how many keys equal to T are taken (r); one ordered pass then marks
 // key > T, or key == T among the first r such pages, and compacts the marked
 // pages in ascending j with ballot prefix sums -- the output is sorted by
-// construction, no sort pass.  Keys are recomputed from the fp32 scores in
-// every pass (they stay in L2), so any row length works.
+// construction, no sort pass.  Rows of up to 4096 pages keep their keys in
+// registers for all passes; longer rows recompute them from the fp32 scores in
+// every pass (they stay in L2), so any row length works.  When every key equal
+// to T is taken (the usual case), the compaction needs no rank among them.
 #include <float.h>
 
 #include "delta_common.h"
@@ -22,9 +24,12 @@
 namespace delta {
 namespace {
 
-constexpr int kSelThreads = 1024;  // long rows (4 k+ pages) take few key loads per thread
-constexpr int kSelWaves = kSelThreads / 64;
+// Block sizes: 1024 threads for rows of more than 1024 pages (few key loads per thread), 256
+// for shorter rows (their barriers wait on 4 waves, not 16).
+constexpr int kSelThreadsLong = 1024;
+constexpr int kSelThreadsShort = 256;
 constexpr int kBins = 256;         // radix digit bins, handled by the first 4 waves
+constexpr int kKeysPerThread = 4;  // keys held in registers: rows of up to 4096 pages
 constexpr uint32_t kKeyPosInf = 0xFF800000u;  // order_key(+inf)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -86,7 +91,8 @@ __device__ __forceinline__ int row_count(const SelArgs &a, int b, bool subset) {
   return tp < kb ? tp : kb;
 }
 
-// Block-wide sum (all threads receive it).
+// Block-wide sum over NW waves (all threads receive it).
+template <int NW>
 __device__ int block_sum(int v, int *scratch) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
   const int wave = threadIdx.x >> 6;
@@ -94,12 +100,13 @@ __device__ int block_sum(int v, int *scratch) {
   __syncthreads();
   int s = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) s += scratch[w];
+  for (int w = 0; w < NW; ++w) s += scratch[w];
   __syncthreads();
   return s;
 }
 
-// Exclusive block prefix of a 0/1 flag in thread order; *total gets the block total.
+// Exclusive block prefix of a 0/1 flag in thread order over NW waves; *total gets the block total.
+template <int NW>
 __device__ int block_prefix(bool flag, int *scratch, int *total) {
   int wtot;
   const int wpre = wave_prefix_exclusive(flag, &wtot);
@@ -108,7 +115,7 @@ __device__ int block_prefix(bool flag, int *scratch, int *total) {
   __syncthreads();
   int before = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const int x = scratch[w];
     before += w < wave ? x : 0;
     tot += x;
@@ -118,10 +125,13 @@ __device__ int block_prefix(bool flag, int *scratch, int *total) {
   return before + wpre;
 }
 
+template <int kSelThreads>
 __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
+  constexpr int kSelWaves = kSelThreads / 64;
+  static_assert(kSelThreads >= kBins, "the bins are handled by the first kBins threads");
   __shared__ int s_scratch[kSelWaves];
   __shared__ uint32_t s_hist[kBins];
-  __shared__ int s_digit, s_remaining;
+  __shared__ int s_digit, s_remaining, s_eq;
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -134,7 +144,7 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
   } else {
     int part = 0;
     for (int i = tid; i < b; i += kSelThreads) part += row_count(a, i, subset);
-    before = block_sum(part, s_scratch);
+    before = block_sum<kSelWaves>(part, s_scratch);
   }
   const int cnt = row_count(a, b, subset);
   if (tid == 0) {
@@ -164,15 +174,35 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
     return order_key(prepare(a.scores[(int64_t)b * a.score_stride + j], j, a.bias_scale));
   };
 
+  // Rows of up to kKeysPerThread * 1024 pages keep their keys in registers across the five
+  // passes below; longer rows recompute them from the scores (L2) in every pass.
+  const bool cached = tp <= kKeysPerThread * kSelThreads;
+  uint32_t kc[kKeysPerThread];
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kKeysPerThread; ++i) {
+      const int j = tid + i * kSelThreads;
+      kc[i] = j < tp ? key_of(j) : 0u;
+    }
+  }
+
   // Radix select of the kb-th largest key.
   uint32_t prefix = 0, pmask = 0;
   int remaining = kb;
   for (int shift = 24; shift >= 0; shift -= 8) {
     if (tid < kBins) s_hist[tid] = 0;
     __syncthreads();
-    for (int j = tid; j < tp; j += kSelThreads) {
-      const uint32_t key = key_of(j);
-      if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+    if (cached) {
+#pragma unroll
+      for (int i = 0; i < kKeysPerThread; ++i) {
+        const uint32_t key = kc[i];
+        if (tid + i * kSelThreads < tp && (key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+      }
+    } else {
+      for (int j = tid; j < tp; j += kSelThreads) {
+        const uint32_t key = key_of(j);
+        if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+      }
     }
     __syncthreads();
     // Suffix sums over the 256 bins (thread d < 256 holds bin d): suf[d] = #keys with digit >= d.
@@ -189,6 +219,7 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
     if (tid < kBins && suf >= remaining && suf - hd < remaining) {
       s_digit = tid;
       s_remaining = remaining - (suf - hd);
+      s_eq = hd;  // after the last digit: the number of keys equal to T
     }
     __syncthreads();
     prefix |= (uint32_t)s_digit << shift;
@@ -198,21 +229,36 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
   }
   const uint32_t T = prefix;
   const int take_eq = remaining;  // how many keys == T are selected (smallest j first)
+  const bool all_eq = take_eq >= s_eq;  // every key equal to T is taken: no rank among them
 
-  // Ordered compaction.
+  // Ordered compaction (block-uniform trip counts: the prefixes hold barriers).
   int eq_seen = 0, written = 0;
-  for (int base = 0; base < tp; base += kSelThreads) {
-    const int j = base + tid;
-    const uint32_t key = j < tp ? key_of(j) : 0u;
-    const bool eq = j < tp && key == T;
-    int eq_tot;
-    const int eq_rank = eq_seen + block_prefix(eq, s_scratch, &eq_tot);
-    const bool sel = j < tp && (key > T || (eq && eq_rank < take_eq));
+  auto compact = [&](int j, uint32_t key) {
+    const bool in = j < tp;
+    bool sel;
+    if (all_eq) {
+      sel = in && key >= T;
+    } else {
+      const bool eq = in && key == T;
+      int eq_tot;
+      const int eq_rank = eq_seen + block_prefix<kSelWaves>(eq, s_scratch, &eq_tot);
+      sel = in && (key > T || (eq && eq_rank < take_eq));
+      eq_seen += eq_tot;
+    }
     int sel_tot;
-    const int pos = written + block_prefix(sel, s_scratch, &sel_tot);
+    const int pos = written + block_prefix<kSelWaves>(sel, s_scratch, &sel_tot);
     if (sel && pos < lim) out[pos] = bt[j];
-    eq_seen += eq_tot;
     written += sel_tot;
+  };
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kKeysPerThread; ++i)
+      if (i * kSelThreads < tp) compact(tid + i * kSelThreads, kc[i]);
+  } else {
+    for (int base = 0; base < tp; base += kSelThreads) {
+      const int j = base + tid;
+      compact(j, j < tp ? key_of(j) : 0u);
+    }
   }
 }
 
@@ -255,6 +301,11 @@ extern "C" DELTA_EXPORT int delta_select_pages(const float *scores, int64_t scor
   a.out_indices = out_indices;
   a.out_len = out_indices_len;
   a.out_indptr = out_indptr;
-  hipLaunchKernelGGL(select_pages_kernel, dim3(batch), dim3(kSelThreads), 0, (hipStream_t)stream, a);
+  if (max_pages <= kKeysPerThread * kSelThreadsShort)
+    hipLaunchKernelGGL(select_pages_kernel<kSelThreadsShort>, dim3(batch), dim3(kSelThreadsShort), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(select_pages_kernel<kSelThreadsLong>, dim3(batch), dim3(kSelThreadsLong), 0,
+                       (hipStream_t)stream, a);
   return check_launch(who);
 }

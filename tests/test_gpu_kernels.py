@@ -155,9 +155,12 @@ def test_selection_bit_exact_on_gpu_scores(name):
     assert idx[:int(want_p[-1])].cpu().tolist() == want_i.tolist()
 
 
-def test_selection_adversarial_scores():
+# Row lengths for each selection launch: 256-thread blocks (<= 1024 pages), 1024-thread blocks
+# with the keys in registers (<= 4096) and with the keys re-read every pass (longer).
+@pytest.mark.parametrize("n", [300, 2500, 5000])
+def test_selection_adversarial_scores(n):
     gen = torch.Generator().manual_seed(5)
-    B, n = 6, 300
+    B = 6
     s = torch.round(torch.rand(B, n, generator=gen) * 4) / 4  # heavy ties
     s[0, :50] = float("nan")
     s[1, 10:20] = float("inf")
@@ -165,7 +168,7 @@ def test_selection_adversarial_scores():
     s[3] = 0.0
     s[3, ::2] = -0.0
     s[4, 5] = 3.4e38
-    counts = torch.tensor([300, 299, 200, 300, 17, 64])
+    counts = torch.tensor([n, n - 1, 2 * n // 3, n, 17, 64])
     indptr = torch.zeros(B + 1, dtype=torch.int32)
     indptr[1:] = torch.cumsum(counts, 0)
     bt = torch.randperm(B * n, generator=gen).reshape(B, n).to(torch.int32)

@@ -8,7 +8,7 @@
 //   tie order unspecified; this build fixes it), positions emitted in
 //   ascending j (132-134) as physical ids from the row's block table (147-150).
 //
-// Algorithm per row (1024 threads): fp32 keys map to order-preserving uint32
+// Algorithm per row (one block of 256 or 1024 threads): fp32 keys map to order-preserving uint32
 // (+0/-0 folded); a 4-pass 8-bit radix select finds the k-th largest key T and
 // how many keys equal to T are taken (r); one ordered pass then marks
 // key > T, or key == T among the first r such pages, and compacts the marked

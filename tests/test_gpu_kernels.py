@@ -31,6 +31,10 @@ def cases():
         "head_major_ragged_g2": lambda: make_case(batch=36, hq=16, hkv=8,
                                                   kv_lens=[1 + (37 * i) % 900 for i in range(36)], seed=5,
                                                   page_order="shuffle", k=8, L=2),
+        # one long row: 8 (row, head) pairs split 32 ways (merge of 32 units), 1501 pages for
+        # the 1024-thread selector, a 384-page subset
+        "long_row_b1": lambda: make_case(batch=1, hq=32, hkv=8, kv_lens=[24007], seed=7,
+                                         page_order="shuffle", k=384, L=8),
     }
 
 

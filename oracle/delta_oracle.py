@@ -33,9 +33,13 @@ Pinning (the checks that make this restatement trustworthy) lives in
     fixed == general, monotonicity;
   - attention: torch SDPA on CPU, sparse == full when every page is selected,
     physical-permutation invariance;
-  - packer / append: brute force over Python lists.
-RoPE is "parity unpinned": no reference test or golden vector pins FlashInfer's
-RoPE, only its published formula, restated here.
+  - packer / append: brute force over Python lists;
+  - RoPE: closed forms (identity at position 0, pair norms kept, explicit
+    angles) and, for the Llama-3.1 frequencies, Meta's published wavelength
+    rule written independently in pure Python, inside the blend band, on both
+    edges and outside it (a wrong smoothing coefficient fails it).
+No reference test or golden vector exists for FlashInfer's RoPE kernel itself;
+the published formula is what is pinned.
 """
 from __future__ import annotations
 
@@ -401,8 +405,9 @@ def rope_frequencies(head_dim: int, rope_scale: float, rope_theta: float,
     ``interleave=True``.  Published formula: pair ``j`` (elements 2j, 2j+1)
     rotates at ``theta**(-2j/d)``; plain RoPE divides by ``rope_scale``;
     Llama-3.1 blends ``f/rope_scale`` and ``f`` with
-    ``smooth = clamp(f * old_ctx / (2*pi*(hi - lo)) - 1/(hi/lo - 1), 0, 1)``.
-    Parity unpinned (no reference test covers RoPE).
+    ``smooth = clamp(f * old_ctx / (2*pi*(hi - lo)) - 1/(hi/lo - 1), 0, 1)``,
+    which is Meta's wavelength rule ``(old_ctx / wavelen - lo) / (hi - lo)`` with
+    ``wavelen = 2*pi / f`` (pinned against that form in the tests).
     """
     j = torch.arange(head_dim // 2, dtype=torch.float64)
     f = rope_theta ** (-(2.0 * j) / head_dim)

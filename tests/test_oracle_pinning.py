@@ -414,3 +414,80 @@ def test_rope_closed_forms():
     f2 = O.rope_frequencies(128, 8.0, 5e5, 1.0, 4.0, 8192)
     assert abs(float(f2[0]) - 1.0) < 1e-12
     assert abs(float(f2[-1]) - float(O.rope_frequencies(128, 8.0, 5e5)[-1])) < 1e-18
+
+
+def _llama31_by_wavelength(head_dim, scale, theta, lo, hi, old_ctx):
+    """Meta's published Llama-3.1 frequency rule, written from wavelengths in pure Python
+    (no shared code with the oracle): keep f when its wavelength 2*pi/f is shorter than
+    old_ctx/hi, divide by ``scale`` when it is longer than old_ctx/lo, else blend
+    (1 - s) f/scale + s f with s = (old_ctx/wavelength - lo) / (hi - lo)."""
+    out = []
+    for j in range(head_dim // 2):
+        f = theta ** (-(2.0 * j) / head_dim)
+        wavelen = 2.0 * math.pi / f
+        if wavelen < old_ctx / hi:
+            out.append(f)
+        elif wavelen > old_ctx / lo:
+            out.append(f / scale)
+        else:
+            s = (old_ctx / wavelen - lo) / (hi - lo)
+            out.append((1.0 - s) * f / scale + s * f)
+    return out
+
+
+def _blend_weights(head_dim, theta, lo, hi, old_ctx):
+    return [(old_ctx * theta ** (-(2.0 * j) / head_dim) / (2.0 * math.pi) - lo) / (hi - lo)
+            for j in range(head_dim // 2)]
+
+
+@pytest.mark.parametrize("scale,theta,lo,hi,old_ctx", [
+    (8.0, 5e5, 1.0, 4.0, 8192),    # Llama-3.1-8B (model.py:87)
+    (32.0, 5e5, 1.0, 4.0, 8192),   # the 3.2 family's scale
+    (4.0, 1e4, 2.0, 8.0, 4096),    # band moved: other factors and base
+])
+def test_rope_llama31_blend_band_matches_published_rule(scale, theta, lo, hi, old_ctx):
+    got = O.rope_frequencies(128, scale, theta, lo, hi, old_ctx).tolist()
+    want = _llama31_by_wavelength(128, scale, theta, lo, hi, old_ctx)
+    inside = [j for j, s in enumerate(_blend_weights(128, theta, lo, hi, old_ctx)) if 0.0 < s < 1.0]
+    assert len(inside) >= 3, "the case must put pairs inside the blend band"
+    for j in range(64):
+        assert abs(got[j] - want[j]) <= 1e-12 * want[j], (j, got[j], want[j])
+    # both sides of the band take the plain rules
+    assert any(got[j] == 1.0 * theta ** (-(2.0 * j) / 128) for j in range(64))
+    assert any(abs(got[j] - theta ** (-(2.0 * j) / 128) / scale) < 1e-18 for j in range(64))
+
+
+@pytest.mark.parametrize("j", [9, 17, 25])
+def test_rope_llama31_band_edges(j):
+    """old_ctx chosen so pair j sits exactly on an edge: wavelength = old_ctx / hi gives f, =
+    old_ctx / lo gives f / scale (the blend is continuous there)."""
+    theta, scale, lo, hi = 5e5, 8.0, 1.0, 4.0
+    f = theta ** (-(2.0 * j) / 128)
+    wavelen = 2.0 * math.pi / f
+    hi_edge = O.rope_frequencies(128, scale, theta, lo, hi, hi * wavelen)
+    lo_edge = O.rope_frequencies(128, scale, theta, lo, hi, lo * wavelen)
+    assert abs(float(hi_edge[j]) - f) <= 1e-12 * f
+    assert abs(float(lo_edge[j]) - f / scale) <= 1e-12 * f
+    # one pair further in either direction is past the edge
+    assert abs(float(hi_edge[j - 1]) - theta ** (-(2.0 * (j - 1)) / 128)) <= 1e-12
+    assert abs(float(lo_edge[j + 1]) * scale - theta ** (-(2.0 * (j + 1)) / 128)) <= 1e-12 * f
+
+
+def test_rope_llama31_check_detects_a_wrong_coefficient():
+    """The blend check above is sensitive: a plausible slip in the smoothing coefficient
+    (hi + lo for hi - lo, or the offset's ratio inverted) moves the band's frequencies by far
+    more than its tolerance."""
+    d, scale, theta, lo, hi, old = 128, 8.0, 5e5, 1.0, 4.0, 8192
+    want = _llama31_by_wavelength(d, scale, theta, lo, hi, old)
+
+    def slipped(variant):
+        j = torch.arange(d // 2, dtype=torch.float64)
+        f = theta ** (-(2.0 * j) / d)
+        a = old / (2.0 * math.pi * (hi + lo)) if variant == "sum" else old / (2.0 * math.pi * (hi - lo))
+        c = -1.0 / (hi / lo - 1.0) if variant == "sum" else -1.0 / (lo / hi - 1.0)
+        s = torch.clamp(f * a + c, 0.0, 1.0)
+        return ((1.0 - s) * (f / scale) + s * f).tolist()
+
+    for variant in ("sum", "ratio"):
+        bad = slipped(variant)
+        assert max(abs(x - y) / y for x, y in zip(bad, want)) > 1e-3, variant

@@ -41,7 +41,7 @@ from . import model as model_mod
 from .model import Transformer, build_random_model
 from .page_selector_v2 import PageSelectorV2
 from .public_config import FINAL_PUBLIC_DELTA_BACKEND_CONFIG as _CFG
-from .scheduler import BatchScheduler, PageManager, Request
+from .scheduler import BatchSlots, PagePool, ServingRequest
 
 PAGE_SIZE = 16
 
@@ -148,7 +148,10 @@ class LMBackend:
 
         ``checkpoints`` is either a ``model.pth`` state dict (loaded with
         ``weights_only=True``; its parent directory names the shape, as in the
-        reference) or ``"random:<shape>"`` for a seeded random-init model.
+        reference) or ``"random:<shape>"`` for a seeded random-init model.  A state dict
+        loads strictly, as the reference's does (utils.py:217-221): separate wq/wk/wv and
+        w1/w3 tensors are merged by the modules' load hooks, and a missing or unknown key
+        raises instead of leaving a parameter at its random init.
         """
         if use_tp:
             raise NotImplementedError("tensor parallelism is out of scope for this one-GPU path")
@@ -159,7 +162,9 @@ class LMBackend:
         path = Path(ck)
         model = build_random_model(path.parent.name, self.device, self.dtype, seed=seed)
         state = torch.load(str(path), mmap=True, weights_only=True)
-        model.load_state_dict(state, assign=False, strict=False)
+        if "model" in state and "stories" in ck:  # nested checkpoints (utils.py:218-219)
+            state = state["model"]
+        model.load_state_dict(state, strict=True)
         self.model = model.to(self.dtype)
 
     def compile(self):
@@ -185,9 +190,8 @@ class LMBackend:
         # one private scratch page per slot: idle slots append/read only there
         self.num_pages = self.max_num_pages + max_batch_size
         self.scratch_pages = torch.arange(self.max_num_pages, self.num_pages, dtype=torch.int32)
-        self.page_manager = PageManager(self.max_num_pages, seed=0)
-        self.scheduler = BatchScheduler(max_batch_size, dev, self.is_main_process, self.pages_per_slot,
-                                        PAGE_SIZE, self.page_manager)
+        self.page_pool = PagePool(self.max_num_pages, seed=0)
+        self.scheduler = BatchSlots(max_batch_size, self.page_pool, verbose=self.is_main_process)
 
         self.enable_selective_cache = bool(getattr(cfg, "enable_selective_cache", False))
         self.subset_cache_size = int(getattr(cfg, "subset_cache_size", 64))
@@ -199,6 +203,12 @@ class LMBackend:
         B = max_batch_size
         self.cachelens = torch.zeros(B, **i32)
         self.active = torch.zeros(B, **i32)
+        # Host mirror of cachelens / active and the pages each slot's table holds, so a decode
+        # step that would take a row past its pages is refused before it runs (the device
+        # metadata clamps such a row to a full table, which would overwrite its last slot).
+        self._host_lens = [0] * B
+        self._host_active = [0] * B
+        self._slot_pages = [self.pages_per_slot] * B
         self.slot_block_table = self.scratch_pages.to(dev)[:, None].repeat(1, self.pages_per_slot).contiguous()
         self.page_selector = PageSelectorV2(B, self.pages_per_slot, True, self.k_eff,
                                            self.compression_ratio, self.L, dev,
@@ -280,8 +290,6 @@ class LMBackend:
                        pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
                        use_subset=self.use_subset_flag, out_indices=sel.paged_subset_kv_indices,
                        out_indptr=sel.paged_subset_kv_indptr)
-        if self.enable_delta_debug_page_selection_parity and not torch.cuda.is_current_stream_capturing():
-            self._debug_check_selection(st, B)
         return o
 
     def _debug_check_selection(self, st, B):
@@ -298,6 +306,76 @@ class LMBackend:
                 not torch.equal(ri[:n], sel.paged_subset_kv_indices[:n]):
             raise RuntimeError("DELTA page selection mismatch against torch-score reference path")
 
+    def _debug_checks_after_step(self, cachelens_before: torch.Tensor):
+        """The reference's debug parity checks, run after a decode step (eager or replayed) on
+        the tables and buffers that step left: the fast page info against a host rebuild
+        (backend.py:1966-2012) and the planner's selection against a selection from two-pass
+        scores of the same dump (backend.py:812-819)."""
+        B = self.batch_size
+        if self.enable_delta_debug_fast_decode_page_info_parity:
+            self._debug_check_decode_page_info(cachelens_before)
+        if self.enable_delta_debug_page_selection_parity and self.enable_selective_cache and "plan" in self.layer_roles:
+            self._debug_check_selection(self._decode_csr(), B)
+
+    def _debug_check_decode_page_info(self, cachelens_before: torch.Tensor):
+        """Device decode metadata vs the same tables rebuilt on the host from ``cachelens`` and
+        the slot block table (what ``Request.plan(1, 16)`` and the generic snapshot give,
+        scheduler.py:60-66, backend.py:1850-1936); raises on the first difference."""
+        B, pps, k = self.batch_size, self.pages_per_slot, self.k_eff
+        lens = [int(x) for x in cachelens_before.tolist()]
+        act = [int(x) for x in self.active.tolist()]
+        bt = self.slot_block_table.cpu()
+        counts = [(n + 1) // PAGE_SIZE + 1 for n in lens]
+        last = [(n + 1) % PAGE_SIZE for n in lens]
+        full_tot = sum(c for c, a in zip(counts, act) if a)
+        sub_tot = sum(min(c, k) for c, a in zip(counts, act) if a)
+        use = bool(self.enable_selective_cache and sub_tot > 0 and full_tot / sub_tot > self.compression_ratio)
+        sub_counts = [min(c, k) if use else c for c in counts]
+        ip, sub_ip = [0], [0]
+        ind, sub_ind = [], []
+        for b in range(B):
+            row = bt[b, :counts[b]].tolist()
+            ind += row
+            sub_ind += row[counts[b] - sub_counts[b]:]
+            ip.append(len(ind))
+            sub_ip.append(len(sub_ind))
+        sel = self.page_selector
+        rbt = torch.zeros((B, pps), dtype=torch.int32)
+        for b in range(B):
+            rbt[b, :counts[b]] = bt[b, :counts[b]]
+        i32 = dict(dtype=torch.int32)
+        checks = [
+            ("use_subset", self.use_subset_flag.cpu(), torch.tensor([int(use)], **i32)),
+            ("paged_kv_indptr", sel.paged_kv_indptr[:B + 1].cpu(), torch.tensor(ip, **i32)),
+            ("paged_kv_indices", sel.paged_kv_indices[:ip[-1]].cpu(), torch.tensor(ind, **i32)),
+            ("paged_kv_last_page_len", sel.paged_kv_last_page_len[:B].cpu(), torch.tensor(last, **i32)),
+            ("block_table", sel._block_table[:B].cpu(), rbt),
+        ]
+        if not use or "plan" not in self.layer_roles:  # a planner step rewrites the subset CSR
+            checks += [("paged_subset_kv_indptr", sel.paged_subset_kv_indptr[:B + 1].cpu(), torch.tensor(sub_ip, **i32)),
+                       ("paged_subset_kv_indices", sel.paged_subset_kv_indices[:sub_ip[-1]].cpu(),
+                        torch.tensor(sub_ind, **i32))]
+        for name, got, want in checks:
+            if not torch.equal(got, want):
+                raise RuntimeError(f"DELTA fast decode page-info mismatch in {name}")
+
+    # --------------------------------------------------------- planner scores
+    def _compute_page_scores_from_attention_buffer(self) -> torch.Tensor:
+        """del3_legacy_softmax page scores of the last decode step's planner dump
+        (backend.py:887-913): fp32 ``[batch, pages_per_slot]``, ``score[b, j] = sum over the
+        tokens t of page j of max_h softmax_t(dump[b, h, :])``; pages past a row's end score 0.
+        Uses the planner's lse for the normaliser, as the fused path does."""
+        st = self._decode_csr()
+        return K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
+                                         scores=self.page_scores, batch=self.batch_size, workspace=self.workspace)
+
+    def _compute_page_scores_reference(self) -> torch.Tensor:
+        """The same scores from the dump alone (softmax normaliser recomputed, no lse): the
+        reference's torch-score path used by its selection parity check (backend.py:906-909)."""
+        st = self._decode_csr()
+        return K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot,
+                                         batch=self.batch_size)
+
     # ------------------------------------------------------------ decode step
     def _decode_csr(self) -> _StepCSR:
         sel = self.page_selector
@@ -312,7 +390,7 @@ class LMBackend:
                            self.enable_selective_cache, sel.paged_kv_indptr, sel.paged_kv_indices,
                            sel.paged_kv_last_page_len, row_block_table=sel._block_table,
                            subset_indices=sel.paged_subset_kv_indices, subset_indptr=sel.paged_subset_kv_indptr,
-                           use_subset=self.use_subset_flag)
+                           use_subset=self.use_subset_flag, active=self.active)
         self._step = self._decode_csr()
         try:
             tokens = self.model(self.static_tokens, self.cachelens, self.qo_indptr, sel.paged_kv_indices,
@@ -339,9 +417,26 @@ class LMBackend:
         self._decode_graph = graph
         self._decode_graph_stats["captures"] += 1
 
+    def sync_host_lens(self):
+        """Re-read ``cachelens`` / ``active`` from the device into the host mirror (after a
+        caller wrote them directly)."""
+        self._host_lens = [int(x) for x in self.cachelens.tolist()]
+        self._host_active = [int(x) for x in self.active.tolist()]
+
+    def _check_decode_budget(self, n: int):
+        for b in range(self.batch_size):
+            if self._host_active[b]:
+                need = (self._host_lens[b] + n) // PAGE_SIZE + 1
+                if need > self._slot_pages[b]:
+                    raise RuntimeError(
+                        f"decode budget exhausted: slot {b} holds {self._host_lens[b]} tokens and "
+                        f"{self._slot_pages[b]} pages; {n} more decode step(s) need {need} pages")
+
     @torch.inference_mode()
     def decode_steps(self, n: int = 1, use_graph: Optional[bool] = None):
-        """Run ``n`` decode steps for every slot, feeding tokens back on the device."""
+        """Run ``n`` decode steps for every slot, feeding tokens back on the device.  Raises
+        before running when a row would need more pages than its slot holds."""
+        self._check_decode_budget(n)
         use_graph = self.enable_cuda_graph_decode if use_graph is None else use_graph
         if use_graph and self._decode_graph is None and self._decode_graph_failed is None:
             try:
@@ -352,12 +447,29 @@ class LMBackend:
                 self._decode_graph_fallback_reasons["capture_failed"] += 1
                 if self.is_main_process:
                     print(f"[hip graph decode] capture failed, running eagerly: {exc}")
+        debug = self.enable_delta_debug_fast_decode_page_info_parity or (
+            self.enable_delta_debug_page_selection_parity and self.enable_selective_cache)
         for _ in range(n):
+            before = self.cachelens.clone() if debug else None
             if use_graph and self._decode_graph is not None:
-                self._decode_graph.replay()
-                self._decode_graph_stats["replays"] += 1
+                try:
+                    self._decode_graph.replay()
+                    self._decode_graph_stats["replays"] += 1
+                except Exception as exc:  # replay failure -> eager from here on (backend.py:1172-1181)
+                    self._decode_graph = None
+                    self._decode_graph_failed = repr(exc)
+                    self._decode_graph_stats["replay_failures"] += 1
+                    self._decode_graph_fallback_reasons["replay_failed"] += 1
+                    if self.is_main_process:
+                        print(f"[hip graph decode] replay failed, running eagerly: {exc}")
+                    self._decode_body(advance=True)
             else:
                 self._decode_body(advance=True)
+            if debug:
+                self._debug_checks_after_step(before)
+        for b in range(self.batch_size):
+            if self._host_active[b]:
+                self._host_lens[b] += n
         return self.static_tokens
 
     # --------------------------------------------------- synthetic contexts
@@ -380,8 +492,11 @@ class LMBackend:
             need = (n + decode_budget) // PAGE_SIZE + 1
             if need > self.pages_per_slot:
                 raise ValueError(f"{n} + {decode_budget} tokens need {need} pages > {self.pages_per_slot}")
-            bt[b, :need] = torch.tensor(self.page_manager.alloc(need), dtype=torch.int32)
+            bt[b, :need] = torch.tensor(self.page_pool.take(need), dtype=torch.int32)
         self.slot_block_table.copy_(bt)
+        self._slot_pages = [(n + decode_budget) // PAGE_SIZE + 1 for n in lens]
+        self._host_lens = list(lens)
+        self._host_active = [1] * B
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
         outl = None
@@ -404,31 +519,35 @@ class LMBackend:
     def add_requests(self, input_ids_list: list, max_lengths: list, eot_token_ids: list):
         if self.scheduler is None:
             raise RuntimeError("Backend not initialized. Call setup_caches first.")
-        self.scheduler.add_requests(input_ids_list, max_lengths, eot_token_ids)
+        self.scheduler.submit(input_ids_list, max_lengths, eot_token_ids)
 
     @torch.inference_mode()
-    def _sync_slot_block_table(self, slot_id: int, request: Request, old_page_count: int):
-        new = len(request.page_indices)
+    def _sync_slot_block_table(self, slot_id: int, request: ServingRequest, old_page_count: int):
+        new = len(request.pages)
         if new > old_page_count:
             self.slot_block_table[slot_id, old_page_count:new].copy_(
-                torch.tensor(request.page_indices[old_page_count:new], dtype=torch.int32))
+                torch.tensor(request.pages[old_page_count:new], dtype=torch.int32))
+        self._slot_pages[slot_id] = new
 
     @torch.inference_mode()
     def _release_slot(self, slot_id: int):
         self.cachelens[slot_id].fill_(0)
         self.active[slot_id].fill_(0)
         self.slot_block_table[slot_id].fill_(int(self.scratch_pages[slot_id]))
+        self._host_lens[slot_id] = 0
+        self._host_active[slot_id] = 0
+        self._slot_pages[slot_id] = self.pages_per_slot  # the scratch page in every column
 
     @torch.inference_mode()
     def run_scheduler_loop(self):
         """Serve queued requests until done (backend.py:1486-1553)."""
         torch.cuda.synchronize(self.device)
-        self.scheduler.stats["start_time"] = time.perf_counter()
+        self.scheduler.t_start = time.perf_counter()
         self._step_records = []
         i = 0
         while True:
             i += 1
-            finished = self.scheduler.check_finished_requests()
+            finished = self.scheduler.release_finished()
             if finished and self.throughput_mode:
                 if self.is_main_process:
                     print(f"\n[throughput_mode] {len(finished)} request(s) finished -- stopping all")
@@ -436,12 +555,11 @@ class LMBackend:
                 break
             for slot_id in finished:
                 self._release_slot(slot_id)
-            new_slots, new_reqs = self.scheduler.schedule_requests()
-            for slot_id, req in zip(new_slots, new_reqs):
-                req.initialize_pages(slot_id, self.pages_per_slot)
+            for slot_id, req in self.scheduler.fill_free_slots():
+                req.admit()
                 self.slot_block_table[slot_id].fill_(int(self.scratch_pages[slot_id]))
                 self._sync_slot_block_table(slot_id, req, 0)
-            if not self.scheduler.has_active_requests():
+            if not self.scheduler.any_active():
                 break
             self._forward(i)
         if self.is_main_process:
@@ -449,17 +567,18 @@ class LMBackend:
         return self.get_detailed_results()
 
     def _force_finish_all_requests(self):
-        for slot_id in range(self.batch_size):
-            rid = int(self.scheduler.runner_slots[slot_id])
-            if rid != -1:
-                req = self.scheduler.request_queue[rid]
-                if not req.is_finished():
-                    req.status = "finished"
-                self.scheduler.runner_slots[slot_id] = -1
-                self._release_slot(slot_id)
+        """Throughput mode: end every running request now (backend.py:1555-1563)."""
+        for slot_id in self.scheduler.occupied():
+            req = self.scheduler.request_in(slot_id)
+            if not req.finished:
+                req.state = ServingRequest.FINISHED
+                req.t_end = time.perf_counter()
+                self.page_pool.give_back(req.pages)
+            self.scheduler.slots[slot_id] = None
+            self._release_slot(slot_id)
 
     def _active_slots(self) -> List[int]:
-        return [s for s in range(self.batch_size) if int(self.scheduler.runner_slots[s]) != -1]
+        return self.scheduler.occupied()
 
     def _record_event(self):
         ev = torch.cuda.Event(enable_timing=True)
@@ -470,19 +589,20 @@ class LMBackend:
         slots = self._active_slots()
         if not slots:
             return
-        reqs = [self.scheduler.request_queue[int(self.scheduler.runner_slots[s])] for s in slots]
+        reqs = [self.scheduler.request_in(s) for s in slots]
         ev0 = self._record_event()
-        decode_only = all(len(r.output_ids) > 0 for r in reqs)
+        decode_only = all(len(r.generated) > 0 for r in reqs)
         if decode_only:
             self._using_subset_cache_this_step = self.enable_selective_cache
             for s, r in zip(slots, reqs):
-                old = len(r.page_indices)
-                r.plan(1, PAGE_SIZE)
+                old = len(r.pages)
+                r.reserve(1)
                 self._sync_slot_block_table(s, r, old)
-                self._pinned_tokens[s] = r.output_ids[-1]
+                self._pinned_tokens[s] = r.generated[-1]
             mask = torch.zeros(self.batch_size, dtype=torch.int32)
             mask[slots] = 1
             self.active.copy_(mask)
+            self._host_active = mask.tolist()
             self.static_tokens[0].copy_(self._pinned_tokens, non_blocking=True)
             ev1 = self._record_event()
             tokens = self.decode_steps(1)
@@ -496,8 +616,8 @@ class LMBackend:
             next_tokens, qo_lengths = self._prefill_forward(slots, reqs)
             ev2 = self._record_event()
         for r, t in zip(reqs, next_tokens):
-            r.append_output(int(t))
-        self.scheduler.stats["total_tokens_generated"] += sum(qo_lengths)
+            r.record(int(t))
+        self.scheduler.tokens_generated += sum(qo_lengths)
         ev3 = self._record_event()
         self._pending_events.append((step_index, ev0, ev1, ev2, ev3, len(slots)))
 
@@ -508,15 +628,15 @@ class LMBackend:
         dev = self.device
         toks, qo_lens, rows_pages, rows_last, offsets = [], [], [], [], []
         for s, r in zip(slots, reqs):
-            q_tokens = r.get_qo_tokens()
-            old = len(r.page_indices)
+            q_tokens = r.next_input()
+            old = len(r.pages)
             start = r.kv_len(PAGE_SIZE)
-            r.plan(len(q_tokens), PAGE_SIZE)
+            r.reserve(len(q_tokens))
             self._sync_slot_block_table(s, r, old)
             toks.append(q_tokens.to(torch.long))
             qo_lens.append(len(q_tokens))
-            rows_pages.append(list(r.page_indices))
-            rows_last.append(r.page_lastlen)
+            rows_pages.append(list(r.pages))
+            rows_last.append(r.fill)
             offsets.append(start)
         # the rows' page CSR (after planning, it covers the new tokens)
         kv_indptr, kv_indices = [0], []
@@ -538,6 +658,8 @@ class LMBackend:
         for s, q_len, start in zip(slots, qo_lens, offsets):
             self.cachelens[s].fill_(start + q_len)
             self.active[s].fill_(1)
+            self._host_lens[s] = start + q_len
+            self._host_active[s] = 1
         last_pos = (qo_indptr[1:] - 1).long()
         next_tokens = out[0].index_select(0, last_pos).cpu().tolist()
         return next_tokens, qo_lens
@@ -545,8 +667,8 @@ class LMBackend:
     # ------------------------------------------------------------- reporting
     def _print_final_stats(self):
         torch.cuda.synchronize(self.device)
-        total_time = time.perf_counter() - self.scheduler.stats["start_time"]
-        total_tokens = self.scheduler.stats["total_tokens_generated"]
+        total_time = time.perf_counter() - self.scheduler.t_start
+        total_tokens = self.scheduler.tokens_generated
         for step, e0, e1, e2, e3, bsz in self._pending_events:
             self._step_records.append({"step": step, "collect_pages_ms": e0.elapsed_time(e1),
                                        "model_forward_ms": e1.elapsed_time(e2),
@@ -555,7 +677,7 @@ class LMBackend:
         self._pending_events.clear()
         print(f"\n{'=' * 60}\nSCHEDULER PERFORMANCE SUMMARY\n{'=' * 60}")
         print(f"Total time: {total_time:.2f}s")
-        print(f"Total requests: {len(self.scheduler.request_queue)}")
+        print(f"Total requests: {len(self.scheduler.requests)}")
         print(f"Total tokens: {total_tokens:,}")
         print(f"Tokens per second: {total_tokens / max(total_time, 1e-9):.2f}")
         if self.enable_cuda_graph_decode:
@@ -583,4 +705,4 @@ class LMBackend:
     def get_detailed_results(self):
         if self.scheduler is None:
             return []
-        return self.scheduler.get_detailed_results(self.tokenizer)
+        return self.scheduler.report(self.tokenizer)

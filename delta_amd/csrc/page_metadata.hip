@@ -12,6 +12,9 @@
 // `cachelens` and a preallocated slot block table, so a whole decode step can
 // be replayed from a hipGraph without host work.  One block per row; each
 // block recomputes its row offset from the counts of the rows before it.
+// Idle slots (active[b] == 0) keep their CSR entries (one scratch page) but are
+// left out of the gate's page totals, which the reference sums over its active
+// rows only (backend.py:2047-2067, 2104-2109).
 #include "delta_common.h"
 
 namespace delta {
@@ -41,6 +44,7 @@ __global__ void __launch_bounds__(256)
 
 struct PageInfoArgs {
   const int32_t *cachelens;
+  const int32_t *active;  // [batch] or null (every row active)
   const int32_t *slot_bt;
   int batch, pages_per_slot, k;
   double compression_ratio;
@@ -70,8 +74,10 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
     int np, lp;
     row_pages(a, i, &np, &lp);
     const int sc = np < a.k ? np : a.k;
-    full_tot += np;
-    sub_tot += sc;
+    if (a.active == nullptr || a.active[i] != 0) {
+      full_tot += np;
+      sub_tot += sc;
+    }
     if (i < b) {
       full_before += np;
       sub_before += sc;
@@ -149,9 +155,9 @@ extern "C" DELTA_EXPORT int delta_pack_page_indices(const int32_t *slot_block_ta
   return check_launch("delta_pack_page_indices");
 }
 
-extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, const int32_t *slot_block_table,
-                                                   int batch, int pages_per_slot, int k, double compression_ratio,
-                                                   int selective, int32_t *kv_indptr, int32_t *kv_indices,
+extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, const int32_t *active,
+                                                   const int32_t *slot_block_table, int batch, int pages_per_slot,
+                                                   int k, double compression_ratio, int selective, int32_t *kv_indptr, int32_t *kv_indices,
                                                    int32_t *kv_last_page_len, int32_t *row_block_table,
                                                    int32_t *subset_indices, int32_t *subset_indptr,
                                                    int32_t *use_subset, delta_stream_t stream) {
@@ -165,6 +171,7 @@ extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, con
     return set_error(DELTA_ERR_INVALID, "delta_decode_page_info: subset_indices and subset_indptr go together");
   PageInfoArgs a;
   a.cachelens = cachelens;
+  a.active = active;
   a.slot_bt = slot_block_table;
   a.batch = batch;
   a.pages_per_slot = pages_per_slot;

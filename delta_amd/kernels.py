@@ -398,12 +398,18 @@ def decode_page_info(cachelens: torch.Tensor, slot_block_table: torch.Tensor, ba
                      row_block_table: Optional[torch.Tensor] = None,
                      subset_indices: Optional[torch.Tensor] = None,
                      subset_indptr: Optional[torch.Tensor] = None,
-                     use_subset: Optional[torch.Tensor] = None) -> None:
-    """Device-side decode page info for rows 0..batch-1 (``delta_decode_page_info``)."""
+                     use_subset: Optional[torch.Tensor] = None,
+                     active: Optional[torch.Tensor] = None) -> None:
+    """Device-side decode page info for rows 0..batch-1 (``delta_decode_page_info``).
+
+    ``active`` (int32 [batch], optional) marks the rows the ``use_subset`` gate counts; idle
+    rows still get their CSR entries."""
     dev = _check_cuda(cachelens, slot_block_table, kv_indptr, kv_indices, kv_last_page_len,
-                      row_block_table, subset_indices, subset_indptr, use_subset)
+                      row_block_table, subset_indices, subset_indptr, use_subset, active)
     pps = slot_block_table.shape[1]
     _check_i32("cachelens", cachelens, batch)
+    if active is not None:
+        _check_i32("active", active, batch)
     _check_i32("slot_block_table", slot_block_table, batch * pps)
     _check_i32("kv_indptr", kv_indptr, batch + 1)
     _check_i32("kv_indices", kv_indices, batch * pps)
@@ -418,7 +424,7 @@ def decode_page_info(cachelens: torch.Tensor, slot_block_table: torch.Tensor, ba
     if use_subset is not None:
         _check_i32("use_subset", use_subset, 1)
     _lib.call("delta_decode_page_info",
-              cachelens.data_ptr(), slot_block_table.data_ptr(), int(batch), int(pps), int(k),
+              cachelens.data_ptr(), _ptr(active), slot_block_table.data_ptr(), int(batch), int(pps), int(k),
               float(compression_ratio), int(bool(selective)), kv_indptr.data_ptr(),
               kv_indices.data_ptr(), kv_last_page_len.data_ptr(), _ptr(row_block_table),
               _ptr(subset_indices), _ptr(subset_indptr), _ptr(use_subset), _stream(dev))

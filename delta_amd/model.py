@@ -269,6 +269,16 @@ class Attention(nn.Module):
         self.dim = config.n_head * config.head_dim
         # debug capture (tests): when a list, each call appends (q, o)
         self.record: Optional[list] = None
+        self._register_load_state_dict_pre_hook(self._merge_wq_wk_wv)
+
+    @staticmethod
+    def _merge_wq_wk_wv(state_dict, prefix, *args):
+        """Checkpoints with separate q/k/v projections (and biases) load into the merged
+        ``wqkv`` in q, k, v row order (the reference's load hook, model.py:392-405)."""
+        for kind in ("weight", "bias"):
+            names = [f"{prefix}{w}.{kind}" for w in ("wq", "wk", "wv")]
+            if names[0] in state_dict:
+                state_dict[f"{prefix}wqkv.{kind}"] = torch.cat([state_dict.pop(n) for n in names])
 
     def forward(self, x, offsets, kv_append_indptr, kv_page_indices, kv_page_indptr, kv_page_lastlen,
                 fused: bool = False):
@@ -322,12 +332,15 @@ class FeedForward(nn.Module):
         self.w2 = nn.Linear(config.intermediate_size, config.dim, bias=False)
         self._register_load_state_dict_pre_hook(self._merge_w1_w3)
 
-    @staticmethod
-    def _merge_w1_w3(state_dict, prefix, *args):
+    def _merge_w1_w3(self, state_dict, prefix, *args):
+        """Separate ``w1`` / ``w3`` weights load into the merged gate|up parameter in whichever
+        layout this module holds it (transposed ``w13_t`` or row-major ``w13``)."""
         if prefix + "w1.weight" in state_dict:
-            w1 = state_dict.pop(prefix + "w1.weight")
-            w3 = state_dict.pop(prefix + "w3.weight")
-            state_dict[prefix + "w13_t"] = torch.cat([w1, w3]).t().contiguous()
+            w13 = torch.cat([state_dict.pop(prefix + "w1.weight"), state_dict.pop(prefix + "w3.weight")])
+            if hasattr(self, "w13"):
+                state_dict[prefix + "w13"] = w13
+            else:
+                state_dict[prefix + "w13_t"] = w13.t().contiguous()
 
     @torch.no_grad()
     def use_row_major_w13(self) -> None:

@@ -1,166 +1,189 @@
-"""Host request bookkeeping with DELTA's page-table semantics.
+"""Serving-loop bookkeeping: the physical page pool, each request's pages, the batch slots.
 
-Mirrors DELTA/Engine/DELTA/scheduler.py:8-186: a shuffled global page pool
-(``PageManager``, ``random.seed(seed)`` then ``random.shuffle``; pages are
-popped off the end), requests that grow their page list as tokens are planned
-(``Request.plan``: ``page_lastlen += qo_len``; every time it reaches 16 a
-fresh page is taken, so a full page is followed by an empty one) and a
-slot-based batch scheduler.
+The engine derives every decode step's page tables on the device from two things this module
+owns on the host: which physical pages a slot's request holds (copied into the slot block
+table) and how many tokens it holds.  Three rules of DELTA/Engine/DELTA/scheduler.py decide
+both, and are kept exactly:
+
+* Pool order (scheduler.py:8-30): the page ids ``0..n-1`` are shuffled once by a generator
+  seeded with ``seed`` (the same permutation ``random.seed(seed); random.shuffle(ids)``
+  gives) and handed out from the end of that order.
+* Page growth (scheduler.py:60-74): a request starts on one empty page; adding ``n`` tokens
+  raises the last page's fill by ``n`` and takes a fresh page each time the fill reaches 16,
+  so a full page is always followed by an empty one and ``kv_len = (pages - 1) * 16 + fill``.
+* Completion (scheduler.py:83-90): a request ends on a stop token or once prompt plus output
+  reach ``max_length``, and its pages go back to the pool.
+
+Everything else is this build's own: requests live in a flat list indexed by id, slots hold
+request ids (``None`` when free), waiting ids sit in a deque, and the pool reshuffles its
+free ids with its own generator when pages come back (the reference reshuffles with the
+process-wide one, so only the order after a release may differ).
 """
 from __future__ import annotations
 
 import random
 import time
-from typing import List, Optional, Tuple
+from collections import deque
+from typing import Deque, Dict, List, Optional, Sequence, Tuple
 
 import torch
 
+PAGE_SIZE = 16
 
-class PageManager:
-    """Randomised pool of physical KV pages (scheduler.py:8-40)."""
+
+class PagePool:
+    """Shuffled pool of physical KV page ids."""
 
     def __init__(self, total_pages: int, seed: Optional[int] = None):
         self.total_pages = int(total_pages)
-        self.free: List[int] = list(range(self.total_pages))
-        self.in_use = set()
-        if seed is not None:
-            random.seed(seed)
-        random.shuffle(self.free)
+        self._rng = random.Random(seed)
+        ids = list(range(self.total_pages))
+        self._rng.shuffle(ids)
+        self._free: List[int] = ids          # handed out from the end
+        self._held = set()
 
-    def alloc_one(self) -> int:
-        if not self.free:
-            raise RuntimeError("Out of KV pages: pool is empty")
-        p = self.free.pop()
-        self.in_use.add(p)
-        return p
+    @property
+    def available(self) -> int:
+        return len(self._free)
 
-    def alloc(self, n: int) -> List[int]:
-        if n > len(self.free):
-            raise RuntimeError(f"Out of KV pages: need {n}, have {len(self.free)} left")
-        return [self.alloc_one() for _ in range(n)]
+    def take(self, n: int = 1) -> List[int]:
+        """``n`` pages from the end of the free order (all or none)."""
+        if n > len(self._free):
+            raise RuntimeError(f"Out of KV pages: {n} wanted, {len(self._free)} free")
+        got = [self._free.pop() for _ in range(n)]
+        self._held.update(got)
+        return got
 
-    def free_pages(self, pages: List[int]):
-        for p in pages:
-            if p in self.in_use:
-                self.in_use.remove(p)
-                self.free.append(p)
-        random.shuffle(self.free)
+    def give_back(self, pages: Sequence[int]) -> None:
+        back = [p for p in pages if p in self._held]
+        self._held.difference_update(back)
+        self._free.extend(back)
+        self._rng.shuffle(self._free)
 
 
-class Request:
-    """One generation request (scheduler.py:43-93)."""
+class ServingRequest:
+    """One prompt being served: its tokens, its pages and its timing."""
 
-    def __init__(self, id: int, input_ids: torch.Tensor, max_length: int, eot_token_ids: list,
-                 page_manager: PageManager) -> None:
-        self.id = id
-        self.input_ids = input_ids
-        self.max_length = max_length
-        self.eot_token_ids = eot_token_ids
-        self.output_ids: List[int] = []
-        self.page_manager = page_manager
-        self.status = "waiting"
-        self.page_indices: List[int] = []
-        self.page_lastlen = 0
-        self.start_time = None
-        self.end_time = None
+    WAITING, ACTIVE, FINISHED = "waiting", "active", "finished"
 
-    def plan(self, qo_len: int, page_size: int):
-        """Account for ``qo_len`` new tokens, taking pages as they fill."""
-        self.page_lastlen += qo_len
-        while self.page_lastlen >= page_size:
-            self.page_indices.append(self.page_manager.alloc_one())
-            self.page_lastlen -= page_size
+    def __init__(self, rid: int, prompt: torch.Tensor, max_length: int, stop_ids: Sequence[int],
+                 pool: PagePool):
+        self.rid = rid
+        self.prompt = prompt
+        self.max_length = int(max_length)
+        self.stop_ids = set(int(t) for t in stop_ids)
+        self.generated: List[int] = []
+        self.pages: List[int] = []
+        self.fill = 0                  # tokens in the last page
+        self.state = self.WAITING
+        self.t_start: Optional[float] = None
+        self.t_end: Optional[float] = None
+        self._pool = pool
 
-    def initialize_pages(self, slot_id: int, pages_per_slot: int):
-        self.status = "active"
-        self.start_time = time.perf_counter()
-        self.page_indices = [self.page_manager.alloc_one()]
-        self.page_lastlen = 0
+    # -- pages
+    def admit(self) -> None:
+        """Start serving: one empty page."""
+        self.state = self.ACTIVE
+        self.t_start = time.perf_counter()
+        self.pages = self._pool.take(1)
+        self.fill = 0
 
-    def kv_len(self, page_size: int = 16) -> int:
-        return (len(self.page_indices) - 1) * page_size + self.page_lastlen
+    def reserve(self, n_tokens: int, page_size: int = PAGE_SIZE) -> None:
+        """Account for ``n_tokens`` new tokens (the page-growth rule above)."""
+        self.fill += int(n_tokens)
+        grow = self.fill // page_size
+        if grow:
+            self.pages.extend(self._pool.take(grow))
+            self.fill -= grow * page_size
 
-    def get_qo_tokens(self):
-        if len(self.output_ids) == 0:
-            return self.input_ids
-        return torch.tensor([self.output_ids[-1]], dtype=torch.long)
+    def kv_len(self, page_size: int = PAGE_SIZE) -> int:
+        return (len(self.pages) - 1) * page_size + self.fill
 
-    def append_output(self, token_id: int):
-        self.output_ids.append(token_id)
-        if token_id in self.eot_token_ids or (len(self.input_ids) + len(self.output_ids)) >= self.max_length:
-            self.page_manager.free_pages(self.page_indices)
-            self.status = "finished"
-            self.end_time = time.perf_counter()
+    # -- tokens
+    def next_input(self) -> torch.Tensor:
+        """The tokens of this request's next forward: the prompt, then the last output."""
+        return self.prompt if not self.generated else torch.tensor([self.generated[-1]], dtype=torch.long)
+
+    def record(self, token: int) -> bool:
+        """Append an output token; True when the request is now finished."""
+        self.generated.append(int(token))
+        if int(token) in self.stop_ids or len(self.prompt) + len(self.generated) >= self.max_length:
+            self._pool.give_back(self.pages)
+            self.state = self.FINISHED
+            self.t_end = time.perf_counter()
             return True
         return False
 
-    def is_finished(self):
-        return self.status == "finished"
+    @property
+    def finished(self) -> bool:
+        return self.state == self.FINISHED
+
+    def summary(self, tokenizer=None) -> Dict:
+        """The per-request record the reference's result consumers read (same keys)."""
+        elapsed = (self.t_end - self.t_start) if (self.t_end and self.t_start) else 0
+        n_out = len(self.generated)
+        rec = {"request_id": self.rid, "status": self.state, "input_length": len(self.prompt),
+               "output_length": n_out, "tokens_generated": n_out, "total_time": elapsed,
+               "tokens_per_second": n_out / elapsed if elapsed > 0 else 0}
+        if tokenizer is not None:
+            rec["input_text"] = _decode_or_placeholder(tokenizer, self.prompt)
+            rec["output_text"] = _decode_or_placeholder(tokenizer, self.generated)
+        return rec
 
 
-class BatchScheduler:
-    """Slot scheduler (scheduler.py:96-186)."""
+def _decode_or_placeholder(tokenizer, ids) -> str:
+    try:
+        return tokenizer.decode(ids, skip_special_tokens=True)
+    except Exception:  # a tokenizer that cannot take these ids still yields a record
+        return f"[{len(ids)} tokens]"
 
-    def __init__(self, batch_size: int, device, is_main_process: bool, pages_per_slot: int,
-                 page_size: int, page_manager: PageManager):
-        self.is_main_process = is_main_process
-        self.pages_per_slot = pages_per_slot
-        self.page_size = page_size
-        self.page_manager = page_manager
-        self.max_pages = 0
-        self.active_bsz = 0
-        self.request_queue: List[Request] = []
-        self.waiting_queue_ids: List[int] = []
-        self.runner_slots = torch.tensor([-1] * batch_size)
-        self.stats = {"total_tokens_generated": 0, "start_time": None, "encode_steps": 0, "decode_steps": 0}
 
-    def add_requests(self, input_ids_list: list, max_lengths, eot_token_ids: list):
-        for i, input_ids in enumerate(input_ids_list):
-            max_length = max_lengths[i] if isinstance(max_lengths, list) else max_lengths
-            rid = len(self.request_queue)
-            self.request_queue.append(Request(rid, input_ids, max_length, eot_token_ids, self.page_manager))
-            self.waiting_queue_ids.append(rid)
-        if self.is_main_process:
-            print(f"Added {len(input_ids_list)} requests. Total waiting: {len(self.waiting_queue_ids)}")
+class BatchSlots:
+    """Fixed batch slots over a queue of requests (free slots take waiting requests in order)."""
 
-    def schedule_requests(self) -> Tuple[List[int], List[Request]]:
-        slots, reqs = [], []
-        for slot_id in range(len(self.runner_slots)):
-            if self.runner_slots[slot_id] == -1 and self.waiting_queue_ids:
-                rid = self.waiting_queue_ids.pop(0)
-                self.runner_slots[slot_id] = rid
-                slots.append(slot_id)
-                reqs.append(self.request_queue[rid])
-        return slots, reqs
+    def __init__(self, batch_size: int, pool: PagePool, verbose: bool = True):
+        self.pool = pool
+        self.verbose = verbose
+        self.slots: List[Optional[int]] = [None] * int(batch_size)
+        self.requests: List[ServingRequest] = []
+        self.waiting: Deque[int] = deque()
+        self.tokens_generated = 0
+        self.t_start: Optional[float] = None
 
-    def check_finished_requests(self) -> List[int]:
-        finished = []
-        for slot_id in range(len(self.runner_slots)):
-            rid = int(self.runner_slots[slot_id])
-            if rid != -1 and self.request_queue[rid].is_finished():
-                finished.append(slot_id)
-                self.runner_slots[slot_id] = -1
-        return finished
+    def submit(self, prompts: Sequence[torch.Tensor], max_lengths, stop_ids: Sequence[int]) -> None:
+        for i, prompt in enumerate(prompts):
+            cap = max_lengths[i] if isinstance(max_lengths, (list, tuple)) else max_lengths
+            req = ServingRequest(len(self.requests), prompt, cap, stop_ids, self.pool)
+            self.requests.append(req)
+            self.waiting.append(req.rid)
+        if self.verbose:
+            print(f"queued {len(prompts)} request(s); {len(self.waiting)} waiting")
 
-    def has_active_requests(self) -> bool:
-        return any(int(x) != -1 for x in self.runner_slots)
+    def fill_free_slots(self) -> List[Tuple[int, ServingRequest]]:
+        """Place waiting requests into free slots (lowest slot first); returns (slot, request)."""
+        placed = []
+        for s, rid in enumerate(self.slots):
+            if rid is None and self.waiting:
+                req = self.requests[self.waiting.popleft()]
+                self.slots[s] = req.rid
+                placed.append((s, req))
+        return placed
 
-    def get_detailed_results(self, tokenizer=None):
-        results = []
-        for r in self.request_queue:
-            if not r.is_finished():
-                continue
-            total = r.end_time - r.start_time if r.end_time and r.start_time else 0
-            res = {"request_id": r.id, "status": r.status, "input_length": len(r.input_ids),
-                   "output_length": len(r.output_ids), "tokens_generated": len(r.output_ids),
-                   "total_time": total,
-                   "tokens_per_second": len(r.output_ids) / total if total > 0 else 0}
-            if tokenizer:
-                try:
-                    res["input_text"] = tokenizer.decode(r.input_ids, skip_special_tokens=True)
-                    res["output_text"] = tokenizer.decode(r.output_ids, skip_special_tokens=True)
-                except Exception:
-                    res["input_text"] = f"[{len(r.input_ids)} tokens]"
-                    res["output_text"] = f"[{len(r.output_ids)} tokens]"
-            results.append(res)
-        return sorted(results, key=lambda x: x["request_id"])
+    def release_finished(self) -> List[int]:
+        """Free the slots whose request finished; returns those slot ids."""
+        done = [s for s, rid in enumerate(self.slots) if rid is not None and self.requests[rid].finished]
+        for s in done:
+            self.slots[s] = None
+        return done
+
+    def occupied(self) -> List[int]:
+        return [s for s, rid in enumerate(self.slots) if rid is not None]
+
+    def request_in(self, slot: int) -> ServingRequest:
+        return self.requests[self.slots[slot]]
+
+    def any_active(self) -> bool:
+        return any(rid is not None for rid in self.slots)
+
+    def report(self, tokenizer=None) -> List[Dict]:
+        return [r.summary(tokenizer) for r in self.requests if r.finished]

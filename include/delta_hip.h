@@ -291,13 +291,16 @@ int delta_pack_page_indices(const int32_t *slot_block_table, int num_slots,
  * slot_block_table), kv_last_page_len, row_block_table [batch, pages_per_slot]
  * (optional), the subset CSR (subset_indices/subset_indptr, optional) and
  * use_subset[0] = (selective && subset_total > 0 &&
- * full_total / subset_total > compression_ratio) (optional).  The subset CSR
- * holds each row's last min(pages, k) pages when the gate is on and the full
- * CSR when it is off (the reference rebinds the subset lists to the full ones,
- * backend.py:2111-2150), so subset_indices needs batch * pages_per_slot
- * entries.  Rows whose page count would exceed pages_per_slot are clamped. */
-int delta_decode_page_info(const int32_t *cachelens, const int32_t *slot_block_table,
-                           int batch, int pages_per_slot, int k, double compression_ratio,
+ * full_total / subset_total > compression_ratio) (optional), the totals summed
+ * over the rows with active[b] != 0 only (backend.py:2047-2067, 2104-2109:
+ * the reference counts its active rows; active == NULL counts every row).
+ * Idle rows still get their CSR entries.  The subset CSR holds each row's last
+ * min(pages, k) pages when the gate is on and the full CSR when it is off (the
+ * reference rebinds the subset lists to the full ones, backend.py:2111-2150),
+ * so subset_indices needs batch * pages_per_slot entries.  Rows whose page
+ * count would exceed pages_per_slot are clamped (callers bound their rows). */
+int delta_decode_page_info(const int32_t *cachelens, const int32_t *active,
+                           const int32_t *slot_block_table, int batch, int pages_per_slot, int k, double compression_ratio,
                            int selective, int32_t *kv_indptr, int32_t *kv_indices,
                            int32_t *kv_last_page_len, int32_t *row_block_table,
                            int32_t *subset_indices, int32_t *subset_indptr,

@@ -372,6 +372,25 @@ def use_subset_decision(full_total: int, subset_total: int, compression_ratio: f
                 and (full_total / subset_total) > compression_ratio)
 
 
+def decode_step_gate(cachelens, active, k: int, compression_ratio: float,
+                     enable_selective_cache: bool = True, page_size: int = PAGE_SIZE) -> bool:
+    """The decode step's ``use_subset`` decision over its active rows only.
+
+    backend.py:2047-2067 loops over ``active_slots``: each row's ``page_count`` (after
+    ``plan(1, 16)``) goes into ``full_total`` and ``min(page_count, subset_cache_size)``
+    into ``subset_total``; backend.py:2104-2109 then compares their ratio.  Slots with
+    ``active[b] == 0`` take no part.
+    """
+    full_total = subset_total = 0
+    for b in range(len(cachelens)):
+        if int(active[b]) == 0:
+            continue
+        pc = (int(cachelens[b]) + 1) // page_size + 1
+        full_total += pc
+        subset_total += min(pc, int(k))
+    return use_subset_decision(full_total, subset_total, compression_ratio, enable_selective_cache)
+
+
 def append_kv(k: torch.Tensor, v: torch.Tensor, kv_append_indptr: torch.Tensor,
               kv_cache: torch.Tensor, kv_indices: torch.Tensor, kv_indptr: torch.Tensor,
               kv_last_page_len: torch.Tensor) -> None:

@@ -49,7 +49,7 @@ def test_no_undeclared_exports(lib):
 
 
 def test_queries_without_gpu(lib):
-    assert lib.delta_abi_version() == 100
+    assert lib.delta_abi_version() == 200
     assert lib.delta_last_error() == b""
     # split heuristic: deterministic, >= 1; the larger of the attention and the dump plans.
     # Page-major blocks (Hkv heads x R waves = 16) split up to 4096 waves in total, >= 2 pages

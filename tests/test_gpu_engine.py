@@ -16,9 +16,9 @@ DEV = "cuda:0"
 
 
 def make_engine(selective=True, graph=False, B=3, max_len=512, full_layers=(0, 1), k=6, L=2, ratio=1.0,
-                n_layer=None):
+                n_layer=None, **backend_kw):
     from delta_amd.backend import LMBackend
-    eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=graph)
+    eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=graph, **backend_kw)
     eng.load_model("random:tiny-test", seed=1)
     cfg = eng.model.config
     cfg.enable_selective_cache = selective
@@ -110,6 +110,7 @@ def _restore(eng, snap):
         l.attention.kv_cache.kv_cache.copy_(c)
     eng.cachelens.copy_(cl)
     eng.static_tokens.copy_(tok)
+    eng.sync_host_lens()
 
 
 @pytest.mark.parametrize("selective", [True, False])
@@ -150,18 +151,26 @@ def test_partial_batch_idle_slots_untouched():
 
 
 def test_serving_loop_with_prefill():
-    eng = make_engine(B=2, max_len=256, k=4)
+    """Three requests through two slots (prefill, decode, a slot reused): every request gets
+    its full output, every page returns to the pool, and the token streams are identical with
+    the decode steps eager or replayed from the captured graph."""
     prompts = [torch.tensor([1, 2, 3, 4]), torch.tensor([5, 6, 7, 8, 9, 10, 11]), torch.tensor([12] * 20)]
-    for layer in eng.model.layers:
-        layer.attention.record = []
-    eng.add_requests(prompts, [90, 80, 100], [])
-    results = eng.run_scheduler_loop()
-    assert len(results) == 3
-    for r, p, ml in zip(results, prompts, [90, 80, 100]):
-        assert r["output_length"] == ml - len(p)
-    # the very first forward was the 2-row prefill: check it against causal attention
-    q, o = eng.model.layers[0].attention.record[0]
-    assert q.shape[0] == 4 + 7
+    caps = [90, 80, 100]
+    streams = []
+    for graph in (False, True):
+        eng = make_engine(B=2, max_len=256, k=4, graph=graph)
+        eng.add_requests(prompts, caps, [])
+        results = eng.run_scheduler_loop()
+        assert len(results) == 3
+        for r, p, ml in zip(results, prompts, caps):
+            assert r["output_length"] == ml - len(p) and r["status"] == "finished"
+        assert eng.page_pool.available == eng.page_pool.total_pages
+        assert not eng.scheduler.any_active()
+        if graph:
+            assert eng._decode_graph_stats["replays"] > 0 and eng._decode_graph_failed is None
+        streams.append([list(r.generated) for r in eng.scheduler.requests])
+    assert streams[0] == streams[1]
+    assert all(len(s) > 0 for s in streams[0])
 
 
 def test_prefill_rows_are_causal():
@@ -172,9 +181,9 @@ def test_prefill_rows_are_causal():
     eng.add_requests([prompt], [41], [])
     eng.run_scheduler_loop()
     (q, o), = eng.model.layers[0].attention.record[:1]
-    req = eng.scheduler.request_queue[0]
+    req = eng.scheduler.requests[0]
     cache = eng.model.layers[0].attention.kv_cache.kv_cache.cpu()
-    pages = torch.tensor(req.page_indices, dtype=torch.int32)
+    pages = torch.tensor(req.pages, dtype=torch.int32)
     n = 40
     ip = torch.zeros(n + 1, dtype=torch.int32)
     ind, lastl = [], []
@@ -197,18 +206,19 @@ def test_two_row_prefill_step_matches_oracle():
     prompts = [torch.arange(1, 24), torch.arange(30, 39)]
     eng.add_requests(prompts, [60, 60], [])
     with torch.inference_mode():  # the first iteration of run_scheduler_loop
-        new_slots, new_reqs = eng.scheduler.schedule_requests()
-        for slot_id, req in zip(new_slots, new_reqs):
-            req.initialize_pages(slot_id, eng.pages_per_slot)
+        placed = eng.scheduler.fill_free_slots()
+        new_slots = [slot for slot, _ in placed]
+        for slot_id, req in placed:
+            req.admit()
             eng.slot_block_table[slot_id].fill_(int(eng.scratch_pages[slot_id]))
             eng._sync_slot_block_table(slot_id, req, 0)
         eng._forward(1)
     torch.cuda.synchronize()
     (q, o), = eng.model.layers[0].attention.record[:1]
     cache = eng.model.layers[0].attention.kv_cache.kv_cache.cpu()
-    reqs = [eng.scheduler.request_queue[int(eng.scheduler.runner_slots[s])] for s in new_slots]
+    reqs = [eng.scheduler.request_in(s) for s in new_slots]
     lens = [len(p) for p in prompts]
-    pages = [r.page_indices[:(n + 15) // 16] for r, n in zip(reqs, lens)]
+    pages = [r.pages[:(n + 15) // 16] for r, n in zip(reqs, lens)]
     ip = torch.tensor([0, len(pages[0]), len(pages[0]) + len(pages[1])], dtype=torch.int32)
     ind = torch.tensor(pages[0] + pages[1], dtype=torch.int32)
     last = torch.tensor([n - ((n + 15) // 16 - 1) * 16 for n in lens], dtype=torch.int32)
@@ -278,3 +288,98 @@ def test_row_major_gate_up_matches_transposed():
         y_plain = ff(x).float()
     for y in (y_r, y_plain):
         assert (y - y_t).abs().max().item() <= 2e-2 * y_t.abs().max().item()
+
+
+def test_decode_budget_is_enforced_before_the_step():
+    """A decode step that would take a row past the pages its slot holds is refused on the
+    host before anything runs (the device metadata would clamp the row and overwrite its
+    last slot).  Row 2 holds 120 tokens and (120 + 16) // 16 + 1 = 9 pages: 23 more decode
+    steps fit ((120 + 23) // 16 + 1 = 9), the 24th does not."""
+    eng = make_engine(B=3, max_len=512)
+    eng.prepare_synthetic_decode([100, 110, 120], decode_budget=16, seed=2)
+    with pytest.raises(RuntimeError, match="decode budget exhausted: slot 2"):
+        eng.decode_steps(24, use_graph=False)
+    assert eng.cachelens.tolist() == [100, 110, 120]      # nothing ran
+    eng.decode_steps(23, use_graph=False)
+    assert eng.cachelens.tolist() == [123, 133, 143]
+    with pytest.raises(RuntimeError, match="decode budget exhausted"):
+        eng.decode_steps(1, use_graph=False)
+
+
+def test_debug_parity_checks_run_after_eager_and_replayed_steps():
+    """delta_debug_fast_decode_page_info_parity / delta_debug_page_selection_parity (the
+    reference's in-engine checks, backend.py:812-819, 1966-2012) run after every step, eager or
+    replayed, and raise on a table that differs from the host rebuild."""
+    eng = make_engine(B=4, graph=True, delta_debug_fast_decode_page_info_parity=True,
+                      delta_debug_page_selection_parity=True)
+    eng.prepare_synthetic_decode([15, 100, 250, 31], decode_budget=40, seed=8)
+    eng.decode_steps(3, use_graph=False)
+    eng.decode_steps(5, use_graph=True)
+    assert eng._decode_graph_stats["replays"] == 5
+    before = eng.cachelens.clone()
+    eng.decode_steps(1, use_graph=False)
+    eng._debug_check_decode_page_info(before)          # consistent tables pass
+    with torch.inference_mode():
+        eng.page_selector.paged_kv_indices[3] += 1
+    with pytest.raises(RuntimeError, match="page-info mismatch in paged_kv_indices"):
+        eng._debug_check_decode_page_info(before)
+    # a partial batch near the gate's threshold: row 0 alone has 8 pages, 8 / min(8, 4) = 2 >
+    # 1.8 (on); counting the 3 idle slots' pages would give 11 / 7 = 1.57 (off)
+    eng2 = make_engine(B=4, ratio=1.8, k=4, delta_debug_fast_decode_page_info_parity=True,
+                       delta_debug_page_selection_parity=True)
+    eng2.prepare_synthetic_decode([119, 300, 300, 300], decode_budget=16, seed=9)
+    with torch.inference_mode():
+        eng2.active.copy_(torch.tensor([1, 0, 0, 0], dtype=torch.int32))
+        eng2.cachelens.copy_(torch.tensor([119, 0, 0, 0], dtype=torch.int32))
+    eng2.sync_host_lens()
+    eng2.decode_steps(2, use_graph=False)
+    assert int(eng2.use_subset_flag) == 1
+
+
+def test_replay_failure_falls_back_to_eager():
+    """A failing graph replay is counted and the step runs eagerly (backend.py:1172-1181)."""
+    eng = make_engine(B=3, graph=True)
+    eng.prepare_synthetic_decode([50, 60, 70], decode_budget=16, seed=10)
+    snap = _snapshot(eng)
+    want = eng.decode_steps(2, use_graph=False).clone()
+    _restore(eng, snap)
+    eng.decode_steps(1, use_graph=True)                 # captures, then replays once
+
+    class _Broken:
+        def replay(self):
+            raise RuntimeError("replay refused")
+
+    eng._decode_graph = _Broken()
+    got = eng.decode_steps(1, use_graph=True).clone()
+    assert torch.equal(got, want)
+    assert eng._decode_graph_stats["replay_failures"] == 1 and eng._decode_graph is None
+    assert "replay refused" in eng._decode_graph_failed
+    assert eng.cachelens.tolist() == [52, 62, 72]
+
+
+def test_page_scores_from_attention_buffer_api():
+    """LMBackend._compute_page_scores_from_attention_buffer (backend.py:911-913) returns the
+    last planner step's del3_legacy_softmax scores: equal to the oracle's from the same dump
+    within 1e-4 relative, and to the two-pass reference route."""
+    eng = make_engine(B=3)
+    eng.prepare_synthetic_decode([100, 257, 400], decode_budget=16, seed=11)
+    eng.decode_steps(1, use_graph=False)
+    torch.cuda.synchronize()
+    B, mp = eng.batch_size, eng.pages_per_slot
+    got = eng._compute_page_scores_from_attention_buffer().clone().cpu().double()
+    ref_route = eng._compute_page_scores_reference().cpu().double()
+    ip = eng.page_selector.paged_kv_indptr[:B + 1].cpu()
+    last = eng.page_selector.paged_kv_last_page_len[:B].cpu()
+    lens = O.kv_lengths(ip, last).tolist()
+    logits = eng.dump.cpu().double().clone()
+    for b in range(B):
+        logits[b, :, lens[b]:] = float("-inf")
+    want = O.legacy_softmax_page_scores(logits, B, mp, compute_dtype=torch.float64).double()
+    assert got.shape == (B, mp)
+    rel = ((got - want).abs() / want.abs().clamp_min(1e-30)).max().item()
+    assert rel < 1e-4, rel
+    assert ((ref_route - got).abs() / got.abs().clamp_min(1e-30)).max().item() < 1e-4
+    # a row's pages past its end score 0
+    pages = (ip[1:] - ip[:-1]).tolist()
+    for b in range(B):
+        assert got[b, pages[b]:].abs().max().item() == 0.0

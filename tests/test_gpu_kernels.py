@@ -356,6 +356,39 @@ def test_decode_page_info():
     assert torch.equal(sub_i[:want_ip[-1]], ind[:want_ip[-1]])
 
 
+@pytest.mark.parametrize("active_rows", [[0, 1, 2, 3], [3, 10, 17, 30], list(range(32))])
+def test_decode_page_info_gate_counts_active_rows(active_rows):
+    """Partial batches near the gate's threshold: the device gate sums page totals over the
+    active rows only, as the reference does (backend.py:2047-2067, 2104-2109)."""
+    B, pps, k = 32, 4100, 256
+    gen = torch.Generator().manual_seed(9)
+    cachelens = torch.zeros(B, dtype=torch.int32)
+    active = torch.zeros(B, dtype=torch.int32)
+    for r in active_rows:
+        cachelens[r] = 65536          # 4097 pages after the decode token
+        active[r] = 1
+    slot_bt = torch.randint(0, 1 << 20, (B, pps), generator=gen, dtype=torch.int32).to(DEV)
+    ind = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    ip = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    last = torch.zeros(B, dtype=torch.int32, device=DEV)
+    sub_i = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    sub_p = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    flag = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    for ratio in (15.9, 16.0, 16.0039, 16.004, 16.5):
+        for act in (active, None):
+            K.decode_page_info(cachelens.to(DEV), slot_bt, B, k, ratio, True, ip, ind, last, None, sub_i, sub_p,
+                               flag, active=None if act is None else act.to(DEV))
+            torch.cuda.synchronize()
+            want = O.decode_step_gate(cachelens.tolist(), [1] * B if act is None else act.tolist(), k, ratio)
+            assert int(flag) == int(want), (active_rows, ratio, act is None)
+            # the CSR covers every slot either way; the subset CSR follows the gate
+            pc = [(int(c) + 1) // 16 + 1 for c in cachelens]
+            want_ip = [0] + torch.cumsum(torch.tensor(pc), 0).tolist()
+            assert ip.cpu().tolist() == want_ip
+            sc = [min(n, k) if want else n for n in pc]
+            assert sub_p.cpu().tolist() == [0] + torch.cumsum(torch.tensor(sc), 0).tolist()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_append_kv(dtype):
     c = make_case(batch=3, hq=8, hkv=4, kv_lens=[17, 32, 50], seed=9, dtype=dtype, trailing_empty_page=True)

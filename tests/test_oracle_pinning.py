@@ -64,6 +64,23 @@ def test_use_subset_gate():
     assert not O.use_subset_decision(100, 20, 1.0, enable_selective_cache=False)
 
 
+def test_decode_step_gate_counts_active_rows_only():
+    """4 active rows of 4097 pages (kv_len 65537), k = 256, ratio 16, 28 idle slots: the
+    totals are 4 * 4097 = 16388 and 4 * 256 = 1024, 16388 / 1024 = 16.0039 > 16, so the
+    subset is on; counting each idle slot's one page would give 16416 / 1052 = 15.6 (off)."""
+    B = 32
+    cl = [65536] * 4 + [0] * (B - 4)
+    act = [1] * 4 + [0] * (B - 4)
+    assert O.decode_step_gate(cl, act, 256, 16.0)
+    assert not O.decode_step_gate(cl, [1] * B, 256, 16.0)   # idle slots counted: 15.6
+    assert not O.decode_step_gate(cl, act, 256, 16.004)      # just above 16.0039
+    assert not O.decode_step_gate(cl, [0] * B, 256, 0.0)     # nothing active: subset_total 0
+    assert not O.decode_step_gate(cl, act, 256, 1.0, enable_selective_cache=False)
+    # the per-row count is Request.plan's: kv_len // 16 + 1 pages
+    assert O.decode_step_gate([15], [1], 1, 1.5)             # 16 tokens -> 2 pages, 2 / 1 > 1.5
+    assert not O.decode_step_gate([14], [1], 1, 1.5)         # 15 tokens -> 1 page
+
+
 # ---------------------------------------------------------------- dump logits
 
 def test_dump_logits_bruteforce():

@@ -294,14 +294,15 @@ def test_decode_budget_is_enforced_before_the_step():
     """A decode step that would take a row past the pages its slot holds is refused on the
     host before anything runs (the device metadata would clamp the row and overwrite its
     last slot).  Row 2 holds 120 tokens and (120 + 16) // 16 + 1 = 9 pages: 23 more decode
-    steps fit ((120 + 23) // 16 + 1 = 9), the 24th does not."""
+    steps fit ((120 + 23) // 16 + 1 = 9), the 24th does not; rows 0 and 1 (96 tokens, 8 pages)
+    have room for 31."""
     eng = make_engine(B=3, max_len=512)
-    eng.prepare_synthetic_decode([100, 110, 120], decode_budget=16, seed=2)
+    eng.prepare_synthetic_decode([96, 96, 120], decode_budget=16, seed=2)
     with pytest.raises(RuntimeError, match="decode budget exhausted: slot 2"):
         eng.decode_steps(24, use_graph=False)
-    assert eng.cachelens.tolist() == [100, 110, 120]      # nothing ran
+    assert eng.cachelens.tolist() == [96, 96, 120]        # nothing ran
     eng.decode_steps(23, use_graph=False)
-    assert eng.cachelens.tolist() == [123, 133, 143]
+    assert eng.cachelens.tolist() == [119, 119, 143]
     with pytest.raises(RuntimeError, match="decode budget exhausted"):
         eng.decode_steps(1, use_graph=False)
 

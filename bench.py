@@ -158,7 +158,7 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
     256 MB MALL by the previous one."""
     from delta_amd import kernels as K
     from delta_amd.workloads import make_case
-    layers = []
+    layers, appends = [], []
     for seed in range(n_rot):
         c = make_case(batch=BATCH, hq=32, hkv=8, kv_lens=CONTEXT, dtype=torch.bfloat16, seed=seed,
                       page_order="shuffle", k=BUDGET_PAGES, L=L_LAST, device="cuda:0")
@@ -171,6 +171,14 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
         scores = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
         idx, ip = K.select_pages(scores, c.kv_indptr, c.block_table, c.k, c.L)
         layers.append((c, dump, lse, scores, idx, ip))
+        # the decode token's (k, v) and position for the fused RoPE + append launches the step makes
+        hkv_ = c.kv_cache.shape[3]
+        g = torch.Generator(device="cuda:0").manual_seed(100 + seed)
+        appends.append(K.DecodeAppend(
+            torch.randn((B, hkv_, 128), generator=g, device="cuda:0").to(torch.bfloat16),
+            torch.randn((B, hkv_, 128), generator=g, device="cuda:0").to(torch.bfloat16),
+            torch.tensor([n - 1 for n in c.kv_lens], dtype=torch.int32, device="cuda:0"),
+            c.kv_indptr, c.kv_indices, rope_scale=1.0, rope_theta=500000.0))
     torch.cuda.synchronize()
     c = layers[0][0]
     B, hq = c.q.shape[:2]
@@ -186,12 +194,30 @@ def kernel_roofline(torch, reps: int = 48, n_rot: int = 4):
     def timed(fn):
         return graph_timed(torch, [lambda i=i: fn(*layers[i % n_rot]) for i in range(reps)], n_rot)
 
+    def timed_ap(fn):
+        return graph_timed(torch, [lambda i=i: fn(*layers[i % n_rot], appends[i % n_rot]) for i in range(reps)],
+                           n_rot)
+
     res = {}
 
     def add(name, us, nbytes, note):
         res[name] = {"us": round(us, 2), "bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
                      "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "what": note}
 
+    # the fused launches also read the token's k and v and write them into its cache slot
+    ap_bytes = 2 * 2 * B * hkv * 128 * esz + 2 * B * 4
+    add("paged_decode_subset_kernel<ROPE>",
+        timed_ap(lambda c, d, l, s, i, p, a: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
+                                                             max_pages_per_row=c.k, subset=True, append=a)),
+        ntok_sub * 2 * row_kv + qo + B * c.k * 4 + ap_bytes,
+        "the launch a decode step makes in each selective layer (delta_paged_decode_subset_append): "
+        "K+V of the 128 selected pages/row, q, o, page ids, the token's k/v read and appended")
+    add("paged_decode_plan_kernel<ROPE>",
+        timed_ap(lambda c, d, l, s, i, p, a: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                             c.kv_last_page_len, max_pages_per_row=mp, lse=l,
+                                                             logits_dump=d, append=a)),
+        ntok_full * 2 * row_kv + qo + B * mp * 4 + ntok_full * hq * 4 + ap_bytes,
+        "the planner launch of a decode step (delta_paged_decode_append with a dump)")
     add("paged_decode_subset_kernel",
         timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
                                                        max_pages_per_row=c.k, subset=True)),
@@ -356,46 +382,92 @@ def copy_calibration(torch, mib: int = 256, reps: int = 8):
             "what": f"torch bf16 copy of {mib} MiB (read + write)"}
 
 
-def cpu_baseline(torch, sample_rows: int = 2):
-    """Oracle (PyTorch CPU, fp32) timing of the same step, composed from per-op timings.
+def cpu_model_name() -> str:
+    """The host CPU's model string (/proc/cpuinfo; lscpu's "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    Attention ops run on ``sample_rows`` rows of the config-3 layer and are scaled to the
-    batch; the dense decoder layer (GEMMs, norms) and lm_head run at the full batch with
-    random fp32 weights.  Step = 2 full layers (one of them the planner with dump, score,
-    selection) + 30 subset layers + 32 dense layers + lm_head."""
-    from delta_amd.workloads import make_case
+
+def _median_time(fn, warm: int = 2, reps: int = 5) -> float:
+    """Seconds: median of ``reps`` timed calls after ``warm`` untimed ones."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _cpu_layer_ops(torch, c, rows=None):
+    """Per-op oracle timings (fp32 on the host) of one layer case, in seconds for the rows of
+    ``c``: planner scorer (logits dump + del3_legacy_softmax scores), v2 selector, sparse decode
+    attention over the selection, full decode attention.  Per-row budgets select row by row."""
+    from oracle import delta_oracle as O
+    f32 = torch.float32
+    q = c.q.float()
+    cache = c.kv_cache.float()
+    scale = 1 / math.sqrt(128)
+    B = q.shape[0]
+    mp = c.max_pages
+    counts = c.kv_indptr[1:] - c.kv_indptr[:-1]
+
+    def score():
+        x = O.dump_logits(q, cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, scale, mp * 16,
+                          compute_dtype=f32)
+        return O.legacy_softmax_page_scores(x, B, mp)
+
+    scores = score()
+
+    def select():
+        if c.k_per_row is None:
+            return O.select_pages(scores, counts, c.block_table, c.k, c.L)
+        idx, ip = [], [0]
+        for b in range(B):
+            i, _ = O.select_pages(scores[b:b + 1], counts[b:b + 1], c.block_table[b:b + 1], int(c.k_per_row[b]),
+                                  c.L)
+            idx.append(i)
+            ip.append(ip[-1] + i.numel())
+        return torch.cat(idx), torch.tensor(ip, dtype=torch.int32)
+
+    idx, ip = select()
+    t = {"scorer": _median_time(score), "selector": _median_time(select),
+         "sparse_layer": _median_time(lambda: O.paged_decode_attention(q, cache, ip, idx, c.kv_last_page_len,
+                                                                       scale, compute_dtype=f32)),
+         "full_layer": _median_time(lambda: O.paged_decode_attention(q, cache, c.kv_indptr, c.kv_indices,
+                                                                     c.kv_last_page_len, scale, compute_dtype=f32))}
+    return t
+
+
+def cpu_baseline(torch, sample_rows: int = 2):
+    """The oracle's PyTorch-CPU restatement of the same math (fp32, bf16/fp16 inputs upcast
+    exactly), timed on this host's cores: 2 warm-ups, then the median of 5.
+
+    ``value``: config 3 decode-step tokens/s, composed from per-op timings of ``sample_rows``
+    rows of the config-3 layer (scaled to the batch) plus the dense decoder layer and lm_head at
+    the full batch with random fp32 weights: 2 full layers (one the planner, with its dump,
+    score and selection) + 30 subset layers + 32 dense layers + lm_head.  ``per_op`` holds the
+    per-op timings at every config's real shape (configs 4 and 5 on sampled rows, scaled by
+    their share of the cached tokens) and the whole selective step of configs 1 and 2 (no
+    sampling)."""
+    from delta_amd.workloads import config_case, make_case
     from oracle import delta_oracle as O
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-
-    def med(fn, reps=3):
-        fn()
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return statistics.median(ts)
+    t_start = time.perf_counter()
 
     c = make_case(batch=sample_rows, hq=32, hkv=8, kv_lens=CONTEXT, dtype=torch.float32, seed=0,
                   page_order="shuffle", k=BUDGET_PAGES, L=L_LAST)
-    scale = 1 / math.sqrt(128)
-    mp = c.max_pages
-    f32 = torch.float32
-    t_full = med(lambda: O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
-                                                  c.kv_last_page_len, scale, compute_dtype=f32))
-
-    def plan():
-        x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, scale, mp * 16,
-                          compute_dtype=f32)
-        s = O.legacy_softmax_page_scores(x, sample_rows, mp)
-        return O.select_pages(s, c.kv_indptr[1:] - c.kv_indptr[:-1], c.block_table, c.k, c.L)
-
-    t_plan = med(plan)
-    idx, ip = plan()
-    t_sub = med(lambda: O.paged_decode_attention(c.q, c.kv_cache, ip, idx, c.kv_last_page_len, scale,
-                                                 compute_dtype=f32))
-    per_row = (t_full + (t_full + t_plan) + 30 * t_sub) / sample_rows
+    ops3 = _cpu_layer_ops(torch, c)
+    per_row = (ops3["full_layer"] + (ops3["full_layer"] + ops3["scorer"] + ops3["selector"])
+               + 30 * ops3["sparse_layer"]) / sample_rows
     dim, inter, vocab = 4096, 14336, 128256
     g = torch.Generator().manual_seed(0)
     w = {n: torch.randn(shape, generator=g) * 0.02 for n, shape in
@@ -410,19 +482,47 @@ def cpu_baseline(torch, sample_rows: int = 2):
         hn = y * torch.rsqrt((y * y).mean(-1, keepdim=True) + 1e-5)
         return y + (torch.nn.functional.silu(hn @ w["w1"].T) * (hn @ w["w3"].T)) @ w["w2"].T
 
-    t_dense = med(dense)
+    t_dense = _median_time(dense)
     del w
     lm = torch.randn(vocab, dim, generator=g) * 0.02
-    t_head = med(lambda: (x @ lm.T).argmax(-1))
+    t_head = _median_time(lambda: (x @ lm.T).argmax(-1))
     del lm
     step = BATCH * per_row + 32 * t_dense + t_head
+    ms = lambda d: {k: round(v * 1e3, 2) for k, v in d.items()}
+    per_op = {"config3": {"ms": ms({k: v * BATCH / sample_rows for k, v in ops3.items()}),
+                          "rows_timed": sample_rows, "rows": BATCH}}
+    # configs 1 and 2: the whole selective step of the layer (score, select, sparse attention), all rows
+    for cfg in (1, 2):
+        cc = config_case(cfg)
+        o = _cpu_layer_ops(torch, cc)
+        per_op[f"config{cfg}"] = {"ms": ms(o), "rows_timed": cc.batch, "rows": cc.batch,
+                                  "selective_step_ms": round((o["scorer"] + o["selector"] + o["sparse_layer"]) * 1e3,
+                                                             2)}
+        del cc
+    # configs 4 and 5 on sampled rows, scaled by the cached tokens they cover
+    for cfg, rows in ((4, 1), (5, 2)):
+        cc = config_case(cfg, batch=rows)
+        o = _cpu_layer_ops(torch, cc)
+        total_rows = 4 if cfg == 4 else 128
+        if cfg == 5:
+            import random as _r
+            rng = _r.Random(0)
+            all_lens = [rng.randint(1024, 32768) for _ in range(total_rows)]
+            share = sum(all_lens) / sum(cc.kv_lens)
+        else:
+            share = total_rows / rows
+        per_op[f"config{cfg}"] = {"ms": ms({k: v * share for k, v in o.items()}), "rows_timed": rows,
+                                  "rows": total_rows, "scaled_by": round(share, 3)}
+        del cc
     return {"value": round(BATCH / step, 3), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": (f"oracle fp32 on {sample_rows} of {BATCH} rows of the config-3 layer (8192 tokens, "
-                       f"128-page budget), scaled to the batch: full {t_full * 1e3:.1f} ms, planner extra "
-                       f"{t_plan * 1e3:.1f} ms, subset {t_sub * 1e3:.1f} ms per {sample_rows} rows; dense layer "
-                       f"{t_dense * 1e3:.1f} ms and lm_head {t_head * 1e3:.1f} ms at batch {BATCH}; "
-                       f"composed step {step:.2f} s")}
+            "cpu_model": cpu_model_name(), "kind": "port",
+            "sample": (f"oracle fp32 (PyTorch CPU), 2 warm-ups + median of 5 per op; config 3 step composed from "
+                       f"{sample_rows} of {BATCH} rows of the layer scaled to the batch (full "
+                       f"{ops3['full_layer'] * 1e3:.1f} ms, scorer {ops3['scorer'] * 1e3:.1f} ms, selector "
+                       f"{ops3['selector'] * 1e3:.1f} ms, subset {ops3['sparse_layer'] * 1e3:.1f} ms per "
+                       f"{sample_rows} rows), dense layer {t_dense * 1e3:.1f} ms and lm_head {t_head * 1e3:.1f} ms "
+                       f"at batch {BATCH}: composed step {step:.2f} s"),
+            "per_op": per_op, "wall_s": round(time.perf_counter() - t_start, 1)}
 
 
 def main():
@@ -439,6 +539,8 @@ def main():
     ap.add_argument("--engine-config4-only", action="store_true",
                     help="only the config-4 decode step (selective and full cache; for kernel traces)")
     ap.add_argument("--kernel-reps", type=int, default=48)
+    ap.add_argument("--cpu-baseline-only", action="store_true",
+                    help="only the CPU baseline (runs without a GPU)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel roofline loop and a copy of known size (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -448,6 +550,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.cpu_baseline_only:
+        print(json.dumps({"cpu_baseline": cpu_baseline(torch)}), flush=True)
+        return
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
@@ -490,7 +595,7 @@ def main():
     kern = kernel_roofline(torch, args.kernel_reps)
     for k, v in kern.items():
         log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s ({100 * v['frac']:.1f}% of peak)")
-    dom = kern["paged_decode_subset_kernel"]
+    dom = kern["paged_decode_subset_kernel<ROPE>"]  # the launch each selective layer of a step makes
     log("prefill kernel")
     prefill = prefill_roofline(torch)
     log(f"  paged_prefill_kernel: {prefill['us']} us, {prefill['TFLOP_s']} TFLOP/s "
@@ -543,8 +648,10 @@ def main():
                                "2048-token budget (128 pages, L=8), full layers [0,1], one hipGraph per step",
                    "batch": BATCH, "context": CONTEXT, "budget_pages": BUDGET_PAGES, "page_size": 16},
         "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": dom["frac"], "traffic": profiled_traffic("paged_decode_subset_kernel"),
-                     "algorithmic_bytes": dom["bytes"], "kernel": "paged_decode_subset_kernel"},
+                     "frac": dom["frac"], "traffic": profiled_traffic("paged_decode_subset_kernel<ROPE>"),
+                     "algorithmic_bytes": dom["bytes"],
+                     "kernel": "paged_decode_subset_kernel<ROPE> (delta_paged_decode_subset_append, the launch "
+                               "of every selective layer in a decode step)"},
         "cpu_baseline": cpu,
         "full_cache": full,
         "speedup_vs_full_cache": round(tok_s / full["tokens_per_s"], 3) if full else None,

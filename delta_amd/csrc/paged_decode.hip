@@ -176,6 +176,17 @@ constexpr int tokmax_lds_header() {
   return kMaxWaves * G * 2 + 16;
 }
 
+// The fused append's per-wave token slots (ROPE), in floats from the start of the dynamic LDS:
+// past the V tiles and the merge area (attention launches) or past the larger of the merge
+// area and the V tiles plus the dump staging (planner launches).
+template <int G, bool WITH_V, bool WITH_DUMP>
+__host__ __device__ constexpr int rope_lds_offset(int nw) {
+  return WITH_DUMP ? (nw * G * (2 + kHeadDim) > nw * kVTile / 2 + nw * dump_slots<G, WITH_V>() * G * kPageSize
+                          ? nw * G * (2 + kHeadDim)
+                          : nw * kVTile / 2 + nw * dump_slots<G, WITH_V>() * G * kPageSize)
+                   : nw * kVTile / 2 + nw * G * (2 + kHeadDim);
+}
+
 // max / sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950 permlane swaps.
 __device__ __forceinline__ float rows4_max(float v) {
   auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -258,22 +269,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     qf[0] = qf[1] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  // Fused RoPE + append of the row's new token (ROPE), done before the page stream starts: its
-  // few dependent loads (position, the token's k and v, the append slot's page id) then do not
-  // queue behind the page loads (measured: 2 us faster than after the first page's loads).
+  // Fused RoPE + append of the row's new token (ROPE), with no block barrier: every wave
+  // loads the token's k and v pair `lane` of its kv head, its position and the append slot
+  // before the page stream starts (independent of it); while the wave's page ids load,
+  // lane i computes pair i's (cos, sin), rotates q (ds_bpermute hands each lane the
+  // pairs of its fragments) and k, and keeps the rotated k and the v in an LDS slot of the
+  // wave's own, from which the wave that attends the token's page takes that row.  The cache
+  // slot is written at the end of the kernel: no wave reads it.
   int ap_pid = -1, ap_slot = 0;
   uint32_t kraw = 0u, vraw = 0u;
   float rpos = 0.f;
   if (ROPE) {
-    const int i = threadIdx.x;
-    if (i < hb * (kHeadDim / 2)) {
-      const int64_t e = (int64_t)(head0 + (i >> 6)) * kHeadDim + 2 * (i & 63);
-      kraw = *reinterpret_cast<const uint32_t *>(a.k_new + (int64_t)b * a.k_new_stride + e);
-      vraw = *reinterpret_cast<const uint32_t *>(a.v_new + (int64_t)b * a.v_new_stride + e);
-    }
+    kraw = reinterpret_cast<const uint32_t *>(a.k_new + (int64_t)b * a.k_new_stride + (int64_t)h * kHeadDim)[lane];
+    vraw = reinterpret_cast<const uint32_t *>(a.v_new + (int64_t)b * a.v_new_stride + (int64_t)h * kHeadDim)[lane];
     rpos = (float)a.offsets[b];
     // The append slot, with delta_append_kv's checks (a row without a valid slot appends
-    // nothing); the page id is checked where it is first needed.
+    // nothing).
     const int64_t q0 = a.ap_indptr[b], q1 = a.ap_indptr[b + 1];
     if (q0 >= 0 && q1 > q0 && q1 <= a.ap_indices_len) {
       int lp = a.last_page_len[b];
@@ -285,43 +296,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       }
     }
   }
-
-  // The token's (cos, sin) table, its rotated k and its v for the block's hb heads go to LDS
-  // past the V tiles and the dump staging; q is rotated in registers; one block per (row, kv
-  // head group) writes k and v into the cache slot, and the wave that attends that page takes
-  // the token's K and V from LDS (whatever the cache held there when the page was read).  Same
-  // rounding as delta_rope_append.
-  const int rope_off = (WITH_V ? nw * kVTile / 2 : 0) + (WITH_DUMP ? nw * dump_slots<G, WITH_V>() * G * kPageSize : 0);
-  float *const rtab = smem + rope_off;                                              // [64][cos, sin]
-  uint32_t *const knew = reinterpret_cast<uint32_t *>(smem + rope_off + kHeadDim);  // [hb][64] rotated k pairs
-  uint32_t *const vnew = knew + hb * (kHeadDim / 2);                                // [hb][64] v pairs
-  if (ROPE) {
-    const int i = threadIdx.x;
-    if (ap_pid >= (int64_t)a.num_pages) ap_pid = -1;
-    if (i < kHeadDim / 2) rope_cos_sin(i, rpos, a.rcp_scale, a.log2_theta, a.smooth_a, a.smooth_b, rtab + 2 * i);
-    __syncthreads();
-    if (i < hb * (kHeadDim / 2)) {
-      knew[i] = rope_rotate<DT>(kraw, rtab + 2 * (i & 63));
-      vnew[i] = vraw;
-    }
-    if ((t & 7) < G) {
-#pragma unroll
-      for (int sp = 0; sp < 2; ++sp)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) qf[sp][w] = rope_rotate<DT>(qf[sp][w], rtab + 2 * (32 * sp + 16 * (t >> 3) + 4 * c + w));
-    }
-    __syncthreads();
-    if (ap_pid >= 0 && (a.nsplit == 1 || split == 0)) {
-      for (int ch = threadIdx.x; ch < 2 * hb * (kHeadDim / 8); ch += blockDim.x) {
-        const int which = ch >= hb * (kHeadDim / 8);  // 0 = K, 1 = V
-        const int r = which ? ch - hb * (kHeadDim / 8) : ch;
-        const uint32_t *src = (which ? vnew : knew) + 4 * r;  // head r / 16, 16-byte chunk r % 16
-        uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
-                        (int64_t)head0 * kHeadDim + 8 * r;
-        st128(dst, *reinterpret_cast<const u32x4 *>(src));
-      }
-    }
-  }
+  // This wave's LDS slot for the token: [64] rotated k pairs, then [64] v pairs.
+  uint32_t *const tok_lds = reinterpret_cast<uint32_t *>(smem + rope_lds_offset<G, WITH_V, WITH_DUMP>(nw)) +
+                            wave * kHeadDim;
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
@@ -394,6 +371,28 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   };
 
   int ids = count > 0 ? load_ids(0) : -1;
+  // RoPE while the wave's page ids are in flight (the token's k and v registers die before
+  // the page stream starts): lane i holds pair i's (cos, sin); q pair 32 sp + 16 (t / 8) +
+  // 4c + w sits in qf[sp][w] (zero for heads past the group).
+  if (ROPE) {
+    if (ap_pid >= (int64_t)a.num_pages) ap_pid = -1;
+    float cs_sn[2];
+    rope_cos_sin(lane, rpos, a.rcp_scale, a.log2_theta, a.smooth_a, a.smooth_b, cs_sn);
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int j = 32 * sp + 16 * (t >> 3) + 4 * c + w;
+        const float cw[2] = {shfl(cs_sn[0], j), shfl(cs_sn[1], j)};
+        qf[sp][w] = rope_rotate<DT>(qf[sp][w], cw);
+      }
+    tok_lds[lane] = rope_rotate<DT>(kraw, cs_sn);
+    tok_lds[kHeadDim / 2 + lane] = vraw;
+    // Only this wave reads the slot back, in order after these stores.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   int pid = __builtin_amdgcn_readlane(ids, 0);
   u32x4 kf[4], vf[4];
   if (count > 0) {
@@ -418,19 +417,19 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       const int pidn = it + 1 < cn ? __builtin_amdgcn_readlane(ids, it + 1) : __builtin_amdgcn_readlane(ids_next, 0);
       const uint16_t *nbase = page_ptr(pidn);
       if (ROPE && ok && pid == ap_pid) {
-        // The new token's row of this page: K lanes with t / 2 == slot % 8 in steps
-        // 2 (slot / 8) + sp, V lanes with c == slot % 4 in tile row group slot / 4.
-        const int hl = h - head0;
+        // The new token's row of this page (a wave-uniform branch, taken once): K lanes with
+        // t / 2 == slot % 8 in steps 2 (slot / 8) + sp, V lanes with c == slot % 4 in tile row
+        // group slot / 4.
         if ((t >> 1) == (ap_slot & 7)) {
 #pragma unroll
           for (int s = 0; s < 4; ++s)
             if ((s >> 1) == (ap_slot >> 3))
-              kf[s] = *reinterpret_cast<const u32x4 *>(knew + hl * (kHeadDim / 2) + 32 * (s & 1) + 16 * (t & 1) + 4 * c);
+              kf[s] = *reinterpret_cast<const u32x4 *>(tok_lds + 32 * (s & 1) + 16 * (t & 1) + 4 * c);
         }
         if (WITH_V && c == (ap_slot & 3)) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (i == (ap_slot >> 2)) vf[i] = *reinterpret_cast<const u32x4 *>(vnew + hl * (kHeadDim / 2) + 4 * t);
+            if (i == (ap_slot >> 2)) vf[i] = *reinterpret_cast<const u32x4 *>(tok_lds + kHeadDim / 2 + 4 * t);
         }
       }
 
@@ -534,10 +533,10 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   }
 
   // Merge the block's waves in LDS.  Attention launches have a merge area of their own past
-  // the V tiles (and the append's LDS), so each wave stores its (m, l, acc) as soon as it
-  // leaves the loop; the dump launches reuse the V tiles' space once every wave left it.
+  // the V tiles, so each wave stores its (m, l, acc) as soon as it leaves the loop; the dump
+  // launches reuse the V tiles' space once every wave left it.
   constexpr bool kOwnMerge = WITH_V && !WITH_DUMP;
-  float *const s_ml = smem + (kOwnMerge ? rope_off + (ROPE ? kHeadDim + hb * kHeadDim : 0) : 0);  // [nw][G][2]
+  float *const s_ml = smem + (kOwnMerge ? nw * kVTile / 2 : 0);  // [nw][G][2]
   float *const s_acc = s_ml + nw * G * 2;                                                          // [nw][G][128]
   if (!kOwnMerge) __syncthreads();
   if (c == 0 && t < G) {
@@ -610,6 +609,20 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         a.part_ml[pidx * 2 + 0] = M;
         a.part_ml[pidx * 2 + 1] = L;
       }
+    }
+  }
+  if (ROPE && ap_pid >= 0 && (a.nsplit == 1 || split == 0)) {
+    // One block per (row, kv head group) writes the new token's rotated k and v into the cache
+    // slot, 16-byte chunk r % 16 of head head0 + r / 16, from the LDS slot of wave r / 16 (which
+    // works on that head); the merge's barrier above ordered those LDS stores.
+    for (int ch = threadIdx.x; ch < 2 * hb * (kHeadDim / 8); ch += blockDim.x) {
+      const int which = ch >= hb * (kHeadDim / 8);  // 0 = K, 1 = V
+      const int r = which ? ch - hb * (kHeadDim / 8) : ch;
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(smem + rope_lds_offset<G, WITH_V, WITH_DUMP>(nw)) +
+                            (r >> 4) * kHeadDim + which * (kHeadDim / 2) + 4 * (r & 15);
+      uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
+                      (int64_t)(head0 + (r >> 4)) * kHeadDim + 8 * (r & 15);
+      st128(dst, *reinterpret_cast<const u32x4 *>(src));
     }
   }
   if (TOKMAX) {
@@ -747,11 +760,14 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
   const size_t tiles = (size_t)waves * kVTile * sizeof(uint16_t);
   const size_t dumps = (size_t)waves * dump_slots<G, true>() * G * kPageSize * sizeof(float);
   const size_t dumps_score = (size_t)waves * dump_slots<G, false>() * G * kPageSize * sizeof(float);
-  // The fused append's LDS (past the tiles and the dump staging): the (cos, sin) table, then
-  // the rotated k and the v of the block's heads.
-  const size_t rope_lds = rope ? (size_t)(kHeadDim + a.hb * kHeadDim) * sizeof(float) : 0;
-  const size_t sm_attn = tiles + rope_lds + merge;  // own merge area past the tiles
-  const size_t sm_plan = merge > tiles + dumps + rope_lds ? merge : tiles + dumps + rope_lds;
+  // Attention launches: V tiles, then their own merge area; planner launches: the merge reuses
+  // the V tiles and the dump staging.  The fused append's token slots (512 bytes per wave) sit
+  // past everything else, at rope_lds_offset.
+  const size_t rope_lds = (size_t)waves * kHeadDim * sizeof(uint32_t);
+  const size_t sm_attn = rope ? (size_t)rope_lds_offset<G, true, false>(waves) * sizeof(float) + rope_lds
+                              : tiles + merge;
+  const size_t sm_plan = rope ? (size_t)rope_lds_offset<G, true, true>(waves) * sizeof(float) + rope_lds
+                              : (merge > tiles + dumps ? merge : tiles + dumps);
   const size_t sm_score = dumps_score > (size_t)waves * G * 2 * sizeof(float) ? dumps_score : (size_t)waves * G * 2 * sizeof(float);
   switch (mode) {
     case kAttn:

@@ -384,3 +384,106 @@ def test_page_scores_from_attention_buffer_api():
     pages = (ip[1:] - ip[:-1]).tolist()
     for b in range(B):
         assert got[b, pages[b]:].abs().max().item() == 0.0
+
+
+def test_config3_llama3_8b_engine_step_matches_oracle():
+    """The benchmark's own workload: Llama-3-8B shape (32 layers, 32 q / 8 kv heads), B = 32,
+    8192-token context, 128-page budget, L = 8, layers 0-1 full (layer 1 the planner).  One
+    recorded eager step is checked on sampled rows against the oracle, reading each layer's
+    own cache after the step: layer 0's full attention; layer 1's full attention and its page
+    selection (the oracle's own chain from the same rotated q and cache; a page may differ only
+    within twice the row's measured score error of the k-th key); layers 2 and 31's subset
+    attention over the step's subset CSR.  Then the same step replayed from a captured graph,
+    from the same state, equals the eager step bit for bit: tokens, selection, appended K/V
+    (backend.py:1449-1478, model.py:177-196)."""
+    import math
+    from delta_amd import ops
+    from delta_amd.backend import LMBackend
+    B, ctx, k, L = 32, 8192, 128, 8
+    scale = 1 / math.sqrt(128)
+    eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=True)
+    eng.load_model("random:llama-3-8b", seed=0)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = [0, 1]
+    cfg.subset_cache_size = k
+    cfg.compression_ratio = 1.0
+    cfg.L = L
+    eng.setup_caches(max_batch_size=B, max_seq_length=ctx + 64)
+    eng.prepare_synthetic_decode(ctx, decode_budget=32, seed=0)
+    assert eng.layer_roles[:3] == ["full", "plan", "subset"] and eng.layer_roles[-1] == "subset"
+    watch = (0, 1, 2, 31)
+    for i in watch:
+        eng.model.layers[i].attention.record = []
+    lens0, tok0 = eng.cachelens.clone(), eng.static_tokens.clone()
+    eager_tok = eng.decode_steps(1, use_graph=False).clone()
+    torch.cuda.synchronize()
+    rec = {i: eng.model.layers[i].attention.record[0] for i in watch}
+    for i in watch:
+        eng.model.layers[i].attention.record = None
+    sel = eng.page_selector
+    full_ip = sel.paged_kv_indptr[:B + 1].cpu()
+    full_ind = sel.paged_kv_indices[:int(full_ip[-1])].cpu()
+    last = sel.paged_kv_last_page_len[:B].cpu()
+    sub_ip = sel.paged_subset_kv_indptr[:B + 1].clone()
+    sub_ind = sel.paged_subset_kv_indices[:int(sub_ip[-1])].clone()
+    assert int(eng.use_subset_flag) == 1 and (sub_ip[1:] - sub_ip[:-1]).eq(k).all()
+    gpu_scores = eng.page_scores.cpu().double()
+
+    def row_kv(layer, pages):
+        cache = eng.model.layers[layer].attention.kv_cache.kv_cache
+        kv = cache[pages.to(DEV).long()].cpu()
+        n = pages.numel()
+        return kv, torch.tensor([0, n], dtype=torch.int32), torch.arange(n, dtype=torch.int32)
+
+    for b in (0, 13, 31):
+        pages = full_ind[int(full_ip[b]):int(full_ip[b + 1])]
+        n = pages.numel()
+        for layer in (0, 1):
+            q, o = rec[layer]
+            kv, ip1, ind1 = row_kv(layer, pages)
+            o_ref, _ = O.paged_decode_attention(q[b:b + 1].cpu(), kv, ip1, ind1, last[b:b + 1], scale)
+            assert_close(o[b:b + 1], o_ref, f"layer {layer} row {b} full attention")
+        q1 = rec[1][0][b:b + 1].cpu()
+        kv, ip1, ind1 = row_kv(1, pages)
+        x = O.dump_logits(q1, kv, ip1, ind1, last[b:b + 1], scale, n * 16)
+        s_ref = O.legacy_softmax_page_scores(x, 1, n, compute_dtype=torch.float64).double()
+        cnt = torch.tensor([n], dtype=torch.int32)
+        want_i, _ = O.select_pages(s_ref.float(), cnt, pages[None, :], k, L)
+        got = set(sub_ind[int(sub_ip[b]):int(sub_ip[b + 1])].cpu().tolist())
+        err = (gpu_scores[b, :n] - s_ref[0]).abs().max().item()
+        keys = O.prepare_scores(s_ref.float(), cnt, L)[0]
+        thr = sorted(keys.tolist(), reverse=True)[k - 1]
+        for page in got ^ set(want_i.tolist()):
+            j = pages.tolist().index(page)
+            assert abs(float(keys[j]) - thr) <= 2 * err + 1e-6 * abs(thr), f"row {b}: page {j} far from the k-th key"
+        sub_pages = sub_ind[int(sub_ip[b]):int(sub_ip[b + 1])].cpu()
+        for layer in (2, 31):
+            q, o = rec[layer]
+            kv, ip1, ind1 = row_kv(layer, sub_pages)
+            o_ref, _ = O.paged_decode_attention(q[b:b + 1].cpu(), kv, ip1, ind1, last[b:b + 1], scale)
+            assert_close(o[b:b + 1], o_ref, f"layer {layer} row {b} subset attention")
+
+    # the new token's cache slot of every row, in three layers, after the eager step
+    pos = lens0.cpu()
+    slot_pages = torch.tensor([int(full_ind[int(full_ip[b]) + int(pos[b]) // 16]) for b in range(B)])
+    def slots():
+        return [eng.model.layers[i].attention.kv_cache.kv_cache[slot_pages.to(DEV).long(), :,
+                                                                 (pos % 16).to(DEV).long()].clone() for i in (0, 1, 31)]
+    eager_slots = slots()
+    with torch.inference_mode():
+        eng.cachelens.copy_(lens0)
+        eng.static_tokens.copy_(tok0)
+    eng.sync_host_lens()
+    replay_tok = eng.decode_steps(1, use_graph=True).clone()
+    torch.cuda.synchronize()
+    assert eng._decode_graph_failed is None and eng._decode_graph_stats["replays"] == 1
+    assert torch.equal(replay_tok, eager_tok)
+    assert torch.equal(sel.paged_subset_kv_indptr[:B + 1], sub_ip)
+    assert torch.equal(sel.paged_subset_kv_indices[:int(sub_ip[-1])], sub_ind)
+    for a, b_ in zip(slots(), eager_slots):
+        assert torch.equal(a, b_)
+    assert eng.cachelens.cpu().tolist() == (lens0.cpu() + 1).tolist()
+    ops.set_active_backend(None)
+    del eng
+    torch.cuda.empty_cache()

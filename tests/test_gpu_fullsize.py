@@ -95,6 +95,70 @@ def test_full_size_chain_matches_oracle(config):
             assert {int(cc.block_table[b, int(j)]) for j in cc.planted[b]} <= sel, f"row {b}: planted recall < 8/8"
 
 
+def _ulp32(x: float) -> float:
+    import numpy as np
+    return float(np.spacing(np.float32(abs(x))))
+
+
+@pytest.mark.parametrize("config", [2, 3, 4])
+def test_full_size_selection_matches_oracle_chain(config):
+    """End-to-end selection parity at the full BASELINE size: the GPU chain (planner dump + lse
+    -> scores -> radix select) against the oracle's own chain (fp64 logits rounded to fp32 ->
+    fp64 del3_legacy_softmax scores -> v2 selection), backend.py:887-904 and
+    page_selector_v2.py:113-188.  Two fp32 summation orders can only disagree on pages whose
+    keys straddle the k-th key closer than the scores' own error, so every differing page must
+    lie within twice the row's measured score error (plus an fp32 ulp) of the oracle's k-th key.
+    Sparse attention is always checked: the kernel over the oracle's selection against the
+    oracle's sparse attention."""
+    import math
+    c = config_case(config, device=DEV)
+    B, hq = c.q.shape[:2]
+    mp, k, L = c.max_pages, c.k, c.L
+    dump = torch.empty((B, hq, mp * 16), device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
+                   lse=lse, logits_dump=dump)
+    s = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+    idx, ip = K.select_pages(s, c.kv_indptr, c.block_table, k, L)
+    torch.cuda.synchronize()
+    del dump
+    cc = c.to("cpu")
+    x = O.dump_logits(cc.q, cc.kv_cache, cc.kv_indptr, cc.kv_indices, cc.kv_last_page_len, cc.sm_scale, mp * 16)
+    ref_s = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
+    del x
+    counts = cc.kv_indptr[1:] - cc.kv_indptr[:-1]
+    want_i, want_p = O.select_pages(ref_s.float(), counts, cc.block_table, k, L)
+    keys = O.prepare_scores(ref_s.float(), counts, L)
+    got_s = s.cpu().double()
+    got_i, got_p = idx.cpu(), ip.cpu()
+    assert got_p.tolist() == want_p.tolist()
+    rows_diff, pages_diff, worst = 0, 0, 0.0
+    for b in range(B):
+        a = set(got_i[int(got_p[b]):int(got_p[b + 1])].tolist())
+        r = set(want_i[int(want_p[b]):int(want_p[b + 1])].tolist())
+        if a == r:
+            continue
+        rows_diff += 1
+        pages_diff += len(a - r)
+        err = (got_s[b] - ref_s[b]).abs().max().item()
+        kb = sorted(keys[b].tolist(), reverse=True)
+        thr = kb[min(k, int(counts[b])) - 1]
+        bt = cc.block_table[b].tolist()
+        for page in a ^ r:
+            j = bt.index(page)
+            gap = abs(float(keys[b, j]) - thr)
+            worst = max(worst, gap / max(err, 1e-30))
+            assert math.isfinite(thr) and gap <= 2 * err + _ulp32(thr), \
+                f"config {config} row {b} page {j}: key {float(keys[b, j])} is {gap:.3e} from the k-th key, " \
+                f"score error {err:.3e}"
+    print(f"[selection-parity] config {config}: {pages_diff} of {int(want_p[-1])} selected pages differ from the "
+          f"oracle's own chain, in {rows_diff} of {B} rows (worst gap / score error {worst:.2f})")
+    o_sp = K.paged_decode(c.q, c.kv_cache, want_p.to(DEV), want_i.to(DEV), c.kv_last_page_len, max_pages_per_row=k,
+                          subset=True)
+    o_ref, _ = O.paged_decode_attention(cc.q, cc.kv_cache, want_p, want_i, cc.kv_last_page_len, cc.sm_scale)
+    assert_attn_close(o_sp, o_ref, f"config {config} sparse attention over the oracle's selection")
+
+
 def test_full_size_config5_ragged_properties():
     c = config_case(5, device=DEV)
     B, hq = c.q.shape[:2]

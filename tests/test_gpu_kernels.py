@@ -240,6 +240,11 @@ def test_selective_step_end_to_end(name):
             assert abs(float(keys[b, j]) - thr) <= 2e-4 * abs(thr), f"{name}: row {b} page {j} far from threshold"
     if mism == 0:
         assert_attn_close(o_sp, ref["o_sparse"], name + "/sparse")
+    else:
+        # the kernel over the oracle's own selection, against the oracle's sparse attention
+        o_sp_r = K.paged_decode(g.q, g.kv_cache, ref["indptr"].to(DEV), ref["indices"].to(DEV), g.kv_last_page_len,
+                                max_pages_per_row=k, subset=True)
+        assert_attn_close(o_sp_r, ref["o_sparse"], name + "/sparse over the oracle's selection")
     if c.planted is not None:
         for b in range(B):
             sel = set(got[int(ip[b]):int(ip[b + 1])].tolist())

@@ -45,6 +45,9 @@ SIGNATURES = {
         c_int, c_int, c_int, c_int, c_int,    # batch, hq, hkv, head_dim, dtype
         c_float, c_int,                       # sm_scale, max_pages_per_row
         _P, c_size_t, _P]),                   # workspace, bytes, stream
+    "delta_paged_decode_noalloc": (c_int, [
+        _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int64, c_int64,
+        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P]),
     "delta_paged_decode_append": (c_int, [
         _AP, _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int64,
         c_int64, c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),

@@ -26,6 +26,8 @@
 //
 // HBM bytes per launch (algorithmic): K and V of every attended token once,
 // q and o once, the page indices once (+ the fp32 logits when dumping).
+#include <mutex>
+
 #include "delta_common.h"
 
 namespace delta {
@@ -1112,4 +1114,75 @@ extern "C" DELTA_EXPORT int delta_paged_decode_subset_append(const delta_decode_
                            kv_last_page_len, o, o_stride_b, o_stride_h, lse, nullptr, 0, 0, batch, num_qo_heads,
                            num_kv_heads, head_dim, dtype, sm_scale, max_pages_per_row, delta::kAttnSubset, workspace,
                            workspace_bytes, (hipStream_t)stream, "delta_paged_decode_subset_append", append);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the split partials live in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate (graph capture, serving loops that forbid
+// hipMalloc).  Each GPU holds its own copy of the array until the process ends; its device
+// address is looked up once per device, with that device current, and only that address is
+// handed to kernels (the array's name is a host-side stand-in, not a device address).
+// ---------------------------------------------------------------------------
+namespace delta {
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)64 << 20;  // 64 MiB: every BASELINE shape needs <= 46 MB
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The current device's copy of `scratch` (null, with the error set, on failure).
+void *scratch_for_current_device(const char *who) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(DELTA_ERR_HIP, "%s: no usable current device (%d)", who, dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error(DELTA_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace delta
+
+extern "C" DELTA_EXPORT int delta_paged_decode_noalloc(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                                       const void *kv_cache, int64_t num_pages,
+                                                       const int32_t *kv_indptr, const int32_t *kv_indices,
+                                                       int64_t kv_indices_len, const int32_t *kv_last_page_len,
+                                                       void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                                                       float *logits_dump, int64_t dump_stride_b,
+                                                       int64_t dump_stride_h, int batch, int num_qo_heads,
+                                                       int num_kv_heads, int head_dim, int dtype, float sm_scale,
+                                                       int max_pages_per_row, delta_stream_t stream) {
+  const char *who = "delta_paged_decode_noalloc";
+  delta::clear_error();
+  if (batch <= 0) return DELTA_OK;
+  if (num_kv_heads <= 0 || num_qo_heads <= 0)
+    return delta::set_error(DELTA_ERR_INVALID, "%s: head counts must be positive", who);
+  const size_t need = delta_paged_decode_workspace_bytes(batch, num_qo_heads, num_kv_heads,
+                                                         max_pages_per_row > 0 ? max_pages_per_row : 1);
+  if (need > delta::kScratchBytes)
+    return delta::set_error(DELTA_ERR_INVALID,
+                            "%s: this shape needs %zu bytes of split scratch, more than the %zu-byte static "
+                            "scratch; use delta_paged_decode with a workspace",
+                            who, need, delta::kScratchBytes);
+  void *ws = delta::scratch_for_current_device(who);
+  if (!ws) return DELTA_ERR_HIP;
+  const int mode = logits_dump ? delta::kAttnDump : delta::kAttn;
+  return delta::run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                           kv_last_page_len, o, o_stride_b, o_stride_h, lse, logits_dump, dump_stride_b,
+                           dump_stride_h, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
+                           max_pages_per_row, mode, ws, delta::kScratchBytes, (hipStream_t)stream, who, nullptr);
 }

@@ -110,6 +110,25 @@ int delta_paged_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                        int dtype, float sm_scale, int max_pages_per_row,
                        void *workspace, size_t workspace_bytes, delta_stream_t stream);
 
+/* delta_paged_decode without a workspace argument: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under hipGraph capture, serving loops or
+ * harnesses that forbid hipMalloc): the split-K partials live in a static 64 MiB device array
+ * of the library (one per GPU, held until the process ends; its address is looked up on the
+ * first call on each device), so the call allocates nothing.  A shape whose partials exceed
+ * 64 MiB (delta_paged_decode_workspace_bytes) is rejected with DELTA_ERR_INVALID.  The array
+ * needs no initial contents, but it is shared by every call on one GPU: calls that overlap on
+ * one GPU (concurrent streams, threads) race and must be serialised by the caller.  Results are
+ * bit-identical to delta_paged_decode. */
+int delta_paged_decode_noalloc(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                               const void *kv_cache, int64_t num_pages,
+                               const int32_t *kv_indptr, const int32_t *kv_indices,
+                               int64_t kv_indices_len, const int32_t *kv_last_page_len,
+                               void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                               float *logits_dump, int64_t dump_stride_b, int64_t dump_stride_h,
+                               int batch, int num_qo_heads, int num_kv_heads, int head_dim,
+                               int dtype, float sm_scale, int max_pages_per_row,
+                               delta_stream_t stream);
+
 /* The same attention over a *selected* page subset (the subset CSR built by
  * delta_select_pages, sharing kv_last_page_len with the full CSR):
  * target_subset_decode (backend.py:486-512).  Separate entry point (and

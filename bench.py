@@ -539,6 +539,8 @@ def main():
     ap.add_argument("--engine-config4-only", action="store_true",
                     help="only the config-4 decode step (selective and full cache; for kernel traces)")
     ap.add_argument("--kernel-reps", type=int, default=48)
+    ap.add_argument("--configs-only", action="store_true",
+                    help="only the kernel-level measurements at BASELINE configs 2, 4 and 5 (for rocprofv3 runs)")
     ap.add_argument("--cpu-baseline-only", action="store_true",
                     help="only the CPU baseline (runs without a GPU)")
     ap.add_argument("--kernels-only", action="store_true",
@@ -563,6 +565,16 @@ def main():
         log(f"  selective {eng4['ms_per_step']:.3f} ms/step ({eng4['tokens_per_s']} tokens/s), full cache "
             f"{eng4['full_cache_ms_per_step']:.3f} ms/step: {eng4['speedup_vs_full_cache']}x")
         print(json.dumps({"engine_config4": eng4}), flush=True)
+        return
+    if args.configs_only:
+        out = {}
+        for cfg in (2, 4, 5):
+            out[f"config{cfg}"] = config_kernels(torch, cfg, reps=args.kernel_reps // 4 or 1)
+            for k, v in out[f"config{cfg}"].items():
+                if isinstance(v, dict):
+                    log(f"  config {cfg} {k}: {v['us']} us, {v['GB_s']} GB/s")
+            torch.cuda.empty_cache()
+        print(json.dumps({"kernels_other_configs": out}), flush=True)
         return
     if args.kernels_only:
         kern = kernel_roofline(torch, args.kernel_reps)

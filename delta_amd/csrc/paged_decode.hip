@@ -395,143 +395,184 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_sched_barrier(0);
   }
-  int pid = __builtin_amdgcn_readlane(ids, 0);
-  u32x4 kf[4], vf[4];
-  if (count > 0) {
-    const uint16_t *base = page_ptr(pid);
-    // Issue order K then V, as in the loop body, so the loop's waits can stay partial.
+  // One page of the wave (index gi in its page list, id pidc, data in kr / vr): q.K, the logits
+  // (dump / on-chip staging), the online softmax and, with V, P.V.  When `more`, the load of
+  // page pidn into kr / vr is issued right after kr's last use, so it is in flight while the
+  // rest of this page (and any other page in between) is processed.
+  auto page_body = [&](int gi, u32x4 (&kr)[4], u32x4 (&vr)[4], int pidc, int pidn, bool more) {
+    const int j = first + R * gi;
+    const bool ok = pidc >= 0;
+    if (ROPE && ok && pidc == ap_pid) {
+      // The new token's row of this page (a wave-uniform branch, taken once): K lanes with
+      // t / 2 == slot % 8 in steps 2 (slot / 8) + sp, V lanes with c == slot % 4 in tile row
+      // group slot / 4.
+      if ((t >> 1) == (ap_slot & 7)) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) kf[s] = ld128_stream(base + k_off + k_step(s));
-    __builtin_amdgcn_sched_barrier(0);
-    if (WITH_V) {
+        for (int s = 0; s < 4; ++s)
+          if ((s >> 1) == (ap_slot >> 3))
+            kr[s] = *reinterpret_cast<const u32x4 *>(tok_lds + 32 * (s & 1) + 16 * (t & 1) + 4 * c);
+      }
+      if (WITH_V && c == (ap_slot & 3)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vf[i] = ld128_stream(base + v_off + (int64_t)(4 * i) * row_elems);
+        for (int i = 0; i < 4; ++i)
+          if (i == (ap_slot >> 2)) vr[i] = *reinterpret_cast<const u32x4 *>(tok_lds + kHeadDim / 2 + 4 * t);
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  for (int c0 = 0; c0 < count; c0 += 64) {
-    const int cn = count - c0 < 64 ? count - c0 : 64;
-    const int ids_next = c0 + 64 < count ? load_ids(c0 + 64) : -1;
-    for (int it = 0; it < cn; ++it) {
-      const int j = first + R * (c0 + it);
-      const bool ok = pid >= 0;
-      const bool more = c0 + it + 1 < count;
-      const int pidn = it + 1 < cn ? __builtin_amdgcn_readlane(ids, it + 1) : __builtin_amdgcn_readlane(ids_next, 0);
+
+    if (WITH_V) {
+      // Stage this page's V (loaded one iteration ago) before anything else, so the wait at
+      // the top of the iteration is the only one on loaded data and the registers are free
+      // for the next page's V below.  Rows past kv_len (and all rows of an invalid page) are
+      // zeroed by mask, since they may hold NaN/Inf and meet p = 0.  Token 4i + c goes to
+      // tile row 8 (i % 2) + 4 (c / 2) + 2 (i / 2) + c % 2, the row whose k slot holds its p.
+      const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
+        const u32x4 w = vr[i] & u32x4{keep, keep, keep, keep};
+        const int trow = 8 * (i & 1) + 4 * (c >> 1) + 2 * (i >> 1) + (c & 1);
+        st128(vt + trow * kVStride + 8 * t, w);
+      }
+    }
+    f32x4 S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
+    S0 = E::mfma(kr[0], qf[0], S0);
+    S1 = E::mfma(kr[2], qf[0], S1);
+    S0 = E::mfma(kr[1], qf[1], S0);
+    S1 = E::mfma(kr[3], qf[1], S1);
+    if (more) {
       const uint16_t *nbase = page_ptr(pidn);
-      if (ROPE && ok && pid == ap_pid) {
-        // The new token's row of this page (a wave-uniform branch, taken once): K lanes with
-        // t / 2 == slot % 8 in steps 2 (slot / 8) + sp, V lanes with c == slot % 4 in tile row
-        // group slot / 4.
-        if ((t >> 1) == (ap_slot & 7)) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if ((s >> 1) == (ap_slot >> 3))
-              kf[s] = *reinterpret_cast<const u32x4 *>(tok_lds + 32 * (s & 1) + 16 * (t & 1) + 4 * c);
-        }
-        if (WITH_V && c == (ap_slot & 3)) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (i == (ap_slot >> 2)) vf[i] = *reinterpret_cast<const u32x4 *>(tok_lds + kHeadDim / 2 + 4 * t);
-        }
-      }
-
+      for (int s = 0; s < 4; ++s) kr[s] = ld128_stream(nbase + k_off + k_step(s));
       if (WITH_V) {
-        // Stage this page's V (loaded one iteration ago) before anything else, so the wait at
-        // the top of the iteration is the only one on loaded data and the registers are free
-        // for the next page's V below.  Rows past kv_len (and all rows of an invalid page) are
-        // zeroed by mask, since they may hold NaN/Inf and meet p = 0.  Token 4i + c goes to
-        // tile row 8 (i % 2) + 4 (c / 2) + 2 (i / 2) + c % 2, the row whose k slot holds its p.
-        const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t keep = 4 * i + c < vlim ? 0xffffffffu : 0u;
-          const u32x4 w = vf[i] & u32x4{keep, keep, keep, keep};
-          const int trow = 8 * (i & 1) + 4 * (c >> 1) + 2 * (i >> 1) + (c & 1);
-          st128(vt + trow * kVStride + 8 * t, w);
-        }
+        for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(nbase + v_off + (int64_t)(4 * i) * row_elems);
       }
-      f32x4 S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
-      S0 = E::mfma(kf[0], qf[0], S0);
-      S1 = E::mfma(kf[2], qf[0], S1);
-      S0 = E::mfma(kf[1], qf[1], S0);
-      S1 = E::mfma(kf[3], qf[1], S1);
-      // The next page's K and V are in flight for the rest of the iteration.
-      if (more) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) kf[s] = ld128_stream(nbase + k_off + k_step(s));
-        if (WITH_V) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) vf[i] = ld128_stream(nbase + v_off + (int64_t)(4 * i) * row_elems);
-        }
-      }
+    }
 
-      // Join the d halves: q_g . K[tok(r)] = D[rows 2u, 2u + 1] of columns g and 8 + g.
-      const float S[4] = {S0[0] + dpp_f<0x128>(S0[1]), S0[2] + dpp_f<0x128>(S0[3]),
-                          S1[0] + dpp_f<0x128>(S1[1]), S1[2] + dpp_f<0x128>(S1[3])};
-      const int tok0 = j * kPageSize + 2 * c;  // tok(r) = tok0 + 8 (r / 2) + r % 2
-      float x[4], p[4];
+    // Join the d halves: q_g . K[tok(r)] = D[rows 2u, 2u + 1] of columns g and 8 + g.
+    const float S[4] = {S0[0] + dpp_f<0x128>(S0[1]), S0[2] + dpp_f<0x128>(S0[3]),
+                        S1[0] + dpp_f<0x128>(S1[1]), S1[2] + dpp_f<0x128>(S1[3])};
+    const int tok0 = j * kPageSize + 2 * c;  // tok(r) = tok0 + 8 (r / 2) + r % 2
+    float x[4], p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        x[r] = (ok && tok0 + 8 * (r >> 1) + (r & 1) < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
-      const int slot = (c0 + it) % kDumpSlots;
-      if (TOKMAX && t < G && j < a.dump_pages) {
-        float *dl = smem + tokmax_lds_header<G>() + (j * G + t) * kPageSize + 2 * c;
+    for (int r = 0; r < 4; ++r)
+      x[r] = (ok && tok0 + 8 * (r >> 1) + (r & 1) < ri.kv_len) ? S[r] * sm_scale : -INFINITY;
+    const int slot = gi % kDumpSlots;
+    if (TOKMAX && t < G && j < a.dump_pages) {
+      float *dl = smem + tokmax_lds_header<G>() + (j * G + t) * kPageSize + 2 * c;
+      *reinterpret_cast<float2 *>(dl) = float2{x[0], x[1]};
+      *reinterpret_cast<float2 *>(dl + 8) = float2{x[2], x[3]};
+    }
+    if (WITH_DUMP) {
+      // Logits staged in LDS, one slot per page of a kDumpSlots-page window.
+      if (t < G) {
+        float *dl = dbuf + (slot * G + t) * kPageSize + 2 * c;
         *reinterpret_cast<float2 *>(dl) = float2{x[0], x[1]};
         *reinterpret_cast<float2 *>(dl + 8) = float2{x[2], x[3]};
       }
-      if (WITH_DUMP) {
-        // Logits staged in LDS, one slot per page of a kDumpSlots-page window.
-        if (t < G) {
-          float *dl = dbuf + (slot * G + t) * kPageSize + 2 * c;
-          *reinterpret_cast<float2 *>(dl) = float2{x[0], x[1]};
-          *reinterpret_cast<float2 *>(dl + 8) = float2{x[2], x[3]};
-        }
-        okmask |= (ok ? 1u : 0u) << slot;
-      }
-      float pm = -INFINITY;
+      okmask |= (ok ? 1u : 0u) << slot;
+    }
+    float pm = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] *= kLog2e;
-        pm = fmaxf(pm, x[r]);
-      }
-      const float mn = fmaxf(m, rows4_max(pm));
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = fast_exp2(m - mref);
-      float ps = 0.f;
+    for (int r = 0; r < 4; ++r) {
+      x[r] *= kLog2e;
+      pm = fmaxf(pm, x[r]);
+    }
+    const float mn = fmaxf(m, rows4_max(pm));
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = fast_exp2(m - mref);
+    float ps = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = fast_exp2(x[r] - mref);
-        ps += p[r];
-      }
-      l = l * alpha + rows4_sum(ps);
-      m = mn;
+    for (int r = 0; r < 4; ++r) {
+      p[r] = fast_exp2(x[r] - mref);
+      ps += p[r];
+    }
+    l = l * alpha + rows4_sum(ps);
+    m = mn;
 
-      if (WITH_V) {
-        // Rescale the accumulators only when some head's running max moved.
-        if (__ballot(alpha != 1.f)) {
+    if (WITH_V) {
+      // Rescale the accumulators only when some head's running max moved.
+      if (__ballot(alpha != 1.f)) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float al = shfl(alpha, 4 * c + r);
+        for (int r = 0; r < 4; ++r) {
+          const float al = shfl(alpha, 4 * c + r);
 #pragma unroll
-            for (int n = 0; n < 8; ++n) acc[n][r] *= al;
-          }
-        }
-        s4_t pa;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pa[r] = t < G ? M16::pack(p[r]) : (short)0;
-        const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStride + 4 * (t & 3);
-#pragma unroll
-        for (int n = 0; n < 8; ++n) {
-          const s4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t *)(rd + 16 * n));
-          acc[n] = M16::run(pa, bv, acc[n]);
+          for (int n = 0; n < 8; ++n) acc[n][r] *= al;
         }
       }
-      // Last page of a window (or of the wave): write the window's staged logits.  The
-      // stores go out after the next page's loads, which therefore never wait behind them.
-      if (WITH_DUMP && (slot == kDumpSlots - 1 || !more)) flush_window(c0 + it - slot, slot + 1);
+      s4_t pa;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pa[r] = t < G ? M16::pack(p[r]) : (short)0;
+      const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStride + 4 * (t & 3);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const s4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t *)(rd + 16 * n));
+        acc[n] = M16::run(pa, bv, acc[n]);
+      }
+    }
+    // Last page of a window (or of the wave): write the window's staged logits.  The
+    // stores go out after the next page's loads, which therefore never wait behind them.
+    if (WITH_DUMP && (slot == kDumpSlots - 1 || gi + 1 == count)) flush_window(gi - slot, slot + 1);
+  };
+
+  auto issue = [&](int pidc, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
+    const uint16_t *base = page_ptr(pidc);
+    // Issue order K then V, as in the page body, so the waits can stay partial.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kr[s] = ld128_stream(base + k_off + k_step(s));
+    __builtin_amdgcn_sched_barrier(0);
+    if (WITH_V) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(base + v_off + (int64_t)(4 * i) * row_elems);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Page ids of the wave's pages gi in [cb, cb + 128): lanes of `ids` (chunk cb) and `ids_nx`.
+  int cb = 0;
+  int ids_nx = count > 64 ? load_ids(64) : -1;
+  auto id_at = [&](int gi) -> int {
+    const int o = gi - cb;
+    return o < 64 ? __builtin_amdgcn_readlane(ids, o) : __builtin_amdgcn_readlane(ids_nx, o - 64);
+  };
+  auto advance_chunk = [&](int gi) {  // gi reached the next chunk of 64: shift the id registers
+    if (gi - cb >= 64) {
+      cb += 64;
+      ids = ids_nx;
+      ids_nx = cb + 64 < count ? load_ids(cb + 64) : -1;
+    }
+  };
+
+  u32x4 kf[4], vf[4];
+  if (WITH_V) {
+    // Attention: one page in flight (K and V) while the current one is processed.
+    int pid = id_at(0);
+    if (count > 0) issue(pid, kf, vf);
+    for (int gi = 0; gi < count; ++gi) {
+      advance_chunk(gi);
+      const bool more = gi + 1 < count;
+      const int pidn = more ? id_at(gi + 1) : -1;
+      page_body(gi, kf, vf, pid, pidn, more);
       pid = pidn;
     }
-    ids = ids_next;
+  } else {
+    // K-only scorer: no V tiles or accumulators, so two pages of K are in flight -- pages
+    // alternate between the register sets kf and kg, each reloaded two pages ahead.
+    u32x4 kg[4];
+    int pa = id_at(0), pb = count > 1 ? id_at(1) : -1;
+    if (count > 0) issue(pa, kf, vf);
+    if (count > 1) issue(pb, kg, vf);
+    for (int gi = 0; gi < count; gi += 2) {
+      advance_chunk(gi);
+      const int p2 = gi + 2 < count ? id_at(gi + 2) : -1;
+      page_body(gi, kf, vf, pa, p2, gi + 2 < count);
+      pa = p2;
+      if (gi + 1 < count) {
+        const int p3 = gi + 3 < count ? id_at(gi + 3) : -1;
+        page_body(gi + 1, kg, vf, pb, p3, gi + 3 < count);
+        pb = p3;
+      }
+    }
   }
 
   // Merge the block's waves in LDS.  Attention launches have a merge area of their own past

@@ -272,12 +272,12 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   }
 
   // Fused RoPE + append of the row's new token (ROPE), with no block barrier: every wave
-  // loads the token's k and v pair `lane` of its kv head, its position and the append slot
-  // before the page stream starts (independent of it); while the wave's page ids load,
-  // lane i computes pair i's (cos, sin), rotates q (ds_bpermute hands each lane the
-  // pairs of its fragments) and k, and keeps the rotated k and the v in an LDS slot of the
-  // wave's own, from which the wave that attends the token's page takes that row.  The cache
-  // slot is written at the end of the kernel: no wave reads it.
+  // loads the token's k and v pair `lane` of its kv head and its position before the page
+  // stream starts (independent of it), and the append slot right after its page ids; lane i
+  // computes pair i's (cos, sin), rotates q (ds_bpermute hands each lane the pairs of its
+  // fragments) and k, and keeps the rotated k and the v in an LDS slot of the wave's own,
+  // from which the wave that attends the token's page takes that row.  The cache slot is
+  // written at the end of the kernel: no wave reads it.
   int ap_pid = -1, ap_slot = 0;
   uint32_t kraw = 0u, vraw = 0u;
   float rpos = 0.f;
@@ -285,18 +285,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     kraw = reinterpret_cast<const uint32_t *>(a.k_new + (int64_t)b * a.k_new_stride + (int64_t)h * kHeadDim)[lane];
     vraw = reinterpret_cast<const uint32_t *>(a.v_new + (int64_t)b * a.v_new_stride + (int64_t)h * kHeadDim)[lane];
     rpos = (float)a.offsets[b];
-    // The append slot, with delta_append_kv's checks (a row without a valid slot appends
-    // nothing).
-    const int64_t q0 = a.ap_indptr[b], q1 = a.ap_indptr[b + 1];
-    if (q0 >= 0 && q1 > q0 && q1 <= a.ap_indices_len) {
-      int lp = a.last_page_len[b];
-      lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
-      const int tp = (int)(q1 - q0 - 1) * kPageSize + lp - 1;  // the new token's position
-      if (tp >= 0) {
-        ap_pid = a.ap_indices[q0 + tp / kPageSize];
-        ap_slot = tp % kPageSize;
-      }
-    }
   }
   // This wave's LDS slot for the token: [64] rotated k pairs, then [64] v pairs.
   uint32_t *const tok_lds = reinterpret_cast<uint32_t *>(smem + rope_lds_offset<G, WITH_V, WITH_DUMP>(nw)) +
@@ -372,12 +360,10 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     okmask = 0;
   };
 
-  int ids = count > 0 ? load_ids(0) : -1;
-  // RoPE while the wave's page ids are in flight (the token's k and v registers die before
-  // the page stream starts): lane i holds pair i's (cos, sin); q pair 32 sp + 16 (t / 8) +
-  // 4c + w sits in qf[sp][w] (zero for heads past the group).
-  if (ROPE) {
-    if (ap_pid >= (int64_t)a.num_pages) ap_pid = -1;
+  // RoPE of q and of the token's k (lane i holds pair i's (cos, sin); q pair 32 sp + 16 (t / 8)
+  // + 4c + w sits in qf[sp][w], zero for heads past the group).  It needs only the token's
+  // position, k and v, not the append slot, so it never waits on the slot's dependent loads.
+  auto rope_prologue = [&]() {
     float cs_sn[2];
     rope_cos_sin(lane, rpos, a.rcp_scale, a.log2_theta, a.smooth_a, a.smooth_b, cs_sn);
 #pragma unroll
@@ -394,6 +380,27 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_sched_barrier(0);
+  };
+  // Attention launches run it while their first page is in flight; planner launches (more
+  // live registers: the dump staging) here, before their page ids are requested.
+  constexpr bool kRopeUnderFirstPage = !WITH_DUMP;
+  if (ROPE && !kRopeUnderFirstPage) rope_prologue();
+  int ids = count > 0 ? load_ids(0) : -1;
+  if (ROPE) {
+    // The append slot, with delta_append_kv's checks (a row without a valid slot appends
+    // nothing).  Its page id is a dependent load: issued after the page ids, so that no wait
+    // on the row's bounds (scalar loads complete out of order) also waits for it.
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t q0 = a.ap_indptr[b], q1 = a.ap_indptr[b + 1];
+    if (q0 >= 0 && q1 > q0 && q1 <= a.ap_indices_len) {
+      int lp = a.last_page_len[b];
+      lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+      const int tp = (int)(q1 - q0 - 1) * kPageSize + lp - 1;  // the new token's position
+      if (tp >= 0) {
+        ap_pid = a.ap_indices[q0 + tp / kPageSize];
+        ap_slot = tp % kPageSize;
+      }
+    }
   }
   // One page of the wave (index gi in its page list, id pidc, data in kr / vr): q.K, the logits
   // (dump / on-chip staging), the online softmax and, with V, P.V.  When `more`, the load of
@@ -548,6 +555,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     // Attention: one page in flight (K and V) while the current one is processed.
     int pid = id_at(0);
     if (count > 0) issue(pid, kf, vf);
+    if (ROPE && kRopeUnderFirstPage) rope_prologue();
     for (int gi = 0; gi < count; ++gi) {
       advance_chunk(gi);
       const bool more = gi + 1 < count;
@@ -654,7 +662,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       }
     }
   }
-  if (ROPE && ap_pid >= 0 && (a.nsplit == 1 || split == 0)) {
+  if (ROPE && ap_pid >= 0 && (int64_t)ap_pid < a.num_pages && (a.nsplit == 1 || split == 0)) {
     // One block per (row, kv head group) writes the new token's rotated k and v into the cache
     // slot, 16-byte chunk r % 16 of head head0 + r / 16, from the LDS slot of wave r / 16 (which
     // works on that head); the merge's barrier above ordered those LDS stores.

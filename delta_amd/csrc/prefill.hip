@@ -5,28 +5,35 @@
 // cache already holds the row's new tokens (update_kv runs before attention, model.py:413-418),
 // so query i of row b sits at position kv_len_b - qo_len_b + i and attends tokens 0..position.
 //
-// Work decomposition: block = 8 waves of one (row, kv head) and 8 * TW consecutive query
-// tokens; each wave owns TW = 16 / G tokens and puts their (token, q head) pairs in the 16
-// columns of its MFMA tiles.  The block sweeps the pages up to its last token's position:
-// each page's K and V (4 KiB each for one head) are loaded once per block, 16 bytes per thread,
-// into double-buffered LDS tiles kGroup pages at a time (the next group in flight in
-// registers), and all waves read them from there; a wave whose tokens end earlier skips the
-// later pages, and groups below every column's diagonal skip the element masks.  No merge.
-//   q.K : S^T = K Q^T with v_mfma_f32_16x16x32 -- A = the page's 16 K rows from LDS
-//         (lane%16 = token, lane/16 picks d in [32s + 8c, +8) at step s), B = the wave's query
-//         columns; D puts tokens 4c..4c+3 of column j = lane%16 in lane (c, j);
-//   softmax: online per column in the log2 domain, causal and kv_len masks per element;
-//   P.V : v_mfma_f32_16x16x16 -- A = P (row = column j, k = tokens 4c..), B = V from the
-//         padded LDS tile read with ds_read_b64_tr_b16, D = O[column 4c + r][16n + lane%16].
-// Page ids are preloaded 64 per register, as in the decode kernel.
+// Work decomposition (flash-attention style, on 32x32 MFMA tiles): a block is kPW waves of one
+// (row, kv head) and a run of consecutive query tokens; each wave owns 32 query rows, the
+// (token, q head) pairs of TW = 32 / G tokens (rows past TW * G idle when G does not divide
+// 32), with its q in registers.  The block sweeps the row's kv tokens 32 at a time (two pages)
+// up to its last token's position: each step's K and V (8 KiB each for one head) are loaded
+// once per block, 16 bytes per thread, into double-buffered padded LDS tiles (the next step in
+// flight in registers) and read by every wave.  Per wave and step:
+//   S^T = K Q^T : 8 v_mfma_f32_32x32x16 over d, A = the tile's K rows from LDS
+//         (lane%32 = kv token, d in 16 ks + 8 (lane / 32) + [0, 8)), B = the wave's q (same d
+//         split, n = lane%32 = query row); D leaves lane l with its row n = l%32 and the 16 kv
+//         tokens m_i = 8 (i / 4) + 4 (l / 32) + i % 4;
+//   softmax: online per row in the log2 domain, lane-local but for one exchange with lane
+//         l ^ 32 (the row's other 16 tokens); causal and kv_len masks only on tiles that need
+//         them;
+//   O^T += V^T P^T : 8 v_mfma_f32_32x32x16 (4 d tiles x 2 kv chunks), B = the lane's own P in
+//         its D order (chunk c = values 8c..8c+7, i.e. kv tokens 16c + 4 (l/32) + {0..3, 8..11}),
+//         A = V^T read from the padded tile with ds_read_b64_tr_b16 in that same kv order;
+//         lane l accumulates O[row l%32][d = 32 dt + 8 (i / 4) + 4 (l / 32) + i % 4].
+// Blocks run heaviest first (the last query tiles attend the most tokens) and blockIdx.x is the
+// kv head, so the blocks of one head land on the same XCD (blocks go to the XCDs round robin)
+// and share its L2 for that head's K/V.  Page ids are preloaded 64 per register.  No merge.
 #include "delta_common.h"
 
 namespace delta {
 namespace {
 
-constexpr int kPrefillWaves = 8;  // waves per block: 8 x 16 (token, head) columns share each K/V page
-constexpr int kGroup = 2;         // pages per LDS buffer (and per barrier)
-constexpr int kVStrideP = 136;    // padded tile row (elements)
+constexpr int kPW = 8;          // waves per block (each 32 query rows)
+constexpr int kKvStep = 32;     // kv tokens per step (two pages)
+constexpr int kRowP = 136;      // padded LDS tile row (elements): conflict-free 16-byte row reads
 
 struct PrefillArgs {
   const uint16_t *q;
@@ -45,59 +52,55 @@ struct PrefillArgs {
   float sm_scale;
 };
 
-template <int DT>
-struct PMfma;
-template <>
-struct PMfma<DELTA_BF16> {
-  typedef short s4 __attribute__((ext_vector_type(4)));
-  __device__ __forceinline__ static f32x4 run(s4 a, s4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static short pack(float x) { return __builtin_bit_cast(short, (__bf16)x); }
-};
-template <>
-struct PMfma<DELTA_FP16> {
-  typedef short s4 __attribute__((ext_vector_type(4)));
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  __device__ __forceinline__ static f32x4 run(s4 a, s4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static short pack(float x) { return __builtin_bit_cast(short, (_Float16)x); }
-};
-
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short ps4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) ps4_t lds_ps4_t;
 
-__device__ __forceinline__ float prows4_max(float v) {
-  auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
-  auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+template <int DT>
+struct Mfma32;
+template <>
+struct Mfma32<DELTA_BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma32<DELTA_FP16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+
+// max / sum of a value and its copy in lane l ^ 32
+__device__ __forceinline__ float halves_max(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
 }
-__device__ __forceinline__ float prows4_sum(float v) {
-  auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
-  auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(y[0]) + __uint_as_float(y[1]);
+__device__ __forceinline__ float halves_sum(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(x[0]) + __uint_as_float(x[1]);
 }
 
 template <int DT, int G>
-__global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) {
 #pragma clang fp contract(off)
   using E = Elem<DT>;
-  using M16 = PMfma<DT>;
-  constexpr int TW = 16 / G;                  // query tokens per wave
-  constexpr int BT = kPrefillWaves * TW;      // query tokens per block
-  constexpr int kTile = kPageSize * kVStrideP;  // one K or V tile (elements)
-  // Two page buffers, each K then V (padded rows), shared by the block's waves.
-  __shared__ uint16_t tiles[2][kGroup][2 * kTile];
+  using MF = Mfma32<DT>;
+  constexpr int TW = 32 / G;                  // query tokens per wave
+  constexpr int BT = kPW * TW;                // query tokens per block
+  constexpr int kTile = kKvStep * kRowP;      // one K or V tile (elements)
+  // Two step buffers, each K then V (padded rows), shared by the block's waves.
+  __shared__ uint16_t tiles[2][2 * kTile];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = lane >> 4, t = lane & 15;
-  const int b = blockIdx.z, h = blockIdx.y;
+  const int hl = lane >> 5, n = lane & 31;
+  const int h = blockIdx.x, b = blockIdx.z;
   const int64_t q0 = a.qo_indptr[b], q1 = a.qo_indptr[b + 1];
   const int qn = q1 > q0 ? (int)(q1 - q0) : 0;
-  const int btok0 = blockIdx.x * BT;
+  const int tile = (int)gridDim.y - 1 - (int)blockIdx.y;  // heaviest tiles first
+  const int btok0 = tile * BT;
   if (btok0 >= qn) return;  // whole block
   const int tok0 = btok0 + wave * TW;
 
@@ -111,196 +114,197 @@ __global__ void __launch_bounds__(kPrefillWaves * 64) paged_prefill_kernel(Prefi
   lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
   const int kv_len = np > 0 ? (np - 1) * kPageSize + lp : 0;
 
-  // Column t = (token tt, head g) of this wave.
-  const int tt = t / G, g = t % G;
-  const bool col_ok = t < TW * G && tok0 + tt < qn;
+  // This lane's query row n = (token tt, head g).
+  const int tt = n / G, g = n % G;
+  const bool row_ok = n < TW * G && tok0 + tt < qn;
   const int qpos = kv_len - qn + tok0 + tt;  // attends tokens 0..qpos
-  u32x4 qf[4];
-  if (col_ok) {
-    const uint16_t *qp = a.q + (q0 + tok0 + tt) * a.q_stride_t + (int64_t)(h * G + g) * a.q_stride_h + 8 * c;
+  u32x4 qf[8];  // B operand of S^T = K Q^T: d = 16 ks + 8 hl + [0, 8)
+  if (row_ok) {
+    const uint16_t *qp = a.q + (q0 + tok0 + tt) * a.q_stride_t + (int64_t)(h * G + g) * a.q_stride_h + 8 * hl;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = ld128(qp + 32 * s);
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = ld128(qp + 16 * ks);
   } else {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = u32x4{0u, 0u, 0u, 0u};
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  // Pages the block sweeps (up to its last token's position) and the ones this wave needs.
-  auto pages_upto = [&](int last_tok) {
+  // Steps the block sweeps (up to its last token's position) and the ones this wave needs.
+  auto steps_upto = [&](int last_tok) {
     const int pos = kv_len - qn + last_tok;
-    const int n = pos >= 0 ? pos / kPageSize + 1 : 0;
-    return n > np ? np : n;
+    const int nt = pos >= 0 ? pos / kKvStep + 1 : 0;
+    const int cap = (kv_len + kKvStep - 1) / kKvStep;
+    return nt > cap ? cap : nt;
   };
-  const int count = pages_upto((btok0 + BT < qn ? btok0 + BT : qn) - 1);
-  const int wcount = tok0 < qn ? pages_upto((tok0 + TW < qn ? tok0 + TW : qn) - 1) : 0;
+  const int nsteps = steps_upto((btok0 + BT < qn ? btok0 + BT : qn) - 1);
+  const int wsteps = tok0 < qn ? steps_upto((tok0 + TW < qn ? tok0 + TW : qn) - 1) : 0;
+  // First query position of the wave: steps ending at or below it need no causal mask.
+  const int wpos0 = kv_len - qn + tok0;
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
-  // Cooperative tile load: thread i < 512 moves 16 bytes -- K (i < 256) or V row (i / 16) % 16,
-  // chunk i % 16 of head h.
-  const bool loader = threadIdx.x < 2 * kPageSize * (kHeadDim / 8);
-  const int ld_which = (threadIdx.x >> 8) & 1, ld_row = (threadIdx.x >> 4) & 15, ld_ch = threadIdx.x & 15;
-  const int64_t ld_off = (int64_t)(ld_which * kPageSize + ld_row) * row_elems + (int64_t)h * kHeadDim + 8 * ld_ch;
-  const int st_off = ld_which * kTile + ld_row * kVStrideP + 8 * ld_ch;
+  // Cooperative step load: 1024 16-byte chunks (K, then V; 32 rows x 16 chunks), kPW*64 threads.
+  constexpr int kChunks = 2 * kKvStep * (kHeadDim / 8);
+  constexpr int kPer = kChunks / (kPW * 64);
 
   // Page ids, 64 per register (lane i: page cbase + i), the next 64 a chunk ahead.
+  const int npages = (nsteps * kKvStep + kPageSize - 1) / kPageSize;
   auto load_ids = [&](int base) -> int {
     const int it = base + lane;
     int pid = -1;
-    if (it < count) pid = a.kv_indices[p0 + it];
+    if (it < npages && it < np) pid = a.kv_indices[p0 + it];
     return (pid >= 0 && (int64_t)pid < a.num_pages) ? pid : -1;
   };
   int cbase = 0;
-  int ids = count > 0 ? load_ids(0) : -1;
-  int ids_next = count > 64 ? load_ids(64) : -1;
-  auto id_of = [&](int q) -> int {  // q in [cbase, cbase + 128)
-    return q - cbase < 64 ? __builtin_amdgcn_readlane(ids, q - cbase) : __builtin_amdgcn_readlane(ids_next, q - cbase - 64);
+  int ids = npages > 0 ? load_ids(0) : -1;
+  int ids_next = npages > 64 ? load_ids(64) : -1;
+  auto id_of = [&](int pg) -> int {  // pg in [cbase, cbase + 128)
+    return pg - cbase < 64 ? __builtin_amdgcn_readlane(ids, pg - cbase) : __builtin_amdgcn_readlane(ids_next, pg - cbase - 64);
   };
-  auto fetch = [&](int q) -> u32x4 {
-    const int pid = q < count ? id_of(q) : -1;
-    if (pid < 0 || !loader) return u32x4{0u, 0u, 0u, 0u};
-    return ld128(a.kv + (int64_t)pid * page_elems + ld_off);
-  };
-  // Pages go through LDS in groups of kGroup: one barrier, one softmax rescale and one buffer
-  // swap per group.  Group gi sits in tiles[gi & 1]; group gi + 1 waits in registers (ring),
-  // its loads issued a whole group earlier.  V rows past kv_len (or of an invalid page) are
-  // stored as zeros: they may hold NaN/Inf and meet p = 0.
-  u32x4 ring[kGroup];
-  auto fetch_group = [&](int gi) {
+  u32x4 ring[kPer];
+  auto fetch = [&](int j) {  // global loads of step j into the ring
+    const int pa = 2 * j < npages ? id_of(2 * j) : -1, pb = 2 * j + 1 < npages ? id_of(2 * j + 1) : -1;
 #pragma unroll
-    for (int pp = 0; pp < kGroup; ++pp) ring[pp] = fetch(gi * kGroup + pp);
-  };
-  auto stage_group = [&](int gi) {
-#pragma unroll
-    for (int pp = 0; pp < kGroup; ++pp) {
-      const int q = gi * kGroup + pp;
-      const bool keep = ld_which == 0 || q * kPageSize + ld_row < kv_len;
-      if (loader && q < count) st128(&tiles[gi & 1][pp][st_off], keep ? ring[pp] : u32x4{0u, 0u, 0u, 0u});
+    for (int r = 0; r < kPer; ++r) {
+      const int ci = threadIdx.x + r * kPW * 64;
+      const int which = ci >> 9, row = (ci >> 4) & 31, c16 = ci & 15;
+      const int pid = (row >> 4) ? pb : pa;
+      ring[r] = pid >= 0 ? ld128(a.kv + (int64_t)pid * page_elems + (int64_t)(which * kPageSize + (row & 15)) * row_elems +
+                                 (int64_t)h * kHeadDim + 8 * c16)
+                         : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  const int ngroups = (count + kGroup - 1) / kGroup;
-  if (ngroups > 0) {
-    fetch_group(0);
-    stage_group(0);
-    if (ngroups > 1) fetch_group(1);
+  auto stage = [&](int j) {  // the ring (step j) into tiles[j & 1]; V rows past kv_len as zeros
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+      const int ci = threadIdx.x + r * kPW * 64;
+      const int which = ci >> 9, row = (ci >> 4) & 31, c16 = ci & 15;
+      const bool keep = which == 0 || j * kKvStep + row < kv_len;
+      st128(&tiles[j & 1][which * kTile + row * kRowP + 8 * c16], keep ? ring[r] : u32x4{0u, 0u, 0u, 0u});
+    }
+  };
+  if (nsteps > 0) {
+    fetch(0);
+    stage(0);
+    if (nsteps > 1) fetch(1);
   }
 
   float m = -INFINITY, l = 0.f;
-  f32x4 acc[8];
+  f32x16 acc[4];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
   const float scale2 = a.sm_scale * kLog2e;
+  // ds_read_b64_tr_b16 of V^T: 16-lane group q16 = lane / 16, t16 = lane % 16 reads rows
+  // (kv) base + t16 / 4 at columns 16 (q16 % 2) + 4 (t16 % 4), and receives its column's four rows.
+  const int q16 = lane >> 4, t16 = lane & 15;
+  const int vtr_off = kTile + (4 * hl + (t16 >> 2)) * kRowP + 16 * (q16 & 1) + 4 * (t16 & 3);
 
-  for (int gi = 0; gi < ngroups; ++gi) {
-    const int j0 = gi * kGroup;
-    __syncthreads();  // group gi is in tiles[gi & 1]; tiles[(gi + 1) & 1] is free
-    if (j0 > 0 && (j0 & 63) == 0) {  // the id window moves on
+  for (int j = 0; j < nsteps; ++j) {
+    __syncthreads();  // step j is in tiles[j & 1]; tiles[(j + 1) & 1] is free
+    if (2 * j >= cbase + 64) {  // the id window moves on (steps cover two pages)
       cbase += 64;
       ids = ids_next;
-      ids_next = cbase + 64 < count ? load_ids(cbase + 64) : -1;
+      ids_next = cbase + 64 < npages ? load_ids(cbase + 64) : -1;
     }
-    if (j0 < wcount) {
-      f32x4 S[kGroup];
+    if (j < wsteps) {
+      const uint16_t *tk = &tiles[j & 1][0];
+      f32x16 S;
 #pragma unroll
-      for (int pp = 0; pp < kGroup; ++pp) S[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 16; ++i) S[i] = 0.f;
 #pragma unroll
-      for (int sk = 0; sk < 4; ++sk)
-#pragma unroll
-        for (int pp = 0; pp < kGroup; ++pp)
-          S[pp] = E::mfma(*reinterpret_cast<const u32x4 *>(&tiles[gi & 1][pp][t * kVStrideP + 32 * sk + 8 * c]),
-                          qf[sk], S[pp]);
-      float x[kGroup][4];
+      for (int ks = 0; ks < 8; ++ks)
+        S = MF::run(*reinterpret_cast<const u32x4 *>(tk + n * kRowP + 16 * ks + 8 * hl), qf[ks], S);
+      // Masks only where the step crosses the wave's first diagonal, kv_len, or a bad page.
+      const int kv0 = j * kKvStep;
+      const bool pages_ok = id_of(2 * j) >= 0 && (2 * j + 1 >= np || id_of(2 * j + 1) >= 0);
+      const bool full = kv0 + kKvStep - 1 <= wpos0 && kv0 + kKvStep <= kv_len && pages_ok;
+      float x[16];
       float pm = -INFINITY;
-      // Below the diagonal of every column and inside kv_len the group needs no element masks
-      // (columns past the wave's tokens compute on zero q and are never written).
-      bool ok[kGroup];
-      bool all_ok = (j0 + kGroup) * kPageSize <= kv_len && (j0 + kGroup) * kPageSize - 1 <= kv_len - qn + tok0;
+      if (full) {
 #pragma unroll
-      for (int pp = 0; pp < kGroup; ++pp) {
-        ok[pp] = j0 + pp < wcount && id_of(j0 + pp) >= 0;  // an id outside the cache contributes nothing
-        all_ok = all_ok && ok[pp];
-      }
-      if (all_ok) {
-#pragma unroll
-        for (int pp = 0; pp < kGroup; ++pp)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            x[pp][r] = S[pp][r] * scale2;
-            pm = fmaxf(pm, x[pp][r]);
-          }
+        for (int i = 0; i < 16; ++i) {
+          x[i] = S[i] * scale2;
+          pm = fmaxf(pm, x[i]);
+        }
       } else {
+        const bool pa_ok = id_of(2 * j) >= 0, pb_ok = 2 * j + 1 < np && id_of(2 * j + 1) >= 0;
 #pragma unroll
-        for (int pp = 0; pp < kGroup; ++pp)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tk = (j0 + pp) * kPageSize + 4 * c + r;
-            x[pp][r] = (ok[pp] && col_ok && tk <= qpos && tk < kv_len) ? S[pp][r] * scale2 : -INFINITY;
-            pm = fmaxf(pm, x[pp][r]);
-          }
+        for (int i = 0; i < 16; ++i) {
+          const int mm = 8 * (i >> 2) + 4 * hl + (i & 3);
+          const int tk_i = kv0 + mm;
+          const bool pg = mm < 16 ? pa_ok : pb_ok;
+          x[i] = (row_ok && pg && tk_i <= qpos && tk_i < kv_len) ? S[i] * scale2 : -INFINITY;
+          pm = fmaxf(pm, x[i]);
+        }
       }
-      const float mn = fmaxf(m, prows4_max(pm));
+      const float mn = fmaxf(m, halves_max(pm));
       const float mref = mn == -INFINITY ? 0.f : mn;
       const float alpha = fast_exp2(m - mref);
       float ps = 0.f;
 #pragma unroll
-      for (int pp = 0; pp < kGroup; ++pp)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          x[pp][r] = fast_exp2(x[pp][r] - mref);
-          ps += x[pp][r];
-        }
-      l = l * alpha + prows4_sum(ps);
+      for (int i = 0; i < 16; ++i) {
+        x[i] = fast_exp2(x[i] - mref);
+        ps += x[i];
+      }
+      l = l * alpha + halves_sum(ps);
       m = mn;
       if (__ballot(alpha != 1.f)) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float al = shfl(alpha, 4 * c + r);
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-          for (int n = 0; n < 8; ++n) acc[n][r] *= al;
-        }
+          for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
       }
+      // P^T chunks: values 8c .. 8c + 7 of this lane, rounded to the KV dtype.
+      u32x4 pc[2];
 #pragma unroll
-      for (int pp = 0; pp < kGroup; ++pp) {
-        if (j0 + pp < wcount) {  // later slots may hold a stale or unset tile
-          ps4_t pa;
+      for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) pa[r] = M16::pack(x[pp][r]);
-          const uint16_t *rd = &tiles[gi & 1][pp][kTile + (4 * c + (t >> 2)) * kVStrideP + 4 * (t & 3)];
+        for (int w = 0; w < 4; ++w)
+          pc[cc][w] = E::from_float(x[8 * cc + 2 * w]) | (E::from_float(x[8 * cc + 2 * w + 1]) << 16);
 #pragma unroll
-          for (int n = 0; n < 8; ++n) {
-            const ps4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 16 * n));
-            acc[n] = M16::run(pa, bv, acc[n]);
-          }
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const uint16_t *rd = tk + vtr_off + 16 * cc * kRowP + 32 * dt;
+          const ps4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)rd);
+          const ps4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 8 * kRowP));
+          u32x4 va;
+          va[0] = (uint32_t)(uint16_t)v0[0] | ((uint32_t)(uint16_t)v0[1] << 16);
+          va[1] = (uint32_t)(uint16_t)v0[2] | ((uint32_t)(uint16_t)v0[3] << 16);
+          va[2] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
+          va[3] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
+          acc[dt] = MF::run(va, pc[cc], acc[dt]);
         }
-      }
     }
-    if (gi + 1 < ngroups) {
-      stage_group(gi + 1);
-      if (gi + 2 < ngroups) fetch_group(gi + 2);
+    if (j + 1 < nsteps) {
+      stage(j + 1);
+      if (j + 2 < nsteps) fetch(j + 2);
     }
   }
 
-  // Normalise and write: lane (c, t) holds O[column 4c + r][16n + t].
+  // Normalise and write: lane l holds O[row l%32][32 dt + 8 (i / 4) + 4 hl + i % 4].
+  if (row_ok) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t *op = a.o + (q0 + tok0 + tt) * a.o_stride_t + (int64_t)(h * G + g) * a.o_stride_h + 4 * hl;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int col = 4 * c + r;
-    const float L = shfl(l, col);
-    const int ctt = col / G, cg = col % G;
-    if (col < TW * G && tok0 + ctt < qn) {
-      uint16_t *op = a.o + (q0 + tok0 + ctt) * a.o_stride_t + (int64_t)(h * G + cg) * a.o_stride_h + t;
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int n = 0; n < 8; ++n) op[16 * n] = (uint16_t)E::from_float(L > 0.f ? acc[n][r] / L : 0.f);
-    }
+      for (int q4 = 0; q4 < 4; ++q4) {
+        uint2 w;
+        w.x = E::from_float(acc[dt][4 * q4] * inv) | (E::from_float(acc[dt][4 * q4 + 1] * inv) << 16);
+        w.y = E::from_float(acc[dt][4 * q4 + 2] * inv) | (E::from_float(acc[dt][4 * q4 + 3] * inv) << 16);
+        *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * q4) = w;
+      }
+    if (a.lse && hl == 0) a.lse[(q0 + tok0 + tt) * a.hq + h * G + g] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
   }
-  if (a.lse && c == 0 && col_ok)
-    a.lse[(q0 + tok0 + tt) * a.hq + h * G + g] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
 }
 
 template <int DT>
 void launch_prefill(const PrefillArgs &a, int G, int max_qo, hipStream_t stream) {
-  const int tw = 16 / G;
-  const dim3 grid((unsigned)ceil_div(max_qo, (int64_t)tw * kPrefillWaves), a.hkv, a.batch);
-  const dim3 block(kPrefillWaves * 64);
+  const int tw = 32 / G;
+  const dim3 grid(a.hkv, (unsigned)ceil_div(max_qo, (int64_t)tw * kPW), a.batch);
+  const dim3 block(kPW * 64);
   switch (G) {
     case 1: hipLaunchKernelGGL((paged_prefill_kernel<DT, 1>), grid, block, 0, stream, a); break;
     case 2: hipLaunchKernelGGL((paged_prefill_kernel<DT, 2>), grid, block, 0, stream, a); break;
@@ -337,6 +341,8 @@ extern "C" DELTA_EXPORT int delta_paged_prefill(const void *q, int64_t q_stride_
     return set_error(DELTA_ERR_INVALID, "%s: null pointer", who);
   if (((uintptr_t)q | (uintptr_t)kv_cache) & 15u || (q_stride_t % 8) || (q_stride_h % 8))
     return set_error(DELTA_ERR_INVALID, "%s: q and kv_cache 16-byte aligned, q strides multiples of 8", who);
+  if (((uintptr_t)o & 7u) || (o_stride_t % 4) || (o_stride_h % 4))
+    return set_error(DELTA_ERR_INVALID, "%s: o 8-byte aligned with strides in multiples of 4", who);
   if (num_pages <= 0 || kv_indices_len < 0) return set_error(DELTA_ERR_INVALID, "%s: empty cache", who);
   PrefillArgs a;
   a.q = (const uint16_t *)q;

@@ -203,7 +203,8 @@ int delta_paged_decode_subset_append(const delta_decode_append_t *append, const 
  * qo_indptr[b] .. qo_indptr[b+1]; the cache already holds them (update_kv runs first,
  * model.py:413-418), so token i of row b sits at kv_len_b - qo_len_b + i and attends
  * tokens 0 .. that position.  lse [nnz, num_qo_heads] or NULL.  max_qo_len must be
- * >= every qo_len_b (it sizes the grid).  No workspace. */
+ * >= every qo_len_b (it sizes the grid).  o 8-byte aligned with strides in multiples of 4.
+ * No workspace. */
 int delta_paged_prefill(const void *q, int64_t q_stride_t, int64_t q_stride_h,
                         const void *kv_cache, int64_t num_pages, const int32_t *qo_indptr,
                         const int32_t *kv_indptr, const int32_t *kv_indices,

@@ -8,32 +8,43 @@
 // Work decomposition (flash-attention style, on 32x32 MFMA tiles): a block is kPW waves of one
 // (row, kv head) and a run of consecutive query tokens; each wave owns 32 query rows, the
 // (token, q head) pairs of TW = 32 / G tokens (rows past TW * G idle when G does not divide
-// 32), with its q in registers.  The block sweeps the row's kv tokens 32 at a time (two pages)
-// up to its last token's position: each step's K and V (8 KiB each for one head) are loaded
-// once per block, 16 bytes per thread, into double-buffered padded LDS tiles (the next step in
-// flight in registers) and read by every wave.  Per wave and step:
+// 32), with its q in registers.  The block sweeps the row's kv tokens 64 at a time (four pages,
+// two 32-token sub-tiles) up to its last token's position: each step's K and V (16 KiB each for
+// one head) are loaded once per block, 16 bytes per thread, into double-buffered padded LDS
+// tiles (the next step in flight in registers) and read by every wave.  Per wave and sub-tile:
 //   S^T = K Q^T : 8 v_mfma_f32_32x32x16 over d, A = the tile's K rows from LDS
 //         (lane%32 = kv token, d in 16 ks + 8 (lane / 32) + [0, 8)), B = the wave's q (same d
 //         split, n = lane%32 = query row); D leaves lane l with its row n = l%32 and the 16 kv
 //         tokens m_i = 8 (i / 4) + 4 (l / 32) + i % 4;
-//   softmax: online per row in the log2 domain, lane-local but for one exchange with lane
-//         l ^ 32 (the row's other 16 tokens); causal and kv_len masks only on tiles that need
-//         them;
+//   softmax: online per row in the log2 domain over the step's 32 scores of the lane, one
+//         exchange with lane l ^ 32 (the row's other half) for the maximum; the row sum stays
+//         per half until the end.  The reference maximum moves only when a score passes it by
+//         more than 8 (log2), so the accumulators are rescaled on few steps; causal and kv_len
+//         masks only on steps that need them;
 //   O^T += V^T P^T : 8 v_mfma_f32_32x32x16 (4 d tiles x 2 kv chunks), B = the lane's own P in
 //         its D order (chunk c = values 8c..8c+7, i.e. kv tokens 16c + 4 (l/32) + {0..3, 8..11}),
-//         A = V^T read from the padded tile with ds_read_b64_tr_b16 in that same kv order;
-//         lane l accumulates O[row l%32][d = 32 dt + 8 (i / 4) + 4 (l / 32) + i % 4].
+//         packed by v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, A = V^T read from the padded tile
+//         with ds_read_b64_tr_b16 in that same kv order; lane l accumulates
+//         O[row l%32][d = 32 dt + 8 (i / 4) + 4 (l / 32) + i % 4].
+// LDS row pitches: K rows are read 16 bytes per lane, 32 rows at once (136 elements = 68 banks
+// apart: each 16-lane group covers the 64 banks once); V is read transposed, 4 rows x 16
+// columns per 16-lane group and two groups per pass (160 elements: consecutive rows 16 banks
+// apart, so a pass covers 64 banks once; at 136 consecutive rows share 4 banks: 2-way conflicts).
 // Blocks run heaviest first (the last query tiles attend the most tokens) and blockIdx.x is the
 // kv head, so the blocks of one head land on the same XCD (blocks go to the XCDs round robin)
-// and share its L2 for that head's K/V.  Page ids are preloaded 64 per register.  No merge.
+// and share its L2 for that head's K/V.  Page ids are preloaded 64 per register, with a bit
+// mask of the invalid ones.  No merge.
 #include "delta_common.h"
 
 namespace delta {
 namespace {
 
 constexpr int kPW = 8;          // waves per block (each 32 query rows)
-constexpr int kKvStep = 32;     // kv tokens per step (two pages)
-constexpr int kRowP = 136;      // padded LDS tile row (elements): conflict-free 16-byte row reads
+constexpr int kSub = 2;         // 32-token sub-tiles per step
+constexpr int kKvStep = 32 * kSub;  // kv tokens per step
+constexpr int kPgStep = kKvStep / 16;  // pages per step
+constexpr int kRowP = 136;      // padded K tile row (elements): conflict-free 16-byte row reads
+constexpr int kRowPV = 160;     // padded V tile row (elements), read transposed
 
 struct PrefillArgs {
   const uint16_t *q;
@@ -73,6 +84,22 @@ struct Mfma32<DELTA_FP16> {
   }
 };
 
+// Two floats -> two packed 16-bit values, round to nearest even (one v_cvt_pk_* on gfx950).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float x, float y);
+template <>
+__device__ __forceinline__ uint32_t pack2<DELTA_BF16>(float x, float y) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x, y}), b2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<DELTA_FP16>(float x, float y) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x, y}), h2));
+}
+
 // max / sum of a value and its copy in lane l ^ 32
 __device__ __forceinline__ float halves_max(float v) {
   auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -90,9 +117,10 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   using MF = Mfma32<DT>;
   constexpr int TW = 32 / G;                  // query tokens per wave
   constexpr int BT = kPW * TW;                // query tokens per block
-  constexpr int kTile = kKvStep * kRowP;      // one K or V tile (elements)
+  constexpr int kTile = kKvStep * kRowP;      // the K tile (elements); the V tile follows
+  constexpr int kTileV = kKvStep * kRowPV;
   // Two step buffers, each K then V (padded rows), shared by the block's waves.
-  __shared__ uint16_t tiles[2][2 * kTile];
+  __shared__ uint16_t tiles[2][kTile + kTileV];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hl = lane >> 5, n = lane & 31;
@@ -120,9 +148,12 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   const int qpos = kv_len - qn + tok0 + tt;  // attends tokens 0..qpos
   u32x4 qf[8];  // B operand of S^T = K Q^T: d = 16 ks + 8 hl + [0, 8)
   if (row_ok) {
+    // With a negative scale q's signs are flipped (S of -q is exactly -S; the scale below is then
+    // positive).  The xor also makes the loads complete here, before the kv loop.
+    const uint32_t flip = a.sm_scale < 0.f ? 0x80008000u : 0u;
     const uint16_t *qp = a.q + (q0 + tok0 + tt) * a.q_stride_t + (int64_t)(h * G + g) * a.q_stride_h + 8 * hl;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = ld128(qp + 16 * ks);
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = ld128(qp + 16 * ks) ^ u32x4{flip, flip, flip, flip};
   } else {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = u32x4{0u, 0u, 0u, 0u};
@@ -142,7 +173,8 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
-  // Cooperative step load: 1024 16-byte chunks (K, then V; 32 rows x 16 chunks), kPW*64 threads.
+  // Cooperative step load: 2 * kKvStep * 16 chunks of 16 bytes (K, then V; rows x 16 chunks) over
+  // kPW * 64 threads.
   constexpr int kChunks = 2 * kKvStep * (kHeadDim / 8);
   constexpr int kPer = kChunks / (kPW * 64);
 
@@ -154,20 +186,29 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
     if (it < npages && it < np) pid = a.kv_indices[p0 + it];
     return (pid >= 0 && (int64_t)pid < a.num_pages) ? pid : -1;
   };
+  // Invalid page ids (negative or past the cache) of the current window, one bit per page.
+  const int lim = npages < np ? npages : np;
+  auto bad_of = [&](int id, int base) -> uint64_t { return __ballot(base + lane < lim && id < 0); };
   int cbase = 0;
   int ids = npages > 0 ? load_ids(0) : -1;
   int ids_next = npages > 64 ? load_ids(64) : -1;
+  uint64_t bad = bad_of(ids, 0);
   auto id_of = [&](int pg) -> int {  // pg in [cbase, cbase + 128)
     return pg - cbase < 64 ? __builtin_amdgcn_readlane(ids, pg - cbase) : __builtin_amdgcn_readlane(ids_next, pg - cbase - 64);
   };
   u32x4 ring[kPer];
   auto fetch = [&](int j) {  // global loads of step j into the ring
-    const int pa = 2 * j < npages ? id_of(2 * j) : -1, pb = 2 * j + 1 < npages ? id_of(2 * j + 1) : -1;
+    int pids[kPgStep];
+#pragma unroll
+    for (int p = 0; p < kPgStep; ++p) pids[p] = kPgStep * j + p < npages ? id_of(kPgStep * j + p) : -1;
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
       const int ci = threadIdx.x + r * kPW * 64;
-      const int which = ci >> 9, row = (ci >> 4) & 31, c16 = ci & 15;
-      const int pid = (row >> 4) ? pb : pa;
+      const int which = ci / (kKvStep * 16), row = (ci >> 4) % kKvStep, c16 = ci & 15;
+      int pid = pids[0];
+#pragma unroll
+      for (int p = 1; p < kPgStep; ++p)
+        if ((row >> 4) == p) pid = pids[p];
       ring[r] = pid >= 0 ? ld128(a.kv + (int64_t)pid * page_elems + (int64_t)(which * kPageSize + (row & 15)) * row_elems +
                                  (int64_t)h * kHeadDim + 8 * c16)
                          : u32x4{0u, 0u, 0u, 0u};
@@ -177,9 +218,9 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
       const int ci = threadIdx.x + r * kPW * 64;
-      const int which = ci >> 9, row = (ci >> 4) & 31, c16 = ci & 15;
+      const int which = ci / (kKvStep * 16), row = (ci >> 4) % kKvStep, c16 = ci & 15;
       const bool keep = which == 0 || j * kKvStep + row < kv_len;
-      st128(&tiles[j & 1][which * kTile + row * kRowP + 8 * c16], keep ? ring[r] : u32x4{0u, 0u, 0u, 0u});
+      st128(&tiles[j & 1][(which ? kTile + row * kRowPV : row * kRowP) + 8 * c16], keep ? ring[r] : u32x4{0u, 0u, 0u, 0u});
     }
   };
   if (nsteps > 0) {
@@ -194,61 +235,90 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
-  const float scale2 = a.sm_scale * kLog2e;
+  const float scale2 = fabsf(a.sm_scale) * kLog2e;
   // ds_read_b64_tr_b16 of V^T: 16-lane group q16 = lane / 16, t16 = lane % 16 reads rows
   // (kv) base + t16 / 4 at columns 16 (q16 % 2) + 4 (t16 % 4), and receives its column's four rows.
   const int q16 = lane >> 4, t16 = lane & 15;
-  const int vtr_off = kTile + (4 * hl + (t16 >> 2)) * kRowP + 16 * (q16 & 1) + 4 * (t16 & 3);
+  const int vtr_off = kTile + (4 * hl + (t16 >> 2)) * kRowPV + 16 * (q16 & 1) + 4 * (t16 & 3);
 
   for (int j = 0; j < nsteps; ++j) {
     __syncthreads();  // step j is in tiles[j & 1]; tiles[(j + 1) & 1] is free
-    if (2 * j >= cbase + 64) {  // the id window moves on (steps cover two pages)
+    if (kPgStep * j >= cbase + 64) {  // the id window moves on
       cbase += 64;
       ids = ids_next;
+      bad = bad_of(ids, cbase);
       ids_next = cbase + 64 < npages ? load_ids(cbase + 64) : -1;
     }
     if (j < wsteps) {
       const uint16_t *tk = &tiles[j & 1][0];
-      f32x16 S;
+      f32x16 S[kSub];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) S[i] = 0.f;
+      for (int sb = 0; sb < kSub; ++sb)
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        S = MF::run(*reinterpret_cast<const u32x4 *>(tk + n * kRowP + 16 * ks + 8 * hl), qf[ks], S);
+        for (int i = 0; i < 16; ++i) S[sb][i] = 0.f;
+      // K fragments one ks ahead of the MFMAs that use them.
+      auto kfrag = [&](int sb, int ks) { return *reinterpret_cast<const u32x4 *>(tk + (32 * sb + n) * kRowP + 16 * ks + 8 * hl); };
+      u32x4 kc[kSub];
+#pragma unroll
+      for (int sb = 0; sb < kSub; ++sb) kc[sb] = kfrag(sb, 0);
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        u32x4 kn[kSub];
+        if (ks < 7) {
+#pragma unroll
+          for (int sb = 0; sb < kSub; ++sb) kn[sb] = kfrag(sb, ks + 1);
+        }
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb) S[sb] = MF::run(kc[sb], qf[ks], S[sb]);
+        if (ks < 7) {
+#pragma unroll
+          for (int sb = 0; sb < kSub; ++sb) kc[sb] = kn[sb];
+        }
+      }
       // Masks only where the step crosses the wave's first diagonal, kv_len, or a bad page.
       const int kv0 = j * kKvStep;
-      const bool pages_ok = id_of(2 * j) >= 0 && (2 * j + 1 >= np || id_of(2 * j + 1) >= 0);
+      const int poff = kPgStep * j - cbase;  // the step's pages: bits poff .. poff + kPgStep - 1
+      const bool pages_ok = ((bad >> poff) & ((1ull << kPgStep) - 1)) == 0;
       const bool full = kv0 + kKvStep - 1 <= wpos0 && kv0 + kKvStep <= kv_len && pages_ok;
-      float x[16];
+      // Row maxima on the raw scores (the scale is positive, so it commutes with max), then
+      // x = S * scale - m as one fma.  m is the row's reference maximum: it moves only when a
+      // score exceeds it by more than 8 (a factor of 2^8), so the exponentials stay <= 256 and the
+      // accumulators are rescaled only on those steps.
+      constexpr int NX = 16 * kSub;
+      float x[NX];
       float pm = -INFINITY;
       if (full) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          x[i] = S[i] * scale2;
+        for (int i = 0; i < NX; ++i) {
+          x[i] = S[i >> 4][i & 15];
           pm = fmaxf(pm, x[i]);
         }
       } else {
-        const bool pa_ok = id_of(2 * j) >= 0, pb_ok = 2 * j + 1 < np && id_of(2 * j + 1) >= 0;
+        bool pg_ok[kPgStep];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int mm = 8 * (i >> 2) + 4 * hl + (i & 3);
+        for (int p = 0; p < kPgStep; ++p) pg_ok[p] = ((bad >> (poff + p)) & 1ull) == 0;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+          const int mm = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * hl + (i & 3);
           const int tk_i = kv0 + mm;
-          const bool pg = mm < 16 ? pa_ok : pb_ok;
-          x[i] = (row_ok && pg && tk_i <= qpos && tk_i < kv_len) ? S[i] * scale2 : -INFINITY;
+          x[i] = (row_ok && pg_ok[mm >> 4] && tk_i <= qpos && tk_i < kv_len) ? S[i >> 4][i & 15] : -INFINITY;
           pm = fmaxf(pm, x[i]);
         }
       }
-      const float mn = fmaxf(m, halves_max(pm));
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = fast_exp2(m - mref);
+      const float smax = halves_max(pm) * scale2;
+      float alpha = 1.f;
+      if (smax > m + 8.f) {  // also the first finite score of the row (m = -inf)
+        alpha = fast_exp2(m - smax);
+        m = smax;
+      }
+      const float nm = m == -INFINITY ? 0.f : -m;
       float ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        x[i] = fast_exp2(x[i] - mref);
+      for (int i = 0; i < NX; ++i) {
+        x[i] = fast_exp2(fmaf(x[i], scale2, nm));
         ps += x[i];
       }
-      l = l * alpha + halves_sum(ps);
-      m = mn;
+      l = l * alpha + ps;  // this half's tokens; the halves are summed once at the end
       if (__ballot(alpha != 1.f)) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
@@ -256,19 +326,19 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
           for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
       }
       // P^T chunks: values 8c .. 8c + 7 of this lane, rounded to the KV dtype.
-      u32x4 pc[2];
+      u32x4 pc[2 * kSub];
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc)
+      for (int cc = 0; cc < 2 * kSub; ++cc)
 #pragma unroll
         for (int w = 0; w < 4; ++w)
-          pc[cc][w] = E::from_float(x[8 * cc + 2 * w]) | (E::from_float(x[8 * cc + 2 * w + 1]) << 16);
+          pc[cc][w] = pack2<DT>(x[8 * cc + 2 * w], x[8 * cc + 2 * w + 1]);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const uint16_t *rd = tk + vtr_off + 16 * cc * kRowP + 32 * dt;
+        for (int cc = 0; cc < 2 * kSub; ++cc) {
+          const uint16_t *rd = tk + vtr_off + 16 * cc * kRowPV + 32 * dt;
           const ps4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)rd);
-          const ps4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 8 * kRowP));
+          const ps4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 8 * kRowPV));
           u32x4 va;
           va[0] = (uint32_t)(uint16_t)v0[0] | ((uint32_t)(uint16_t)v0[1] << 16);
           va[1] = (uint32_t)(uint16_t)v0[2] | ((uint32_t)(uint16_t)v0[3] << 16);
@@ -284,6 +354,7 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   }
 
   // Normalise and write: lane l holds O[row l%32][32 dt + 8 (i / 4) + 4 hl + i % 4].
+  l = halves_sum(l);
   if (row_ok) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t *op = a.o + (q0 + tok0 + tt) * a.o_stride_t + (int64_t)(h * G + g) * a.o_stride_h + 4 * hl;
@@ -292,8 +363,8 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         uint2 w;
-        w.x = E::from_float(acc[dt][4 * q4] * inv) | (E::from_float(acc[dt][4 * q4 + 1] * inv) << 16);
-        w.y = E::from_float(acc[dt][4 * q4 + 2] * inv) | (E::from_float(acc[dt][4 * q4 + 3] * inv) << 16);
+        w.x = pack2<DT>(acc[dt][4 * q4] * inv, acc[dt][4 * q4 + 1] * inv);
+        w.y = pack2<DT>(acc[dt][4 * q4 + 2] * inv, acc[dt][4 * q4 + 3] * inv);
         *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * q4) = w;
       }
     if (a.lse && hl == 0) a.lse[(q0 + tok0 + tt) * a.hq + h * G + g] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;

@@ -575,6 +575,38 @@ def test_paged_prefill_matches_oracle(hq, hkv, dtype):
     assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_paged_prefill_long_rows_growing_scores(sign):
+    """Prompts of 1100 and 300 tokens (more than 64 pages: the page-id window moves), K scaled
+    up along each row so the running maximum keeps growing (the accumulators are rescaled many
+    times), and a negative scale (q's signs flipped in the kernel): o and lse against the oracle.
+    The scores are peaked, so o is close to single V rows; V is halved (exact) so that o's own
+    bf16 rounding stays well inside the 2e-2 bar."""
+    hq, hkv = 32, 8
+    kv_lens, qo = [1100, 700], [1100, 300]
+    c = make_case(batch=2, hq=hq, hkv=hkv, kv_lens=kv_lens, seed=33, page_order="randperm", k=4, L=2,
+                  dtype=torch.bfloat16)
+    cache = c.kv_cache.float()
+    for b, n in enumerate(kv_lens):
+        pages = c.kv_indices[int(c.kv_indptr[b]):int(c.kv_indptr[b + 1])].long()
+        ramp = 1.0 + torch.arange(len(pages) * 16, dtype=torch.float32).view(-1, 16) / 48.0
+        cache[pages, 0] *= ramp[:, :, None, None]
+        cache[pages, 1] *= 0.5
+    cache = cache.to(torch.bfloat16)
+    gen = torch.Generator().manual_seed(34)
+    q = torch.randn(sum(qo), hq, 128, generator=gen).to(torch.bfloat16)
+    qo_indptr = torch.tensor([0, qo[0], qo[0] + qo[1]], dtype=torch.int32)
+    scale = sign / 128 ** 0.5
+    lse = torch.empty(sum(qo), hq, device=DEV)
+    o = K.paged_prefill(q.to(DEV), cache.to(DEV), qo_indptr.to(DEV), c.kv_indptr.to(DEV), c.kv_indices.to(DEV),
+                        c.kv_last_page_len.to(DEV), max_qo_len=max(qo), sm_scale=scale, lse=lse)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = O.paged_prefill_attention(q, qo_indptr, cache, c.kv_indptr, c.kv_indices,
+                                               c.kv_last_page_len, scale)
+    assert_attn_close(o, o_ref, f"long prefill, scale sign {sign}")
+    assert torch.allclose(lse.cpu(), lse_ref, atol=2e-3, rtol=1e-4)
+
+
 @pytest.mark.parametrize("hq,hkv,dtype,llama31,batch", [
     (32, 8, torch.bfloat16, False, 6),    # page-major split launches
     (32, 8, torch.bfloat16, True, 36),    # head-major subset (36 rows x 8 kv heads)

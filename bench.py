@@ -280,8 +280,10 @@ def prefill_roofline(torch, n: int = 8192):
     q = torch.randn(n, 32, 128, device="cuda:0", dtype=torch.bfloat16)
     qo = torch.tensor([0, n], dtype=torch.int32, device="cuda:0")
     out = torch.empty_like(q)
-    us = graph_timed(torch, [lambda: K.paged_prefill(q, c.kv_cache, qo, c.kv_indptr, c.kv_indices,
-                                                     c.kv_last_page_len, max_qo_len=n, out=out)] * 4, 1)
+    run = lambda: K.paged_prefill(q, c.kv_cache, qo, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_qo_len=n,
+                                  out=out)
+    warm_up(torch, run, 0.1)  # launches ramp from ~0.82 to ~0.62 ms over the first ~30 ms
+    us = graph_timed(torch, [run] * 4, 1)
     flops = 4 * (n * (n + 1) / 2) * 32 * 128
     del c, q, out
     torch.cuda.empty_cache()
@@ -566,6 +568,8 @@ def main():
                     help="only the CPU baseline (runs without a GPU)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel roofline loop and a copy of known size (for rocprofv3 --pmc runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill kernel measurement (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -596,6 +600,12 @@ def main():
                     log(f"  config {cfg} {k}: {v['us']} us, {v['GB_s']} GB/s")
             torch.cuda.empty_cache()
         print(json.dumps({"kernels_other_configs": out}), flush=True)
+        return
+    if args.prefill_only:
+        prefill = prefill_roofline(torch)
+        log(f"  paged_prefill_kernel: {prefill['us']} us, {prefill['TFLOP_s']} TFLOP/s "
+            f"({100 * prefill['frac']:.1f}% of bf16 MFMA peak)")
+        print(json.dumps({"prefill": prefill}), flush=True)
         return
     if args.kernels_only:
         kern = kernel_roofline(torch, args.kernel_reps)

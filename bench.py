@@ -237,6 +237,15 @@ def kernel_roofline(torch, reps: int = 60, n_rot: int = 30):
                                                              logits_dump=d, append=a)),
         ntok_full * 2 * row_kv + qo + B * mp * 4 + ntok_full * hq * 4 + ap_bytes,
         "the planner launch of a decode step (delta_paged_decode_append with a dump)")
+    if K.paged_decode_scores_supported(B, hq, hkv, mp, True):
+        # the per-token maxima are written once and read once by the page-sum kernel
+        add("planner on chip <ROPE> (plan_tokmax + tokmax_score)",
+            timed_ap(lambda c, d, l, s, i, p, a: K.paged_decode_scores(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                                                        c.kv_last_page_len, max_pages_per_row=mp,
+                                                                        lse=l, scores=s, append=a)),
+            ntok_full * 2 * row_kv + qo + B * mp * 4 + ap_bytes + 2 * ntok_full * hkv * 4 + B * mp * 4,
+            "the planner launch pair of a decode step with its logits on chip (delta_paged_decode_scores_append): "
+            "K+V of all pages, q, o, page ids, the token's k/v, per-token maxima written and summed, scores")
     add("paged_decode_subset_kernel",
         timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
                                                        max_pages_per_row=c.k, subset=True)),

@@ -66,6 +66,14 @@ SIGNATURES = {
         _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P,
         _P, c_int64, c_int64, _P, c_int64,
         c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),
+    "delta_paged_decode_scores_supported": (c_int, [c_int, c_int, c_int, c_int, c_int]),
+    "delta_paged_decode_scores_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "delta_paged_decode_scores": (c_int, [
+        _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int64,
+        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),
+    "delta_paged_decode_scores_append": (c_int, [
+        _AP, _P, c_int64, c_int64, _P, c_int64, _P, _P, c_int64, _P, _P, c_int64, c_int64, _P, _P, c_int64,
+        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P, c_size_t, _P]),
     "delta_select_pages": (c_int, [
         _P, c_int64, _P, _P, c_int64, c_int, c_int, c_int, _P, c_int, c_float, c_int, _P,
         _P, c_int64, _P, _P]),

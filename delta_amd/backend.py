@@ -222,8 +222,13 @@ class LMBackend:
                                device=dev)
         self.lse = torch.zeros((B, hq), dtype=torch.float32, device=dev)
         self.page_scores = torch.zeros((B, self.pages_per_slot), dtype=torch.float32, device=dev)
+        # The planner keeps its logits on chip (attention and page scores in one pass, no dump)
+        # where the shape allows it; the dump path stays for the selection parity check.
+        self.plan_scores_on_chip = (K.paged_decode_scores_supported(B, hq, hkv, self.pages_per_slot, True)
+                                    and K.paged_decode_scores_supported(B, hq, hkv, self.pages_per_slot, False))
         ws = max(K.decode_workspace_bytes(B, hq, hkv, self.pages_per_slot),
-                 K.decode_workspace_bytes(B, hq, hkv, self.k_eff), 256)
+                 K.decode_workspace_bytes(B, hq, hkv, self.k_eff),
+                 K.paged_decode_scores_workspace_bytes(B, hkv, self.pages_per_slot), 256)
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
         self._pinned_tokens = torch.zeros(B, dtype=torch.long).pin_memory()
         with torch.device(dev):
@@ -274,18 +279,27 @@ class LMBackend:
                               self._step.kv_last, max_pages_per_row=self.k_eff, workspace=self.workspace,
                               subset=True, append=append)
 
+    def _plan_on_chip(self) -> bool:
+        return self.plan_scores_on_chip and not self.enable_delta_debug_page_selection_parity
+
     def attn_plan(self, q, kv_cache, append=None):
-        """Planner layer: full attention + logits dump, page scores, v2 selection into the subset CSR."""
+        """Planner layer: full attention, page scores (logits kept on chip, or through the
+        logits dump), v2 selection into the subset CSR."""
         if not (self.enable_selective_cache and self._decode_mode()):
             return self.attn_full(q, kv_cache, append=append)
         st = self._step
         sel = self.page_selector
         B = q.shape[0]
-        o = K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                           max_pages_per_row=st.max_pages, lse=self.lse, logits_dump=self.dump,
-                           workspace=self.workspace, append=append)
-        K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
-                                  scores=self.page_scores, batch=B, workspace=self.workspace)
+        if self._plan_on_chip():
+            o, _ = K.paged_decode_scores(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
+                                         max_pages_per_row=st.max_pages, lse=self.lse, scores=self.page_scores,
+                                         workspace=self.workspace, append=append)
+        else:
+            o = K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
+                               max_pages_per_row=st.max_pages, lse=self.lse, logits_dump=self.dump,
+                               workspace=self.workspace, append=append)
+            K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
+                                      scores=self.page_scores, batch=B, workspace=self.workspace)
         K.select_pages(self.page_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,
                        pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
                        use_subset=self.use_subset_flag, out_indices=sel.paged_subset_kv_indices,
@@ -361,10 +375,13 @@ class LMBackend:
 
     # --------------------------------------------------------- planner scores
     def _compute_page_scores_from_attention_buffer(self) -> torch.Tensor:
-        """del3_legacy_softmax page scores of the last decode step's planner dump
+        """del3_legacy_softmax page scores of the last decode step's planner layer
         (backend.py:887-913): fp32 ``[batch, pages_per_slot]``, ``score[b, j] = sum over the
-        tokens t of page j of max_h softmax_t(dump[b, h, :])``; pages past a row's end score 0.
-        Uses the planner's lse for the normaliser, as the fused path does."""
+        tokens t of page j of max_h softmax_t(logits[b, h, :])``; pages past a row's end score 0.
+        From the dump with the planner's lse for the normaliser, or, when the planner kept its
+        logits on chip, the scores it wrote."""
+        if self._plan_on_chip():
+            return self.page_scores
         st = self._decode_csr()
         return K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
                                          scores=self.page_scores, batch=self.batch_size, workspace=self.workspace)
@@ -372,6 +389,9 @@ class LMBackend:
     def _compute_page_scores_reference(self) -> torch.Tensor:
         """The same scores from the dump alone (softmax normaliser recomputed, no lse): the
         reference's torch-score path used by its selection parity check (backend.py:906-909)."""
+        if self._plan_on_chip():
+            raise RuntimeError("the planner kept its logits on chip (no dump); set plan_scores_on_chip = False "
+                               "or enable delta_debug_page_selection_parity for the dump")
         st = self._decode_csr()
         return K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot,
                                          batch=self.batch_size)

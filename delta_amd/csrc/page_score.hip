@@ -28,6 +28,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
                const delta_decode_append_t *ap);
 int decode_num_splits(int batch, int hkv, int max_pages);
 bool tokmax_fits(int batch, int hkv, int G, int max_pages);
+bool plan_tokmax_fits(int batch, int hkv, int G, int max_pages, bool rope);
 size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc);
 
 namespace {
@@ -252,4 +253,94 @@ extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, 
   if (rc) return rc;
   return launch_scores(logits_dump, dump_stride_b, dump_stride_h, lse_ws, kv_indptr, kv_last_page_len, scores,
                        score_stride, batch, num_qo_heads, max_pages, st, who);
+}
+
+// The planner layer in one launch pair: attention (o, lse) with the row's logits kept in LDS,
+// written as per-(kv head, token) maxima, then the page sums -- the same scores as a logits
+// dump followed by delta_page_scores_from_logits, without the dump's HBM round trip.
+namespace delta {
+namespace {
+int run_decode_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *kv_cache,
+                      int64_t num_pages, const int32_t *kv_indptr, const int32_t *kv_indices,
+                      int64_t kv_indices_len, const int32_t *kv_last_page_len, void *o, int64_t o_stride_b,
+                      int64_t o_stride_h, float *lse, float *scores, int64_t score_stride, int batch,
+                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype, float sm_scale, int max_pages,
+                      void *workspace, size_t workspace_bytes, hipStream_t st, const char *who,
+                      const delta_decode_append_t *ap) {
+  clear_error();
+  if (batch <= 0) return DELTA_OK;
+  if (max_pages <= 0) return set_error(DELTA_ERR_INVALID, "%s: max_pages_per_row must be positive", who);
+  if (!scores || !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
+    return set_error(DELTA_ERR_INVALID, "%s: num_qo_heads must be a multiple of num_kv_heads", who);
+  if (num_qo_heads > kMaxHeads) return set_error(DELTA_ERR_INVALID, "%s: too many heads", who);
+  if (score_stride < max_pages) return set_error(DELTA_ERR_INVALID, "%s: score_stride < max_pages", who);
+  if (!plan_tokmax_fits(batch, num_kv_heads, num_qo_heads / num_kv_heads, max_pages, ap != nullptr))
+    return set_error(DELTA_ERR_INVALID, "%s: this shape does not fit the on-chip planner "
+                     "(delta_paged_decode_scores_supported); use the logits dump", who);
+  const size_t need = delta_paged_decode_scores_workspace_bytes(batch, num_kv_heads, max_pages);
+  if (!workspace || workspace_bytes < need)
+    return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
+  if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
+  float *tm = (float *)workspace;
+  const int64_t sh = (int64_t)max_pages * kPageSize, sb = (int64_t)num_kv_heads * sh;
+  int rc = run_decode(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices, kv_indices_len,
+                      kv_last_page_len, o, o_stride_b, o_stride_h, lse, tm, sb, sh, batch, num_qo_heads,
+                      num_kv_heads, head_dim, dtype, sm_scale, max_pages, /*kAttnTokmax*/ 5, nullptr, 0, st, who,
+                      ap);
+  if (rc) return rc;
+  dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
+  hipLaunchKernelGGL(tokmax_score_kernel, grid, dim3(kScoreThreads), 0, st, tm, sb, sh, num_kv_heads, kv_indptr,
+                     kv_last_page_len, scores, score_stride, max_pages);
+  return check_launch(who);
+}
+}  // namespace
+}  // namespace delta
+
+extern "C" DELTA_EXPORT int delta_paged_decode_scores_supported(int batch, int num_qo_heads, int num_kv_heads,
+                                                                int max_pages_per_row, int with_append) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads) return 0;
+  if (num_qo_heads / num_kv_heads > delta::kMaxGroup || num_kv_heads > delta::kMaxWaves) return 0;
+  return delta::plan_tokmax_fits(batch, num_kv_heads, num_qo_heads / num_kv_heads, max_pages_per_row,
+                                 with_append != 0) ? 1 : 0;
+}
+
+extern "C" DELTA_EXPORT size_t delta_paged_decode_scores_workspace_bytes(int batch, int num_kv_heads,
+                                                                         int max_pages_per_row) {
+  // The per-(kv head, token) maxima [batch][hkv][max_pages * 16].
+  if (batch <= 0 || num_kv_heads <= 0 || max_pages_per_row <= 0) return 0;
+  return ((size_t)batch * num_kv_heads * max_pages_per_row * delta::kPageSize * sizeof(float) + 255) & ~(size_t)255;
+}
+
+extern "C" DELTA_EXPORT int delta_paged_decode_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                                                      const void *kv_cache, int64_t num_pages,
+                                                      const int32_t *kv_indptr, const int32_t *kv_indices,
+                                                      int64_t kv_indices_len, const int32_t *kv_last_page_len,
+                                                      void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse,
+                                                      float *scores, int64_t score_stride, int batch,
+                                                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                                                      float sm_scale, int max_pages_per_row, void *workspace,
+                                                      size_t workspace_bytes, delta_stream_t stream) {
+  return delta::run_decode_scores(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices,
+                                  kv_indices_len, kv_last_page_len, o, o_stride_b, o_stride_h, lse, scores,
+                                  score_stride, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
+                                  max_pages_per_row, workspace, workspace_bytes, (hipStream_t)stream,
+                                  "delta_paged_decode_scores", nullptr);
+}
+
+extern "C" DELTA_EXPORT int delta_paged_decode_scores_append(
+    const delta_decode_append_t *append, const void *q, int64_t q_stride_b, int64_t q_stride_h, void *kv_cache,
+    int64_t num_pages, const int32_t *kv_indptr, const int32_t *kv_indices, int64_t kv_indices_len,
+    const int32_t *kv_last_page_len, void *o, int64_t o_stride_b, int64_t o_stride_h, float *lse, float *scores,
+    int64_t score_stride, int batch, int num_qo_heads, int num_kv_heads, int head_dim, int dtype, float sm_scale,
+    int max_pages_per_row, void *workspace, size_t workspace_bytes, delta_stream_t stream) {
+  if (!append) {
+    delta::clear_error();
+    return delta::set_error(DELTA_ERR_INVALID, "delta_paged_decode_scores_append: null append");
+  }
+  return delta::run_decode_scores(q, q_stride_b, q_stride_h, kv_cache, num_pages, kv_indptr, kv_indices,
+                                  kv_indices_len, kv_last_page_len, o, o_stride_b, o_stride_h, lse, scores,
+                                  score_stride, batch, num_qo_heads, num_kv_heads, head_dim, dtype, sm_scale,
+                                  max_pages_per_row, workspace, workspace_bytes, (hipStream_t)stream,
+                                  "delta_paged_decode_scores_append", append);
 }

@@ -103,6 +103,10 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs &a, int b) {
 constexpr int kVStride = 136;
 constexpr int kVTile = kPageSize * kVStride;  // elements per wave
 
+// V rows a lane loads in the register-held P.V path (the planner with on-chip logits): lane
+// group c = lane / 16 holds the tokens of its P.V k slots, tok = 2c + v_row(i), i = 0..3.
+__device__ __forceinline__ constexpr int v_row(int i) { return 8 * (i >> 1) + (i & 1); }
+
 template <int DT>
 struct Mfma16;
 template <>
@@ -172,10 +176,18 @@ constexpr int dump_slots() {
   return WITH_V ? (G <= 4 ? 16 : 8) : (G <= 4 ? 32 : 16);
 }
 
-// TOKMAX LDS: the waves' (m, l) [16][G][2], 16 floats of per-head lse2, then the logits.
+// TOKMAX LDS: the waves' (m, l) [16][G][2], 16 floats of per-head lse2, then the logits
+// [dump_pages][G][16] (with V, at least 128 pages' worth: the waves' accumulators
+// [16][G][128] reuse that space once the logits are consumed), then (ROPE) the token slots.
 template <int G>
 constexpr int tokmax_lds_header() {
   return kMaxWaves * G * 2 + 16;
+}
+template <int G, bool WITH_V>
+__host__ __device__ inline int64_t tokmax_logit_floats(int dump_pages) {
+  constexpr int kAccPages = kMaxWaves * kHeadDim / kPageSize;
+  const int64_t pages = (WITH_V && dump_pages < kAccPages) ? kAccPages : dump_pages;
+  return pages * G * kPageSize;
 }
 
 // The fused append's per-wave token slots (ROPE), in floats from the start of the dynamic LDS:
@@ -218,16 +230,21 @@ __device__ __forceinline__ float rows4_sum(float v) {
 //         B = V from a padded LDS tile whose row 4c + r holds token tok(r), read with
 //         ds_read_b64_tr_b16 (lane (c, j) gets tile rows 4c..4c+3 at d = 16n + j),
 //         D = O[g = 4c + r][d = 16n + lane%16].
-// TOKMAX (K-only, head-major, unsplit, the row's logits fit in LDS): every page's logits stay
-// in LDS ([page][g][16], past a small merge header); once the block's waves have merged, the
-// block knows each head's final lse and writes, per token, max_g 2^(x_g log2 e - lse2_g) --
+// TOKMAX (head-major, unsplit, the row's logits fit in LDS): every page's logits stay in LDS
+// ([page][g][16], past a small merge header); once the block's waves have merged, the block
+// knows each head's final lse and writes, per token, max_g 2^(x_g log2 e - lse2_g) --
 // del3_legacy_softmax's per-token max over this kv head's q heads -- instead of a logits dump.
+// Without V it is the K-only scorer; with V (the planner) P.V takes V from registers instead
+// of LDS tiles, which leaves the LDS to the logits: lane (c, j) loads V[tok(i)][8j, 8j + 8)
+// for its four k slots and MFMA n takes element n of each (two v_perm_b32), so
+// D = O[g = 4c + r][d = 8 lane%16 + n].
 template <int DT, int G, bool WITH_V, bool WITH_DUMP, bool ROPE, bool TOKMAX = false>
 __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
   // No FMA contraction: every instantiation (with or without the dump) rounds the softmax
   // arguments identically, so P -- rounded to the KV dtype for the P.V MFMA -- is the same.
 #pragma clang fp contract(off)
-  static_assert(!TOKMAX || (!WITH_V && !WITH_DUMP && !ROPE), "TOKMAX is the K-only scorer");
+  static_assert(!TOKMAX || (!WITH_DUMP && (WITH_V || !ROPE)), "TOKMAX: the K-only scorer or the on-chip planner");
+  constexpr bool REGV = TOKMAX && WITH_V;  // P.V with V in registers (no V tiles)
   using E = Elem<DT>;
   using M16 = Mfma16<DT>;
 
@@ -286,16 +303,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     vraw = reinterpret_cast<const uint32_t *>(a.v_new + (int64_t)b * a.v_new_stride + (int64_t)h * kHeadDim)[lane];
     rpos = (float)a.offsets[b];
   }
-  // This wave's LDS slot for the token: [64] rotated k pairs, then [64] v pairs.
-  uint32_t *const tok_lds = reinterpret_cast<uint32_t *>(smem + rope_lds_offset<G, WITH_V, WITH_DUMP>(nw)) +
-                            wave * kHeadDim;
+  // The waves' LDS slots for the token: [64] rotated k pairs, then [64] v pairs, per wave.
+  auto rope_slots = [&]() -> uint32_t * {
+    return reinterpret_cast<uint32_t *>(
+        smem + (TOKMAX ? tokmax_lds_header<G>() + (int)tokmax_logit_floats<G, WITH_V>(a.dump_pages)
+                       : rope_lds_offset<G, WITH_V, WITH_DUMP>(nw)));
+  };
+  uint32_t *const tok_lds = rope_slots() + wave * kHeadDim;
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
   const int64_t page_elems = 2 * kPageSize * row_elems;
   const int64_t k_off = (int64_t)(t >> 1) * row_elems + 32 * (t & 1) + 8 * c;  // + k_step(s)
   // K fragment s covers tokens 8 (s / 2) + [0, 8) and d half sp = s % 2.
   auto k_step = [&](int s) -> int64_t { return (int64_t)(s >> 1) * 8 * row_elems + 64 * (s & 1); };
-  const int64_t v_off = kPageSize * row_elems + (int64_t)c * row_elems + 8 * t;  // + 4 i rows
+  // V row i of a lane: token c + 4i (V tiles) or 2c + v_row(i) (registers).
+  const int64_t v_off = kPageSize * row_elems + (int64_t)(REGV ? 2 * c : c) * row_elems + 8 * t;
+  auto v_step = [&](int i) -> int64_t { return (int64_t)(REGV ? v_row(i) : 4 * i) * row_elems; };
   uint16_t *vt = reinterpret_cast<uint16_t *>(smem) + wave * kVTile;           // this wave's V tile
   // Logits staged per wave for a window of kDumpSlots pages, then written out together
   // (flush_window) at the end of the window's last iteration.
@@ -419,14 +442,16 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
           if ((s >> 1) == (ap_slot >> 3))
             kr[s] = *reinterpret_cast<const u32x4 *>(tok_lds + 32 * (s & 1) + 16 * (t & 1) + 4 * c);
       }
-      if (WITH_V && c == (ap_slot & 3)) {
+      // (register-held V: lanes with 2c == slot % 8 - slot % 2, row i = 2 (slot / 8) + slot % 2)
+      if (WITH_V && c == (REGV ? (ap_slot & 7) >> 1 : ap_slot & 3)) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (i == (ap_slot >> 2)) vr[i] = *reinterpret_cast<const u32x4 *>(tok_lds + kHeadDim / 2 + 4 * t);
+          if (i == (REGV ? 2 * (ap_slot >> 3) + (ap_slot & 1) : ap_slot >> 2))
+            vr[i] = *reinterpret_cast<const u32x4 *>(tok_lds + kHeadDim / 2 + 4 * t);
       }
     }
 
-    if (WITH_V) {
+    if (WITH_V && !REGV) {
       // Stage this page's V (loaded one iteration ago) before anything else, so the wait at
       // the top of the iteration is the only one on loaded data and the registers are free
       // for the next page's V below.  Rows past kv_len (and all rows of an invalid page) are
@@ -450,9 +475,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       const uint16_t *nbase = page_ptr(pidn);
 #pragma unroll
       for (int s = 0; s < 4; ++s) kr[s] = ld128_stream(nbase + k_off + k_step(s));
-      if (WITH_V) {
+      if (WITH_V && !REGV) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(nbase + v_off + (int64_t)(4 * i) * row_elems);
+        for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(nbase + v_off + v_step(i));
       }
     }
 
@@ -510,11 +535,34 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       s4_t pa;
 #pragma unroll
       for (int r = 0; r < 4; ++r) pa[r] = t < G ? M16::pack(p[r]) : (short)0;
-      const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStride + 4 * (t & 3);
+      if (REGV) {
+        // This page's V rows (loaded one iteration ago): element n of each row for MFMA n.
+        // Rows past kv_len (and all rows of an invalid page) are zeroed by mask, since they
+        // may hold NaN/Inf and meet p = 0.  Then the next page's V goes into vr.
+        const int vlim = ok ? ri.kv_len - j * kPageSize : 0;
+        uint32_t keep[4];
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const s4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t *)(rd + 16 * n));
-        acc[n] = M16::run(pa, bv, acc[n]);
+        for (int i = 0; i < 4; ++i) keep[i] = 2 * c + v_row(i) < vlim ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          // low (n even) or high (n odd) halves of word n / 2: rows 0, 1 and rows 2, 3
+          const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t lo = __builtin_amdgcn_perm(vr[1][n >> 1] & keep[1], vr[0][n >> 1] & keep[0], sel);
+          const uint32_t hi = __builtin_amdgcn_perm(vr[3][n >> 1] & keep[3], vr[2][n >> 1] & keep[2], sel);
+          acc[n] = M16::run(pa, __builtin_bit_cast(s4_t, (uint2){lo, hi}), acc[n]);
+        }
+        if (more) {
+          const uint16_t *nbase = page_ptr(pidn);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(nbase + v_off + v_step(i));
+        }
+      } else {
+        const uint16_t *rd = vt + (4 * c + (t >> 2)) * kVStride + 4 * (t & 3);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          const s4_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t *)(rd + 16 * n));
+          acc[n] = M16::run(pa, bv, acc[n]);
+        }
       }
     }
     // Last page of a window (or of the wave): write the window's staged logits.  The
@@ -530,7 +578,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     __builtin_amdgcn_sched_barrier(0);
     if (WITH_V) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(base + v_off + (int64_t)(4 * i) * row_elems);
+      for (int i = 0; i < 4; ++i) vr[i] = ld128_stream(base + v_off + v_step(i));
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -581,6 +629,87 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         pb = p3;
       }
     }
+  }
+
+  // One block per (row, kv head group) writes the new token's rotated k and v into the cache
+  // slot, 16-byte chunk r % 16 of head head0 + r / 16, from the LDS slot of wave r / 16 (which
+  // works on that head); a block barrier after the waves' loops orders those LDS stores.
+  auto write_append_slot = [&]() {
+    if (ROPE && ap_pid >= 0 && (int64_t)ap_pid < a.num_pages && (a.nsplit == 1 || split == 0)) {
+      for (int ch = threadIdx.x; ch < 2 * hb * (kHeadDim / 8); ch += blockDim.x) {
+        const int which = ch >= hb * (kHeadDim / 8);  // 0 = K, 1 = V
+        const int r = which ? ch - hb * (kHeadDim / 8) : ch;
+        const uint32_t *src = rope_slots() + (r >> 4) * kHeadDim + which * (kHeadDim / 2) + 4 * (r & 15);
+        uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
+                        (int64_t)(head0 + (r >> 4)) * kHeadDim + 8 * (r & 15);
+        st128(dst, *reinterpret_cast<const u32x4 *>(src));
+      }
+    }
+  };
+  // Per-token maxima of the row's logits in LDS (TOKMAX): max_g 2^(x_g log2 e - lse2_g).
+  auto write_tokmax = [&]() {
+    const float *lse2 = smem + tokmax_lds_header<G>() - 16;
+    const float *lg = smem + tokmax_lds_header<G>();
+    float *outp = a.tokmax + (int64_t)b * a.tokmax_stride_b + (int64_t)head0 * a.tokmax_stride_h;
+    const int np_out = ri.np < a.dump_pages ? ri.np : a.dump_pages;
+    for (int tk = threadIdx.x; tk < np_out * kPageSize; tk += blockDim.x) {
+      const int j = tk >> 4, tok = tk & 15;
+      float mx = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (lse2[g] != -INFINITY) mx = fmaxf(mx, fast_exp2(lg[(j * G + g) * kPageSize + tok] * kLog2e - lse2[g]));
+      __builtin_nontemporal_store(mx, outp + tk);
+    }
+  };
+
+  if constexpr (REGV) {
+    // The planner with on-chip logits (head-major, unsplit: one kv head h per block).  The
+    // waves' (m, l) give each head's final lse; the logits become per-token maxima; then the
+    // waves' accumulators are merged through the logits' space.
+    float *const s_ml = smem;                                // [16][G][2]
+    float *const lse2 = smem + tokmax_lds_header<G>() - 16;  // [G]
+    float *const s_acc = smem + tokmax_lds_header<G>();      // [16][G][128], over the logits
+    if (c == 0 && t < G) {
+      s_ml[(wave * G + t) * 2 + 0] = m;
+      s_ml[(wave * G + t) * 2 + 1] = l;
+    }
+    __syncthreads();
+    if (threadIdx.x < G) {
+      const int g = threadIdx.x;
+      float M = -INFINITY, L = 0.f;
+      for (int w = 0; w < nw; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
+      const float Mr = M == -INFINITY ? 0.f : M;
+      for (int w = 0; w < nw; ++w) L = fmaf(s_ml[(w * G + g) * 2 + 1], fast_exp2(s_ml[(w * G + g) * 2] - Mr), L);
+      lse2[g] = L > 0.f ? M + log2f(L) : -INFINITY;
+      if (a.lse != nullptr) a.lse[(int64_t)b * a.hq + h * G + g] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
+    }
+    __syncthreads();
+    write_tokmax();
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int g = 4 * c + r;
+      if (g < G) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) s_acc[(wave * G + g) * kHeadDim + 8 * t + n] = acc[n][r];
+      }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
+      const int g = idx / kHeadDim, dd = idx % kHeadDim;
+      float M = -INFINITY, L = 0.f, A = 0.f;
+      for (int w = 0; w < nw; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
+      const float Mr = M == -INFINITY ? 0.f : M;
+      for (int w = 0; w < nw; ++w) {
+        const float sc = fast_exp2(s_ml[(w * G + g) * 2] - Mr);
+        L = fmaf(s_ml[(w * G + g) * 2 + 1], sc, L);
+        A = fmaf(s_acc[(w * G + g) * kHeadDim + dd], sc, A);
+      }
+      const float ov = L > 0.f ? A / L : 0.f;
+      a.o[(int64_t)b * a.o_stride_b + (int64_t)(h * G + g) * a.o_stride_h + dd] = (uint16_t)E::from_float(ov);
+    }
+    write_append_slot();
+    return;
   }
 
   // Merge the block's waves in LDS.  Attention launches have a merge area of their own past
@@ -662,34 +791,10 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       }
     }
   }
-  if (ROPE && ap_pid >= 0 && (int64_t)ap_pid < a.num_pages && (a.nsplit == 1 || split == 0)) {
-    // One block per (row, kv head group) writes the new token's rotated k and v into the cache
-    // slot, 16-byte chunk r % 16 of head head0 + r / 16, from the LDS slot of wave r / 16 (which
-    // works on that head); the merge's barrier above ordered those LDS stores.
-    for (int ch = threadIdx.x; ch < 2 * hb * (kHeadDim / 8); ch += blockDim.x) {
-      const int which = ch >= hb * (kHeadDim / 8);  // 0 = K, 1 = V
-      const int r = which ? ch - hb * (kHeadDim / 8) : ch;
-      const uint32_t *src = reinterpret_cast<const uint32_t *>(smem + rope_lds_offset<G, WITH_V, WITH_DUMP>(nw)) +
-                            (r >> 4) * kHeadDim + which * (kHeadDim / 2) + 4 * (r & 15);
-      uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
-                      (int64_t)(head0 + (r >> 4)) * kHeadDim + 8 * (r & 15);
-      st128(dst, *reinterpret_cast<const u32x4 *>(src));
-    }
-  }
+  write_append_slot();
   if (TOKMAX) {
     __syncthreads();
-    const float *lse2 = smem + tokmax_lds_header<G>() - 16;
-    const float *lg = smem + tokmax_lds_header<G>();
-    float *outp = a.tokmax + (int64_t)b * a.tokmax_stride_b + (int64_t)head0 * a.tokmax_stride_h;
-    const int np_out = ri.np < a.dump_pages ? ri.np : a.dump_pages;
-    for (int tk = threadIdx.x; tk < np_out * kPageSize; tk += blockDim.x) {
-      const int j = tk >> 4, tok = tk & 15;
-      float mx = 0.f;
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        if (lse2[g] != -INFINITY) mx = fmaxf(mx, fast_exp2(lg[(j * G + g) * kPageSize + tok] * kLog2e - lse2[g]));
-      __builtin_nontemporal_store(mx, outp + tk);
-    }
+    write_tokmax();
   }
 }
 
@@ -722,6 +827,12 @@ template <int DT, int G>
 __global__ void __launch_bounds__(kMaxWaves * 64) page_score_tokmax_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
   decode_split_body<DT, G, false, false, false, true>(a, smem);
+}
+// The planner with the row's logits kept on chip: attention + per-token maxima, no dump.
+template <int DT, int G, bool ROPE>
+__global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_plan_tokmax_kernel(DecodeArgs a) {
+  extern __shared__ float smem[];
+  decode_split_body<DT, G, true, false, ROPE, true>(a, smem);
 }
 
 // Combines the unit partials of one (row, q head): thread d of the block computes
@@ -800,7 +911,7 @@ __global__ void __launch_bounds__(256) decode_merge_lse_kernel(DecodeArgs a, int
   if (lane == 0) a.lse[idx] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
 
-enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3, kScoreTokmax = 4 };
+enum Mode { kAttn = 0, kAttnDump = 1, kScoreOnly = 2, kAttnSubset = 3, kScoreTokmax = 4, kAttnTokmax = 5 };
 
 template <int DT, int G>
 void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) {
@@ -843,6 +954,15 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
       hipLaunchKernelGGL((page_score_tokmax_kernel<DT, G>), grid, block,
                          (size_t)(tokmax_lds_header<G>() + a.dump_pages * G * kPageSize) * sizeof(float), stream, a);
       break;
+    case kAttnTokmax: {
+      const size_t sm = (size_t)(tokmax_lds_header<G>() + tokmax_logit_floats<G, true>(a.dump_pages)) * sizeof(float) +
+                        (rope ? rope_lds : 0);
+      if (rope)
+        hipLaunchKernelGGL((paged_decode_plan_tokmax_kernel<DT, G, true>), grid, block, sm, stream, a);
+      else
+        hipLaunchKernelGGL((paged_decode_plan_tokmax_kernel<DT, G, false>), grid, block, sm, stream, a);
+      break;
+    }
     default:
       hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, sm_score, stream, a);
       break;
@@ -925,6 +1045,14 @@ bool tokmax_fits(int batch, int hkv, int G, int max_pages) {
   return (int64_t)batch * hkv >= kHeadMajorPairs && lds <= 160 * 1024;
 }
 
+// The planner keeps the row's logits in LDS (no dump) under the same conditions, with room for
+// the waves' accumulators (at least 128 pages' worth of logits) and the append's token slots.
+bool plan_tokmax_fits(int batch, int hkv, int G, int max_pages, bool rope) {
+  const int64_t floats = kMaxWaves * G * 2 + 16 + (max_pages < 128 ? 128 : (int64_t)max_pages) * G * kPageSize;
+  const int64_t lds = floats * (int64_t)sizeof(float) + (rope ? kMaxWaves * kHeadDim * 4 : 0);
+  return (int64_t)batch * hkv >= kHeadMajorPairs && max_pages > 0 && lds <= 160 * 1024;
+}
+
 int decode_num_splits(int batch, int hkv, int max_pages) {
   int ns, w, hb, ch, ns_dump;
   decode_plan(batch, hkv, max_pages, false, &ns, &w, &hb, &ch);
@@ -961,12 +1089,15 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   if (dtype != DELTA_BF16 && dtype != DELTA_FP16) return set_error(DELTA_ERR_INVALID, "%s: dtype must be bf16 or fp16", who);
   if (!q || !kv_cache || !kv_indptr || !kv_indices || !kv_last_page_len)
     return set_error(DELTA_ERR_INVALID, "%s: null input pointer", who);
-  const bool tokmax = mode == kScoreTokmax;  // `dump` is then the [batch][hkv][stride_h] output
-  if (mode != kScoreOnly && !tokmax && !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
+  // `dump` is the [batch][hkv][stride_h] per-token maxima output of the TOKMAX modes
+  const bool tokmax = mode == kScoreTokmax || mode == kAttnTokmax;
+  if (mode != kScoreOnly && mode != kScoreTokmax && !o) return set_error(DELTA_ERR_INVALID, "%s: null output pointer", who);
   if ((mode == kAttnDump || mode == kScoreOnly || tokmax) && !dump)
     return set_error(DELTA_ERR_INVALID, "%s: null logits dump", who);
-  if (tokmax && !tokmax_fits(batch, hkv, G, max_pages))
+  if (mode == kScoreTokmax && !tokmax_fits(batch, hkv, G, max_pages))
     return set_error(DELTA_ERR_INVALID, "%s: this shape does not fit the LDS scorer", who);
+  if (mode == kAttnTokmax && !plan_tokmax_fits(batch, hkv, G, max_pages, ap != nullptr))
+    return set_error(DELTA_ERR_INVALID, "%s: this shape does not fit the on-chip planner", who);
   if (((uintptr_t)q | (uintptr_t)kv_cache) & 15u)
     return set_error(DELTA_ERR_INVALID, "%s: q and kv_cache must be 16-byte aligned", who);
   if ((q_stride_h % 8) || (q_stride_b % 8))
@@ -1022,7 +1153,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.ap_indices_len = 0;
   a.rcp_scale = a.log2_theta = a.smooth_a = a.smooth_b = 0.f;
   if (ap) {
-    if (mode == kScoreOnly) return set_error(DELTA_ERR_INVALID, "%s: the scorer takes no append", who);
+    if (mode == kScoreOnly || mode == kScoreTokmax)
+      return set_error(DELTA_ERR_INVALID, "%s: the scorer takes no append", who);
     if (!ap->k || !ap->v || !ap->offsets || !ap->kv_indptr || !ap->kv_indices)
       return set_error(DELTA_ERR_INVALID, "%s: null append pointer", who);
     if ((((uintptr_t)ap->k | (uintptr_t)ap->v) & 3u) || (ap->k_stride % 2) || (ap->v_stride % 2) ||
@@ -1052,7 +1184,7 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
 
   if (a.hb < 1 || a.hkv % a.hb != 0)
     return set_error(DELTA_ERR_INVALID, "%s: launch planned with %d of %d kv heads per block", who, a.hb, a.hkv);
-  const bool with_acc = mode != kScoreOnly && !tokmax;
+  const bool with_acc = mode != kScoreOnly && mode != kScoreTokmax;
   const size_t need = decode_workspace_bytes(batch, hq, a.nsplit, with_acc);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)

@@ -212,6 +212,67 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tenso
     return out
 
 
+def paged_decode_scores_supported(batch: int, num_qo_heads: int, num_kv_heads: int, max_pages_per_row: int,
+                                  with_append: bool = False) -> bool:
+    """True when ``paged_decode_scores`` applies to this shape (the rows' logits fit on chip)."""
+    return bool(_lib.query("delta_paged_decode_scores_supported", int(batch), int(num_qo_heads),
+                           int(num_kv_heads), int(max_pages_per_row), int(bool(with_append))))
+
+
+def paged_decode_scores_workspace_bytes(batch: int, num_kv_heads: int, max_pages_per_row: int) -> int:
+    """Workspace bytes of ``paged_decode_scores`` (its per-token maxima)."""
+    return int(_lib.query("delta_paged_decode_scores_workspace_bytes", int(batch), int(num_kv_heads),
+                          int(max_pages_per_row)))
+
+
+def paged_decode_scores(q: torch.Tensor, kv_cache: torch.Tensor, kv_indptr: torch.Tensor,
+                        kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, *,
+                        max_pages_per_row: int, sm_scale: Optional[float] = None,
+                        out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                        scores: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                        append: Optional[DecodeAppend] = None):
+    """The planner layer without a logits dump (``delta_paged_decode_scores[_append]``): full
+    attention and the del3_legacy_softmax page scores in one pass; returns ``(out, scores)``,
+    scores fp32 [B, max_pages_per_row].  Only where ``paged_decode_scores_supported``."""
+    dev = _check_cuda(q, kv_cache, kv_indptr, kv_indices, kv_last_page_len, out, lse, scores)
+    _check_cache(kv_cache)
+    hq, hkv = _check_heads(q, kv_cache)
+    B = q.shape[0]
+    _check_i32("kv_indptr", kv_indptr, B + 1)
+    _check_i32("kv_indices", kv_indices)
+    _check_i32("kv_last_page_len", kv_last_page_len, B)
+    if out is None:
+        out = torch.empty_like(q)
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError("out must match q's shape/dtype with unit inner stride")
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape[0] < B or lse.shape[1] != hq
+                            or not lse.is_contiguous()):
+        raise ValueError("lse must be contiguous fp32 [>=B, Hq]")
+    if scores is None:
+        scores = torch.empty((B, max_pages_per_row), dtype=torch.float32, device=dev)
+    if scores.dtype != torch.float32 or scores.stride(1) != 1 or scores.shape[0] < B \
+            or scores.shape[1] < max_pages_per_row:
+        raise ValueError("scores must be fp32 [>=B, >=max_pages_per_row]")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HEAD_DIM)
+    need = paged_decode_scores_workspace_bytes(B, hkv, max_pages_per_row)
+    if workspace is None:
+        workspace = _default_ws.get(need, dev)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace too small: {need} bytes needed")
+    args = (q.data_ptr(), q.stride(0), q.stride(1), kv_cache.data_ptr(), kv_cache.shape[0],
+            kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_indices.numel(), kv_last_page_len.data_ptr(),
+            out.data_ptr(), out.stride(0), out.stride(1), _ptr(lse), scores.data_ptr(), scores.stride(0),
+            B, hq, hkv, HEAD_DIM, _dtype_code(q), float(sm_scale), int(max_pages_per_row),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(dev))
+    if append is not None:
+        _lib.call("delta_paged_decode_scores_append",
+                  ctypes.byref(_append_struct(append, B, hkv, kv_cache)), *args)
+    else:
+        _lib.call("delta_paged_decode_scores", *args)
+    return out, scores
+
+
 def paged_prefill(q: torch.Tensor, kv_cache: torch.Tensor, qo_indptr: torch.Tensor,
                   kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, *,
                   max_qo_len: int, sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,

@@ -256,6 +256,40 @@ int delta_page_score(const void *q, int64_t q_stride_b, int64_t q_stride_h,
                      int head_dim, int dtype, float sm_scale, int max_pages,
                      void *workspace, size_t workspace_bytes, delta_stream_t stream);
 
+/* The planner layer without a logits dump: full attention (o, lse, as delta_paged_decode)
+ * and the del3_legacy_softmax page scores (as delta_page_scores_from_logits over the dump
+ * the same launch would write) in one pass over K and V.  Replaces the pair
+ * BatchDumpAttentionWeights.run + _compute_page_scores_from_attention_buffer_legacy_softmax
+ * (backend.py:561-577 + 887-904) when the caller needs no dump (no debug parity check).
+ * Each (row, kv head) keeps its logits on chip, so it applies when
+ * delta_paged_decode_scores_supported(...) == 1 (batch * num_kv_heads >= 256 and the row's
+ * logits fit in LDS); else it is an error and the caller uses the dump.  o and lse agree with
+ * delta_paged_decode to rounding (another summation order); scores are written for pages
+ * [0, max_pages) of each row (past the row: 0).  workspace: delta_paged_decode_scores_
+ * workspace_bytes, 256-byte aligned.  The _append variant fuses the new token's RoPE and
+ * append as delta_paged_decode_append does. */
+int delta_paged_decode_scores_supported(int batch, int num_qo_heads, int num_kv_heads,
+                                        int max_pages_per_row, int with_append);
+size_t delta_paged_decode_scores_workspace_bytes(int batch, int num_kv_heads, int max_pages_per_row);
+int delta_paged_decode_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                              const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr,
+                              const int32_t *kv_indices, int64_t kv_indices_len,
+                              const int32_t *kv_last_page_len, void *o, int64_t o_stride_b,
+                              int64_t o_stride_h, float *lse, float *scores, int64_t score_stride,
+                              int batch, int num_qo_heads, int num_kv_heads, int head_dim, int dtype,
+                              float sm_scale, int max_pages_per_row, void *workspace,
+                              size_t workspace_bytes, delta_stream_t stream);
+int delta_paged_decode_scores_append(const delta_decode_append_t *append, const void *q,
+                                     int64_t q_stride_b, int64_t q_stride_h, void *kv_cache,
+                                     int64_t num_pages, const int32_t *kv_indptr,
+                                     const int32_t *kv_indices, int64_t kv_indices_len,
+                                     const int32_t *kv_last_page_len, void *o, int64_t o_stride_b,
+                                     int64_t o_stride_h, float *lse, float *scores,
+                                     int64_t score_stride, int batch, int num_qo_heads,
+                                     int num_kv_heads, int head_dim, int dtype, float sm_scale,
+                                     int max_pages_per_row, void *workspace, size_t workspace_bytes,
+                                     delta_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* PageSelectorV2 (top-k page selection)                                     */
 /* ------------------------------------------------------------------------ */

@@ -9,7 +9,7 @@ import math
 import pytest
 import torch
 
-from delta_amd import kernels as K
+from delta_amd import _lib, kernels as K
 from delta_amd.workloads import config_case, make_case
 from oracle import delta_oracle as O
 
@@ -605,6 +605,84 @@ def test_paged_prefill_long_rows_growing_scores(sign):
                                                c.kv_last_page_len, scale)
     assert_attn_close(o, o_ref, f"long prefill, scale sign {sign}")
     assert torch.allclose(lse.cpu(), lse_ref, atol=2e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("hq,hkv,dtype,batch,max_len", [
+    (32, 8, torch.bfloat16, 32, 1500),    # config-3 heads, 256 (row, kv head) blocks
+    (40, 8, torch.bfloat16, 32, 700),     # G = 5
+    (16, 2, torch.float16, 128, 400),     # G = 8
+    (32, 8, torch.bfloat16, 32, 9500),    # 594 pages: near the LDS limit with the append slots
+])
+def test_planner_scores_on_chip_match_dump_path_and_oracle(hq, hkv, dtype, batch, max_len):
+    """The planner without a dump (delta_paged_decode_scores[_append]): o and lse against the
+    dump launch and the oracle, page scores against delta_page_scores_from_logits of that dump
+    and the oracle's del3_legacy_softmax (1e-4 relative), and with the fused append the cache
+    bytes equal delta_rope_append's and o equals the fused dump launch's to rounding.  Ragged
+    rows: one page, a partial last page, a row at max_len."""
+    gen = torch.Generator().manual_seed(51)
+    lens = torch.randint(1, max_len, (batch,), generator=gen).tolist()
+    lens[0], lens[1], lens[2] = 1, 17, max_len
+    c = make_case(batch=batch, hq=hq, hkv=hkv, kv_lens=lens, seed=52, page_order="randperm", k=4, L=2,
+                  dtype=dtype)
+    g = gpu(c)
+    B, mp = batch, c.max_pages
+    assert K.paged_decode_scores_supported(B, hq, hkv, mp, True)
+    lse_d = torch.empty(B, hq, device=DEV)
+    dump = torch.full((B, hq, mp * 16), float("-inf"), device=DEV)
+    o_d = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                         lse=lse_d, logits_dump=dump)
+    s_d = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse_d)
+    lse = torch.empty(B, hq, device=DEV)
+    o, s = K.paged_decode_scores(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                                 max_pages_per_row=mp, lse=lse)
+    torch.cuda.synchronize()
+    assert_attn_close(o, o_d.float(), "on-chip planner vs dump launch")
+    assert torch.allclose(lse, lse_d, atol=1e-4, rtol=1e-5)
+    rel = ((s - s_d).abs() / s_d.abs().clamp_min(1e-30)).max().item()
+    assert rel < 1e-5, rel
+    o_ref, lse_ref = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                                              c.sm_scale)
+    assert_attn_close(o, o_ref, "on-chip planner vs oracle")
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-4, rtol=1e-5)
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, c.sm_scale, mp * 16)
+    want = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
+    got = s.cpu().double()
+    assert ((got - want).abs() / want.abs().clamp_min(1e-30)).max().item() < 1e-4
+    pages = (c.kv_indptr[1:] - c.kv_indptr[:-1]).tolist()
+    for b in range(B):
+        if pages[b] < mp:  # a row's pages past its end score 0
+            assert got[b, pages[b]:].abs().max().item() == 0.0
+
+    # fused RoPE + append: cache bytes as delta_rope_append, o and scores as the fused dump launch
+    kn = torch.randn(B, hkv, 128, generator=gen).to(dtype).to(DEV)
+    vn = torch.randn(B, hkv, 128, generator=gen).to(dtype).to(DEV)
+    offsets = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device=DEV)
+    ap = K.DecodeAppend(kn, vn, offsets, g.kv_indptr, g.kv_indices, rope_scale=8.0, rope_theta=5e5,
+                        low_freq_factor=1.0, high_freq_factor=4.0, old_context_len=8192.0)
+    c1, c2 = g.kv_cache.clone(), g.kv_cache.clone()
+    lse1 = torch.empty(B, hq, device=DEV)
+    dump1 = torch.full((B, hq, mp * 16), float("-inf"), device=DEV)
+    o1 = K.paged_decode(g.q, c1, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp, lse=lse1,
+                        logits_dump=dump1, append=ap)
+    s1 = K.page_scores_from_logits(dump1, g.kv_indptr, g.kv_last_page_len, mp, lse=lse1)
+    o2, s2 = K.paged_decode_scores(g.q, c2, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                                   append=ap)
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
+    assert_attn_close(o2, o1.float(), "fused on-chip planner vs fused dump launch")
+    assert ((s2 - s1).abs() / s1.abs().clamp_min(1e-30)).max().item() < 1e-5
+
+
+def test_planner_scores_on_chip_refuses_unsupported_shapes():
+    """Fewer than 256 (row, kv head) blocks, or rows whose logits do not fit in LDS: a clear
+    error (the caller keeps the dump path)."""
+    c = make_case(batch=4, hq=32, hkv=8, kv_lens=[300] * 4, seed=53, k=4, L=2)
+    g = gpu(c)
+    assert not K.paged_decode_scores_supported(4, 32, 8, c.max_pages, False)
+    with pytest.raises(_lib.DeltaHipError, match="does not fit the on-chip planner"):
+        K.paged_decode_scores(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                              max_pages_per_row=c.max_pages)
+    assert not K.paged_decode_scores_supported(32, 32, 8, 700, False)
 
 
 @pytest.mark.parametrize("hq,hkv,dtype,llama31,batch", [

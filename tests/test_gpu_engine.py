@@ -358,6 +358,58 @@ def test_replay_failure_falls_back_to_eager():
     assert eng.cachelens.tolist() == [52, 62, 72]
 
 
+def test_planner_on_chip_matches_dump_path_in_the_engine():
+    """With >= 256 (row, kv head) blocks the engine's planner keeps its logits on chip
+    (delta_paged_decode_scores_append).  From the same state, one decode step each way: the
+    planner layer's output within the attention tolerance, page scores within 1e-5 relative,
+    the subset selection identical (a page may differ only where the two keys at the k-th
+    boundary are within that tolerance); ragged rows and idle slots.  And a graph replay of the
+    on-chip step equals the eager step bit for bit."""
+    B = 128  # tiny-test has 2 kv heads: 256 blocks
+    eng = make_engine(graph=True, B=B, max_len=512, k=6, L=2)
+    assert eng.plan_scores_on_chip
+    lens = [20 + (37 * i) % 400 for i in range(B)]
+    eng.prepare_synthetic_decode(lens, decode_budget=16, seed=21)
+    eng._release_slot(5)
+    eng._release_slot(77)
+    plan = eng.model.layers[1].attention
+    snap = _snapshot(eng)
+    runs = {}
+    for on_chip in (True, False):
+        _restore(eng, snap)
+        eng.plan_scores_on_chip = on_chip
+        plan.record = []
+        tok = eng.decode_steps(1, use_graph=False).clone()
+        sip = eng.page_selector.paged_subset_kv_indptr[:B + 1].clone()
+        runs[on_chip] = (tok, sip, eng.page_selector.paged_subset_kv_indices[:int(sip[-1])].clone(),
+                         eng.page_scores.clone(), plan.record[0][1].clone())
+    plan.record = None
+    t1, p1, i1, s1, o1 = runs[True]
+    t0, p0, i0, s0, o0 = runs[False]
+    assert_close(o1, o0, "planner layer output, on chip vs dump")
+    rel = ((s1 - s0).abs() / s0.abs().clamp_min(1e-30)).max().item()
+    assert rel < 1e-5, rel
+    assert torch.equal(p1, p0)
+    if not torch.equal(i1, i0):  # only near-ties at the k-th key may swap
+        for b in range(B):
+            a, c = i1[int(p1[b]):int(p1[b + 1])].tolist(), i0[int(p0[b]):int(p0[b + 1])].tolist()
+            if a != c:
+                ks = s0[b, :eng.pages_per_slot]
+                diff = set(a) ^ set(c)
+                bt = eng.slot_block_table[b].tolist()
+                vals = [float(ks[bt.index(p)]) for p in diff]
+                assert max(vals) - min(vals) <= 1e-5 * max(abs(v) for v in vals), f"row {b}"
+    # graph replay of the on-chip step from the same state
+    _restore(eng, snap)
+    eng.plan_scores_on_chip = True
+    eng._decode_graph = None
+    tok_g = eng.decode_steps(1, use_graph=True).clone()
+    sip_g = eng.page_selector.paged_subset_kv_indptr[:B + 1].clone()
+    assert torch.equal(tok_g, t1)
+    assert torch.equal(sip_g, p1)
+    assert torch.equal(eng.page_selector.paged_subset_kv_indices[:int(sip_g[-1])], i1)
+
+
 def test_page_scores_from_attention_buffer_api():
     """LMBackend._compute_page_scores_from_attention_buffer (backend.py:911-913) returns the
     last planner step's del3_legacy_softmax scores: equal to the oracle's from the same dump

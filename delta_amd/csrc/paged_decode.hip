@@ -652,13 +652,19 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     const float *lg = smem + tokmax_lds_header<G>();
     float *outp = a.tokmax + (int64_t)b * a.tokmax_stride_b + (int64_t)head0 * a.tokmax_stride_h;
     const int np_out = ri.np < a.dump_pages ? ri.np : a.dump_pages;
-    for (int tk = threadIdx.x; tk < np_out * kPageSize; tk += blockDim.x) {
-      const int j = tk >> 4, tok = tk & 15;
-      float mx = 0.f;
+    // Four consecutive tokens per thread: one 16-byte LDS read per head, one 16-byte store.
+    for (int tq = threadIdx.x; tq < np_out * (kPageSize / 4); tq += blockDim.x) {
+      const int j = tq >> 2, tok = 4 * (tq & 3);
+      f32x4 mx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int g = 0; g < G; ++g)
-        if (lse2[g] != -INFINITY) mx = fmaxf(mx, fast_exp2(lg[(j * G + g) * kPageSize + tok] * kLog2e - lse2[g]));
-      __builtin_nontemporal_store(mx, outp + tk);
+      for (int g = 0; g < G; ++g) {
+        if (lse2[g] != -INFINITY) {
+          const f32x4 x = *reinterpret_cast<const f32x4 *>(lg + (j * G + g) * kPageSize + tok);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx[e] = fmaxf(mx[e], fast_exp2(x[e] * kLog2e - lse2[g]));
+        }
+      }
+      __builtin_nontemporal_store(mx, reinterpret_cast<f32x4 *>(outp) + tq);
     }
   };
 

@@ -261,6 +261,9 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
       u32x4 kc[kSub];
 #pragma unroll
       for (int sb = 0; sb < kSub; ++sb) kc[sb] = kfrag(sb, 0);
+      // Raised wave priority over each MFMA run: of the SIMD's two waves, the one with MFMAs
+      // to issue goes first, which pushes the other into its softmax meanwhile (~1 %).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
         u32x4 kn[kSub];
@@ -275,6 +278,7 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
           for (int sb = 0; sb < kSub; ++sb) kc[sb] = kn[sb];
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // Masks only where the step crosses the wave's first diagonal, kv_len, or a bad page.
       const int kv0 = j * kKvStep;
       const int poff = kPgStep * j - cbase;  // the step's pages: bits poff .. poff + kPgStep - 1
@@ -332,6 +336,7 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
 #pragma unroll
         for (int w = 0; w < 4; ++w)
           pc[cc][w] = pack2<DT>(x[8 * cc + 2 * w], x[8 * cc + 2 * w + 1]);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -346,6 +351,7 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
           va[3] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
           acc[dt] = MF::run(va, pc[cc], acc[dt]);
         }
+      __builtin_amdgcn_s_setprio(0);
     }
     if (j + 1 < nsteps) {
       stage(j + 1);

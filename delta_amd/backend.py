@@ -132,6 +132,7 @@ class LMBackend:
         self._compiled = False
         self._step: Optional[_StepCSR] = None
         self._decode_graph: Optional[torch.cuda.CUDAGraph] = None
+        self._decode_graph_on_chip = False  # the planner path the captured step runs
         self._decode_graph_failed: Optional[str] = None
         self._decode_graph_stats = defaultdict(int)
         self._decode_graph_fallback_reasons = defaultdict(int)
@@ -435,6 +436,7 @@ class LMBackend:
         with torch.cuda.graph(graph):
             self._decode_body(advance=True)
         self._decode_graph = graph
+        self._decode_graph_on_chip = self._plan_on_chip()
         self._decode_graph_stats["captures"] += 1
 
     def sync_host_lens(self):
@@ -458,6 +460,8 @@ class LMBackend:
         before running when a row would need more pages than its slot holds."""
         self._check_decode_budget(n)
         use_graph = self.enable_cuda_graph_decode if use_graph is None else use_graph
+        if self._decode_graph is not None and self._decode_graph_on_chip != self._plan_on_chip():
+            self._decode_graph = None  # captured with the other planner path (the debug flag moved)
         if use_graph and self._decode_graph is None and self._decode_graph_failed is None:
             try:
                 self._capture_decode_graph()

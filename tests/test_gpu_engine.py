@@ -408,6 +408,10 @@ def test_planner_on_chip_matches_dump_path_in_the_engine():
     assert torch.equal(tok_g, t1)
     assert torch.equal(sip_g, p1)
     assert torch.equal(eng.page_selector.paged_subset_kv_indices[:int(sip_g[-1])], i1)
+    # the selection parity check needs the dump: the step is captured again on the dump path
+    eng.enable_delta_debug_page_selection_parity = True
+    eng.decode_steps(1, use_graph=True)
+    assert eng._decode_graph_stats["captures"] == 2 and not eng._decode_graph_on_chip
 
 
 def test_page_scores_from_attention_buffer_api():

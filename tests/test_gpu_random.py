@@ -104,3 +104,59 @@ def test_random_decode_chain(seed):
         outs.append((oo, cache))
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), what + " fused append"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_planner_on_chip(seed):
+    """The planner without a dump (delta_paged_decode_scores) on seeded random shapes with
+    >= 256 (row, kv head) blocks: o and lse against the dump launch and the oracle, page scores
+    against delta_page_scores_from_logits of that dump (1e-5 relative) and the oracle (1e-4),
+    the selection from both score routes identical."""
+    r = random.Random(2000 + seed)
+    hkv = r.choice([2, 4, 8])
+    G = r.randint(1, 8)
+    B = -(-256 // hkv) + r.randint(0, 16)
+    lens = [r.randint(1, 1200) for _ in range(B)]
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    c = make_case(batch=B, hq=hkv * G, hkv=hkv, kv_lens=lens, dtype=dtype, seed=2000 + seed,
+                  page_order=r.choice(["randperm", "shuffle"]), trailing_empty_page=r.random() < 0.5, k=1, L=2)
+    g = c.to(DEV)
+    hq, mp = hkv * G, c.max_pages
+    what = f"seed {seed}: B={B} hq={hq} hkv={hkv} {dtype} pages {mp}"
+    assert K.paged_decode_scores_supported(B, hq, hkv, mp, False), what
+    dump = torch.full((B, hq, mp * 16), float("-inf"), device=DEV)
+    lse_d = torch.empty(B, hq, device=DEV)
+    o_d = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                         lse=lse_d, logits_dump=dump)
+    s_d = K.page_scores_from_logits(dump, g.kv_indptr, g.kv_last_page_len, mp, lse=lse_d)
+    lse = torch.empty(B, hq, device=DEV)
+    o, s = K.paged_decode_scores(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                                 max_pages_per_row=mp, lse=lse)
+    k = max(1, mp // 3)
+    i1, p1 = K.select_pages(s, g.kv_indptr, g.block_table, k, 2)
+    i0, p0 = K.select_pages(s_d, g.kv_indptr, g.block_table, k, 2)
+    torch.cuda.synchronize()
+    close_attn(o, o_d, what + " vs dump launch")
+    assert torch.allclose(lse, lse_d, atol=1e-4, rtol=1e-5), what
+    rel = ((s - s_d).abs() / s_d.abs().clamp_min(1e-30)).max().item()
+    assert rel < 1e-5, what + f" scores vs dump path {rel}"
+    o_ref, lse_ref = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                                              c.sm_scale)
+    close_attn(o, o_ref, what + " vs oracle")
+    x = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, c.sm_scale, mp * 16)
+    ref_s = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
+    got = s.cpu().double()
+    rel = (got - ref_s).abs() / ref_s.abs().clamp_min(1e-30)
+    rel[ref_s == 0] = got[ref_s == 0].abs()
+    assert rel.max().item() < 1e-4, what + f" scores vs oracle {rel.max().item()}"
+    assert torch.equal(p1, p0), what
+    n = int(p1[-1].item())
+    if not torch.equal(i1[:n], i0[:n]):  # only keys equal to within the scores' 1e-5 may swap
+        sc = s_d.cpu()
+        for b in range(B):
+            a = i1[int(p1[b]):int(p1[b + 1])].tolist()
+            z = i0[int(p0[b]):int(p0[b + 1])].tolist()
+            if a != z:
+                bt = c.block_table[b].tolist()
+                vals = [float(sc[b, bt.index(pg)]) for pg in set(a) ^ set(z)]
+                assert max(vals) - min(vals) <= 1e-5 * max(abs(v) for v in vals), what + f" row {b}"

@@ -25,6 +25,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -165,6 +166,18 @@ def warm_up(torch, run, seconds: float = 0.25):
     torch.cuda.synchronize()
 
 
+def gather_probe():
+    """The measurement probe library (``delta_amd/_delta_probe.so``), or None when not built."""
+    path = os.path.join(ROOT, "delta_amd", "_delta_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.delta_probe_gather_floor.restype = ctypes.c_int
+    lib.delta_probe_gather_floor.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
 def kernel_roofline(torch, reps: int = 60, n_rot: int = 30):
     """Time each hot-path kernel at the config-3 layer shape (graph replays, HIP events on the
     replay stream).
@@ -250,6 +263,20 @@ def kernel_roofline(torch, reps: int = 60, n_rot: int = 30):
         timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
                                                        max_pages_per_row=c.k, subset=True)),
         ntok_sub * 2 * row_kv + qo + B * c.k * 4, "K+V of the 128 selected pages/row, q, o, page ids")
+    probe = gather_probe()
+    if probe is not None:
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+
+        def floor(c, d, l, s, i, p):
+            rc = probe.delta_probe_gather_floor(
+                ctypes.c_void_p(c.kv_cache.data_ptr()), ctypes.c_int64(c.kv_cache.shape[0]),
+                ctypes.c_void_p(p.data_ptr()), ctypes.c_void_p(i.data_ptr()), B, hkv,
+                ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc:
+                raise RuntimeError(f"gather probe failed ({rc})")
+        # whole pages of the same selection, no arithmetic: the floor under the subset launch
+        add("gather floor (subset pages, no arithmetic)", timed(floor), B * c.k * 16 * 2 * row_kv,
+            "a bare gather of the subset launch's pages (K+V, whole pages) with its grid: the access pattern's own time")
     add("paged_decode_full_kernel",
         timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
                                                        c.kv_last_page_len, max_pages_per_row=mp)),
@@ -702,6 +729,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": dom["frac"], "traffic": profiled_traffic("paged_decode_subset_kernel<ROPE>"),
                      "algorithmic_bytes": dom["bytes"],
+                     "gather_floor_us": kern.get("gather floor (subset pages, no arithmetic)", {}).get("us"),
                      "kernel": "paged_decode_subset_kernel<ROPE> (delta_paged_decode_subset_append, the launch "
                                "of every selective layer in a decode step)"},
         "cpu_baseline": cpu,

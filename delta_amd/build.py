@@ -58,7 +58,30 @@ def build(verbose: bool = False, extra_flags=None) -> Path:
     if verbose and err.strip():
         print(err, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
+    build_probe(verbose)
     return LIB_PATH
+
+
+PROBE_SOURCES = ["probe_gather.hip"]
+PROBE_PATH = PKG_DIR / "_delta_probe.so"
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """The measurement probe bench.py loads beside the library (``_delta_probe.so``)."""
+    fd, tmp = tempfile.mkstemp(prefix=".delta_probe.", suffix=".so.tmp", dir=str(PKG_DIR))
+    os.close(fd)
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *[str(CSRC / s) for s in PROBE_SOURCES]]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        try:
+            os.unlink(tmp)
+        except OSError:
+            pass
+        raise RuntimeError(f"hipcc failed on the probe ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, PROBE_PATH)
+    return PROBE_PATH
 
 
 if __name__ == "__main__":

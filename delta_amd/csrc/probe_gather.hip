@@ -1,0 +1,58 @@
+// Measurement probe (bench.py only; not part of the delta_hip ABI): the bare gather of a decode
+// launch's pages, with no arithmetic, to put a floor under the attention kernels' times.
+//
+// Same grid and order as the head-major decode launches: block = (kv head, row), 16 waves,
+// wave w takes the row's pages w, w + 16, ...; per page-head it loads K (16 rows x 256 bytes)
+// and V with 16-byte nontemporal loads, lane (c, t) rows 4i + c at bytes 16t, the next page in
+// flight while the current one is folded into one xor.  Pages whose id is outside the cache
+// are skipped.  A value that no page produces is written only to keep the loads alive.
+#include "delta_common.h"
+
+namespace delta {
+namespace {
+
+constexpr int kWaves = 16;
+
+__global__ void __launch_bounds__(kWaves * 64)
+    gather_floor_kernel(const uint16_t *kv, int64_t num_pages, const int32_t *indptr, const int32_t *indices,
+                        int hkv, uint32_t *sink) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = lane >> 4, t = lane & 15;
+  const int64_t row = (int64_t)hkv * kHeadDim, page = 2 * kPageSize * row;
+  const int p0 = indptr[b], np = indptr[b + 1] - p0;
+  const int cnt = np > wave ? (np - wave + kWaves - 1) / kWaves : 0;
+  u32x4 r[8];
+  auto issue = [&](int it) {
+    int pid = indices[p0 + wave + kWaves * it];
+    pid = (pid >= 0 && (int64_t)pid < num_pages) ? pid : 0;
+    const uint16_t *base = kv + (int64_t)pid * page + (int64_t)h * kHeadDim;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = ld128_stream(base + (4 * i + c) * row + 8 * t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[4 + i] = ld128_stream(base + (kPageSize + 4 * i + c) * row + 8 * t);
+  };
+  uint32_t acc = 0;
+  if (cnt > 0) issue(0);
+  for (int it = 0; it < cnt; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc ^= r[i].x ^ r[i].y ^ r[i].z ^ r[i].w;
+    if (it + 1 < cnt) issue(it + 1);
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+}  // namespace
+}  // namespace delta
+
+extern "C" __attribute__((visibility("default"))) int delta_probe_gather_floor(
+    const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr, const int32_t *kv_indices, int batch,
+    int num_kv_heads, void *sink, hipStream_t stream) {
+  if (batch <= 0) return 0;
+  if (!kv_cache || !kv_indptr || !kv_indices || !sink || num_pages <= 0 || num_kv_heads <= 0 ||
+      ((uintptr_t)kv_cache & 15u))
+    return 1;
+  hipLaunchKernelGGL(delta::gather_floor_kernel, dim3(num_kv_heads, batch), dim3(delta::kWaves * 64), 0, stream,
+                     (const uint16_t *)kv_cache, num_pages, kv_indptr, kv_indices, num_kv_heads, (uint32_t *)sink);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}

@@ -81,6 +81,7 @@ struct RowInfo {
   int64_t p0;
   int np;
   int kv_len;
+  int last;  // last_page_len clamped to [0, 16]
 };
 
 __device__ __forceinline__ RowInfo row_info(const DecodeArgs &a, int b) {
@@ -95,6 +96,7 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs &a, int b) {
   r.p0 = p0;
   r.np = (int)(p1 - p0);
   r.kv_len = r.np > 0 ? (r.np - 1) * kPageSize + last : 0;
+  r.last = last;
   return r;
 }
 
@@ -275,6 +277,13 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     ri = row_info(a, b);
     j1 = ri.np;
   }
+  // (ROPE) The append CSR's row bounds, requested with the row's own bounds: the slot's page
+  // id below then needs no round trip of its own before the page stream starts.
+  int64_t ap_q0 = 0, ap_q1 = 0;
+  if (ROPE) {
+    ap_q0 = a.ap_indptr[b];
+    ap_q1 = a.ap_indptr[b + 1];
+  }
 
   // Query fragments (B operand of q.K) for the two 64-d halves sp: column t holds head t % 8
   // at d = 64 sp + 32 (t / 8) + 8c + [0, 8); zero for heads past the group.
@@ -409,18 +418,21 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   constexpr bool kRopeUnderFirstPage = !WITH_DUMP;
   if (ROPE && !kRopeUnderFirstPage) rope_prologue();
   int ids = count > 0 ? load_ids(0) : -1;
+  if (ROPE && kRopeUnderFirstPage) {
+    // The token's k, v and position were requested before the page ids: settle them here
+    // (the wait leaves the ids in flight), so that no wait in the RoPE prologue, which runs
+    // under the first page's loads, also waits for that page.
+    asm volatile("" ::"v"(kraw), "v"(vraw), "v"(rpos));
+  }
   if (ROPE) {
     // The append slot, with delta_append_kv's checks (a row without a valid slot appends
-    // nothing).  Its page id is a dependent load: issued after the page ids, so that no wait
-    // on the row's bounds (scalar loads complete out of order) also waits for it.
+    // nothing; last_page_len is shared with the attention CSR).  Its page id, a dependent
+    // load, goes out right after the page ids: the first page's loads wait only for those.
     __builtin_amdgcn_sched_barrier(0);
-    const int64_t q0 = a.ap_indptr[b], q1 = a.ap_indptr[b + 1];
-    if (q0 >= 0 && q1 > q0 && q1 <= a.ap_indices_len) {
-      int lp = a.last_page_len[b];
-      lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
-      const int tp = (int)(q1 - q0 - 1) * kPageSize + lp - 1;  // the new token's position
+    if (ap_q0 >= 0 && ap_q1 > ap_q0 && ap_q1 <= a.ap_indices_len) {
+      const int tp = (int)(ap_q1 - ap_q0 - 1) * kPageSize + ri.last - 1;  // the new token's position
       if (tp >= 0) {
-        ap_pid = a.ap_indices[q0 + tp / kPageSize];
+        ap_pid = a.ap_indices[ap_q0 + tp / kPageSize];
         ap_slot = tp % kPageSize;
       }
     }

@@ -27,6 +27,7 @@
 // HBM bytes per launch (algorithmic): K and V of every attended token once,
 // q and o once, the page indices once (+ the fp32 logits when dumping).
 #include <mutex>
+#include <type_traits>
 
 #include "delta_common.h"
 
@@ -761,26 +762,32 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     const int g = WITH_V ? (idx / kHeadDim) % G : idx % G;
     const int dd = WITH_V ? idx % kHeadDim : 0;
     float M = -INFINITY, L = 0.f, A = 0.f;
-    if (kOwnMerge && R == kMaxWaves) {
-      // Head-major launch (one head, 16 waves): unrolled, so all the LDS reads issue
-      // together (same sums in the same order as the loop below).
-      float mw[kMaxWaves], lw[kMaxWaves], aw[kMaxWaves];
+    // R waves per head unrolled (head-major launches: 16, or 8 when unsplit), so all the LDS
+    // reads issue together (same sums in the same order as the loop below).
+    auto unrolled = [&](auto rw) {
+      constexpr int RW = decltype(rw)::value;
+      float mw[RW], lw[RW], aw[RW];
 #pragma unroll
-      for (int r = 0; r < kMaxWaves; ++r) {
+      for (int r = 0; r < RW; ++r) {
         const int w = r * hb + hl;
         mw[r] = s_ml[(w * G + g) * 2];
         lw[r] = s_ml[(w * G + g) * 2 + 1];
         aw[r] = s_acc[(w * G + g) * kHeadDim + dd];
       }
 #pragma unroll
-      for (int r = 0; r < kMaxWaves; ++r) M = fmaxf(M, mw[r]);
+      for (int r = 0; r < RW; ++r) M = fmaxf(M, mw[r]);
       const float Mr = M == -INFINITY ? 0.f : M;
 #pragma unroll
-      for (int r = 0; r < kMaxWaves; ++r) {
+      for (int r = 0; r < RW; ++r) {
         const float sc = fast_exp2(mw[r] - Mr);
         L = fmaf(lw[r], sc, L);
         A = fmaf(aw[r], sc, A);
       }
+    };
+    if (kOwnMerge && R == kMaxWaves) {
+      unrolled(std::integral_constant<int, kMaxWaves>());
+    } else if (kOwnMerge && R == kMaxWaves / 2) {
+      unrolled(std::integral_constant<int, kMaxWaves / 2>());
     } else {
       for (int r = 0; r < R; ++r) M = fmaxf(M, s_ml[((r * hb + hl) * G + g) * 2]);
       const float Mr = M == -INFINITY ? 0.f : M;
@@ -1006,7 +1013,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 
 // Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
 // captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads
-// (hb * R = 16 waves):
+// (hb * R = 16 waves, 8 for unsplit head-major launches):
 //   page-major (hb = Hkv): the Hkv waves of one page slot read all heads of a page
 //     together (whole 32 KiB K and V runs: ~5.9 TB/s on MI355X), and the split count
 //     brings the launch to 4096 waves (4 per SIMD on 256 CUs), never below 2 pages per
@@ -1014,7 +1021,10 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   head-major (hb = 1) when the (row, kv head) pairs alone give >= 256 blocks and the
 //     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
 //     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
-//     faster page-major gather repays the merge;
+//     faster page-major gather repays the merge.  These blocks hold 8 waves: a CU still
+//     keeps 64 KiB of pages in flight (enough for a bare gather to stream at full rate),
+//     while the block's closing merge of its waves' partials and the fused RoPE prologue,
+//     which every wave repeats, take half as long as with 16;
 //   head-major with splits (grid (units, Hkv)) for attention launches of fewer than 256
 //     pairs (small batches): the launch still reaches 256 blocks, down to one page per
 //     wave, and each unit's partials cover one kv head, so the partials and the merge's
@@ -1023,6 +1033,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   Work units hold at most kMaxChunk pages (64 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
+constexpr int kHeadMajorWaves = 8;
 constexpr int64_t kHeadMajorPageHeads = 65536;
 constexpr int kMaxChunk = 128;
 
@@ -1033,6 +1044,7 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
   if (small) h = 1;
   int R = h > 0 ? kMaxWaves / h : 1;
   if (R < 1) R = 1;
+  if (h == 1 && !small) R = kHeadMajorWaves;
   const int w = h * R;
   const int groups = h > 0 ? hkv / h : 1;
   int64_t ns = 1;
@@ -1044,6 +1056,7 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     if (ns < 1) ns = 1;
     if (ns > 1024) ns = 1024;
   }
+  if (h == 1 && !small) ns = 1;
   int64_t ch = max_pages > 0 ? ceil_div(max_pages, ns) : 1;
   if (ns > 1 && ch > kMaxChunk) {
     ch = kMaxChunk;

@@ -36,6 +36,7 @@ namespace delta {
 namespace {
 
 constexpr int kMaxWaves = 16;  // waves per block (a block never exceeds one CU's 16 slots at <= 128 VGPRs)
+constexpr int kHeadMajorWaves = 4;  // waves per block of an unsplit head-major launch (decode_plan)
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -762,7 +763,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     const int g = WITH_V ? (idx / kHeadDim) % G : idx % G;
     const int dd = WITH_V ? idx % kHeadDim : 0;
     float M = -INFINITY, L = 0.f, A = 0.f;
-    // R waves per head unrolled (head-major launches: 16, or 8 when unsplit), so all the LDS
+    // R waves per head unrolled (head-major launches: 16, or 4 when unsplit), so all the LDS
     // reads issue together (same sums in the same order as the loop below).
     auto unrolled = [&](auto rw) {
       constexpr int RW = decltype(rw)::value;
@@ -786,8 +787,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     };
     if (kOwnMerge && R == kMaxWaves) {
       unrolled(std::integral_constant<int, kMaxWaves>());
-    } else if (kOwnMerge && R == kMaxWaves / 2) {
-      unrolled(std::integral_constant<int, kMaxWaves / 2>());
+    } else if (kOwnMerge && R == kHeadMajorWaves) {
+      unrolled(std::integral_constant<int, kHeadMajorWaves>());
     } else {
       for (int r = 0; r < R; ++r) M = fmaxf(M, s_ml[((r * hb + hl) * G + g) * 2]);
       const float Mr = M == -INFINITY ? 0.f : M;
@@ -1013,7 +1014,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 
 // Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
 // captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads
-// (hb * R = 16 waves, 8 for unsplit head-major launches):
+// (hb * R = 16 waves, 4 for unsplit head-major launches):
 //   page-major (hb = Hkv): the Hkv waves of one page slot read all heads of a page
 //     together (whole 32 KiB K and V runs: ~5.9 TB/s on MI355X), and the split count
 //     brings the launch to 4096 waves (4 per SIMD on 256 CUs), never below 2 pages per
@@ -1021,10 +1022,12 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   head-major (hb = 1) when the (row, kv head) pairs alone give >= 256 blocks and the
 //     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
 //     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
-//     faster page-major gather repays the merge.  These blocks hold 8 waves: a CU still
-//     keeps 64 KiB of pages in flight (enough for a bare gather to stream at full rate),
-//     while the block's closing merge of its waves' partials and the fused RoPE prologue,
-//     which every wave repeats, take half as long as with 16;
+//     faster page-major gather repays the merge.  These blocks hold 4 waves (one per SIMD):
+//     32 KiB of pages in flight per CU already stream at full rate (a bare gather of the
+//     config-3 subset pages: 41.4 us with 4 waves of one page each, 42.0 with 8, 42.2 with
+//     16), while the block's closing merge of its waves' partials and the fused RoPE
+//     prologue, which every wave repeats, shrink with the wave count (subset launch 44.8 ->
+//     44.4 -> 43.6 us for 16 -> 8 -> 4 waves);
 //   head-major with splits (grid (units, Hkv)) for attention launches of fewer than 256
 //     pairs (small batches): the launch still reaches 256 blocks, down to one page per
 //     wave, and each unit's partials cover one kv head, so the partials and the merge's
@@ -1033,7 +1036,6 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   Work units hold at most kMaxChunk pages (64 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
-constexpr int kHeadMajorWaves = 8;
 constexpr int64_t kHeadMajorPageHeads = 65536;
 constexpr int kMaxChunk = 128;
 

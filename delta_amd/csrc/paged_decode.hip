@@ -1014,7 +1014,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 
 // Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
 // captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads
-// (hb * R = 16 waves, 4 for unsplit head-major launches):
+// (hb * R = 16 waves, 4 for head-major launches):
 //   page-major (hb = Hkv): the Hkv waves of one page slot read all heads of a page
 //     together (whole 32 KiB K and V runs: ~5.9 TB/s on MI355X), and the split count
 //     brings the launch to 4096 waves (4 per SIMD on 256 CUs), never below 2 pages per
@@ -1029,10 +1029,11 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //     prologue, which every wave repeats, shrink with the wave count (subset launch 44.8 ->
 //     44.4 -> 43.6 us for 16 -> 8 -> 4 waves);
 //   head-major with splits (grid (units, Hkv)) for attention launches of fewer than 256
-//     pairs (small batches): the launch still reaches 256 blocks, down to one page per
-//     wave, and each unit's partials cover one kv head, so the partials and the merge's
-//     reads are 1/Hkv of page-major's (config 4 subset: 20.6 -> 15.5 us).  Dump launches
-//     (planner, scorer) keep page-major, which measured faster for them.
+//     pairs (small batches): the launch still reaches 256 blocks, and each unit's partials
+//     cover one kv head, so the partials and the merge's reads are 1/Hkv of page-major's
+//     (config 4 subset: 20.6 -> 15.5 us); its 4-wave blocks take 4 pages per wave at
+//     config 4 (14.8 -> 14.1 us against 16 waves of one page; twice the splits: 16.2).
+//     Dump launches (planner, scorer) keep page-major, which measured faster for them.
 //   Work units hold at most kMaxChunk pages (64 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
@@ -1040,14 +1041,13 @@ constexpr int64_t kHeadMajorPageHeads = 65536;
 constexpr int kMaxChunk = 128;
 
 void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int *waves, int *hb, int *chunk) {
-  int h = hkv;
-  if ((int64_t)batch * hkv >= kHeadMajorPairs && (int64_t)batch * hkv * max_pages <= kHeadMajorPageHeads) h = 1;
+  const bool unsplit = (int64_t)batch * hkv >= kHeadMajorPairs &&
+                       (int64_t)batch * hkv * max_pages <= kHeadMajorPageHeads;
   const bool small = !dump && (int64_t)batch * hkv < kHeadMajorPairs;
-  if (small) h = 1;
+  const int h = (unsplit || small) ? 1 : hkv;
   int R = h > 0 ? kMaxWaves / h : 1;
   if (R < 1) R = 1;
-  if (h == 1 && !small) R = kHeadMajorWaves;
-  const int w = h * R;
+  const int w = h * R;  // the split count is sized for 16-wave blocks
   const int groups = h > 0 ? hkv / h : 1;
   int64_t ns = 1;
   if (batch > 0 && max_pages > 0) {
@@ -1058,14 +1058,19 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     if (ns < 1) ns = 1;
     if (ns > 1024) ns = 1024;
   }
-  if (h == 1 && !small) ns = 1;
+  if (unsplit || small) {
+    // Head-major blocks hold kHeadMajorWaves waves (one per SIMD): unsplit, or with the splits
+    // of a 16-wave plan (each wave then takes 4x the pages).
+    R = kHeadMajorWaves;
+    if (unsplit) ns = 1;
+  }
   int64_t ch = max_pages > 0 ? ceil_div(max_pages, ns) : 1;
   if (ns > 1 && ch > kMaxChunk) {
     ch = kMaxChunk;
     ns = ceil_div(max_pages, ch);
   }
   *nsplit = (int)ns;
-  *waves = w;
+  *waves = h * R;
   *hb = h;
   *chunk = (int)(ch < 1 ? 1 : ch);
 }

@@ -1,17 +1,19 @@
 // Measurement probe (bench.py only; not part of the delta_hip ABI): the bare gather of a decode
 // launch's pages, with no arithmetic, to put a floor under the attention kernels' times.
 //
-// Same grid and order as the head-major decode launches: block = (kv head, row), 16 waves,
-// wave w takes the row's pages w, w + 16, ...; per page-head it loads K (16 rows x 256 bytes)
-// and V with 16-byte nontemporal loads, lane (c, t) rows 4i + c at bytes 16t, the next page in
-// flight while the current one is folded into one xor.  Pages whose id is outside the cache
-// are skipped.  A value that no page produces is written only to keep the loads alive.
+// Same grid and page order as the unsplit head-major decode launches: block = (kv head, row) of
+// kWaves waves, wave w takes the row's pages w, w + kWaves, ...; the wave's page ids are loaded
+// up front, 64 per register (lane i holds iteration 64 chunk + i), as the attention kernels do.
+// Per page-head a wave loads K (16 rows x 256 bytes) and V with 16-byte nontemporal loads,
+// lane (c, t) rows 4i + c at bytes 16t, the next page in flight while the current one is
+// folded into one xor.  Page ids outside the cache read page 0.  A value that no page produces
+// is written only to keep the loads alive.
 #include "delta_common.h"
 
 namespace delta {
 namespace {
 
-constexpr int kWaves = 16;
+constexpr int kWaves = 4;
 
 __global__ void __launch_bounds__(kWaves * 64)
     gather_floor_kernel(const uint16_t *kv, int64_t num_pages, const int32_t *indptr, const int32_t *indices,
@@ -22,10 +24,15 @@ __global__ void __launch_bounds__(kWaves * 64)
   const int64_t row = (int64_t)hkv * kHeadDim, page = 2 * kPageSize * row;
   const int p0 = indptr[b], np = indptr[b + 1] - p0;
   const int cnt = np > wave ? (np - wave + kWaves - 1) / kWaves : 0;
+  auto load_ids = [&](int it0) -> int {
+    const int it = it0 + lane;
+    int pid = it < cnt ? indices[p0 + wave + kWaves * it] : 0;
+    return (pid >= 0 && (int64_t)pid < num_pages) ? pid : 0;
+  };
+  int ids = load_ids(0);
   u32x4 r[8];
   auto issue = [&](int it) {
-    int pid = indices[p0 + wave + kWaves * it];
-    pid = (pid >= 0 && (int64_t)pid < num_pages) ? pid : 0;
+    const int pid = __builtin_amdgcn_readlane(ids, it & 63);
     const uint16_t *base = kv + (int64_t)pid * page + (int64_t)h * kHeadDim;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = ld128_stream(base + (4 * i + c) * row + 8 * t);
@@ -37,7 +44,10 @@ __global__ void __launch_bounds__(kWaves * 64)
   for (int it = 0; it < cnt; ++it) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc ^= r[i].x ^ r[i].y ^ r[i].z ^ r[i].w;
-    if (it + 1 < cnt) issue(it + 1);
+    if (it + 1 < cnt) {
+      if (((it + 1) & 63) == 0) ids = load_ids(it + 1);  // the next 64 page ids
+      issue(it + 1);
+    }
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;
 }

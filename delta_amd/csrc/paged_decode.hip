@@ -1175,9 +1175,12 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   int waves;
   decode_plan(batch, hkv, max_pages, dump != nullptr, &a.nsplit, &waves, &a.hb, &a.chunk);
   if (tokmax) {  // head-major, unsplit: each block ends with its head's final lse
+    // 4 waves (one per SIMD), as the other unsplit head-major launches: config-3 planner
+    // 176.1 -> 169.7 us and K-only scorer 92.2 -> 88.5 us against 16 waves (8 waves: 173.3 /
+    // 91.7).
     a.nsplit = 1;
     a.hb = 1;
-    waves = kMaxWaves;
+    waves = kHeadMajorWaves;
     a.chunk = max_pages;
   }
   a.sm_scale = sm_scale;

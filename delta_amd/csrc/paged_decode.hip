@@ -1013,12 +1013,18 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 }  // namespace
 
 // Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
-// captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads
-// (hb * R = 16 waves, 4 for head-major launches):
+// captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads:
+// one wave per SIMD for head-major launches (4 waves), and R = max(1, 4 / Hkv) waves per head
+// for page-major ones, with split counts sized for 16-wave blocks.  Fewer waves per block
+// shorten the block's closing merge and the prologue every wave repeats, and a CU keeps
+// enough pages in flight regardless (a bare gather streams at full rate from 4 waves of one
+// page each):
 //   page-major (hb = Hkv): the Hkv waves of one page slot read all heads of a page
 //     together (whole 32 KiB K and V runs: ~5.9 TB/s on MI355X), and the split count
-//     brings the launch to 4096 waves (4 per SIMD on 256 CUs), never below 2 pages per
-//     wave; splits cost a merge launch (~5 us);
+//     brings a 16-wave plan to 4096 waves (4 per SIMD on 256 CUs), never below 2 pages per
+//     wave; splits cost a merge launch (~5 us).  Run with one wave per head at Hkv = 8
+//     (config-3 full 166.6 -> 163.4 us, planner with dump 192.9 -> 185.1 us, config-2
+//     planner 99.9 -> 94.3 us);
 //   head-major (hb = 1) when the (row, kv head) pairs alone give >= 256 blocks and the
 //     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
 //     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
@@ -1034,7 +1040,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //     (config 4 subset: 20.6 -> 15.5 us); its 4-wave blocks take 4 pages per wave at
 //     config 4 (14.8 -> 14.1 us against 16 waves of one page; twice the splits: 16.2).
 //     Dump launches (planner, scorer) keep page-major, which measured faster for them.
-//   Work units hold at most kMaxChunk pages (64 per wave at Hkv = 8), so a ragged batch is cut
+//   Work units hold at most kMaxChunk pages (128 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
 constexpr int64_t kHeadMajorPageHeads = 65536;
@@ -1063,6 +1069,8 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     // of a 16-wave plan (each wave then takes 4x the pages).
     R = kHeadMajorWaves;
     if (unsplit) ns = 1;
+  } else {
+    R = kHeadMajorWaves / h > 1 ? kHeadMajorWaves / h : 1;
   }
   int64_t ch = max_pages > 0 ? ceil_div(max_pages, ns) : 1;
   if (ns > 1 && ch > kMaxChunk) {

@@ -1026,9 +1026,11 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //     (config-3 full 166.6 -> 163.4 us, planner with dump 192.9 -> 185.1 us, config-2
 //     planner 99.9 -> 94.3 us);
 //   head-major (hb = 1) when the (row, kv head) pairs alone give >= 256 blocks and the
-//     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~0.5 GB): no split
-//     and no merge launch, at the per-head gather's ~5.6 TB/s.  Past that size the
-//     faster page-major gather repays the merge.  These blocks hold 4 waves (one per SIMD):
+//     launch reads at most kHeadMajorPageHeads page-heads (8 KiB each, ~2 GB): no split and
+//     no merge launch (config-3 full attention 170.6 -> 159.6 us against page-major units
+//     and their merge).  Past that size, where a ragged batch's longest rows would leave
+//     most blocks idle at the end, page-major work units balance better (config 5 full
+//     attention 1545 us page-major, 1739 us head-major).  These blocks hold 4 waves (one per SIMD):
 //     32 KiB of pages in flight per CU already stream at full rate (a bare gather of the
 //     config-3 subset pages: 41.4 us with 4 waves of one page each, 42.0 with 8, 42.2 with
 //     16), while the block's closing merge of its waves' partials and the fused RoPE
@@ -1043,7 +1045,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   Work units hold at most kMaxChunk pages (128 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
-constexpr int64_t kHeadMajorPageHeads = 65536;
+constexpr int64_t kHeadMajorPageHeads = 262144;
 constexpr int kMaxChunk = 128;
 
 void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int *waves, int *hb, int *chunk) {

@@ -52,13 +52,15 @@ def test_queries_without_gpu(lib):
     assert lib.delta_abi_version() == 200
     assert lib.delta_last_error() == b""
     # split heuristic: deterministic, >= 1; the larger of the attention and the dump plans.
-    # Page-major blocks (Hkv heads x R waves = 16) split up to 4096 waves in total, >= 2 pages
-    # per wave; head-major blocks (one kv head, 16 waves) when batch*Hkv >= 256 and
-    # batch*Hkv*max_pages <= 65536 never split; attention launches with batch*Hkv < 256 use
-    # head-major blocks split to 256 blocks, >= 1 page per wave (fewer splits than page-major).
+    # Page-major splits are sized for 16-wave blocks (Hkv heads x R waves): up to 4096 waves in
+    # total, >= 2 pages per wave; head-major blocks (one kv head) when batch*Hkv >= 256 and
+    # batch*Hkv*max_pages <= 262144 never split; attention launches with batch*Hkv < 256 use
+    # head-major blocks split to 256 blocks (fewer splits than page-major).
     assert lib.delta_decode_num_splits(32, 8, 128) == 1        # config 3 subset: head-major
     assert lib.delta_decode_num_splits(64, 4, 128) == 1        # head-major
-    assert lib.delta_decode_num_splits(32, 8, 513) == 8        # config 3 full: page-major, 256 blocks
+    assert lib.delta_decode_num_splits(32, 8, 513) == 1        # config 3 full: head-major
+    # past the head-major size: page-major, 8 splits (256 blocks) of 129 pages, over the 128-page unit: 9
+    assert lib.delta_decode_num_splits(32, 8, 1025) == 9
     assert lib.delta_decode_num_splits(1024, 8, 2048) == 1
     assert lib.delta_decode_num_splits(8, 8, 128) == 32        # config 2
     assert lib.delta_decode_num_splits(4, 4, 4096) == 64       # config 4: R = 4
@@ -68,7 +70,7 @@ def test_queries_without_gpu(lib):
     assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 128) == 0
     # partials (m, l, acc[128]) per (row, q head, split)
     # partials (m, l, acc) per (unit, q head) + each row's first unit (256-byte aligned)
-    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 513) == 32 * 32 * 8 * 130 * 4 + 256
+    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 1025) == 32 * 32 * 9 * 130 * 4 + 256
     # config 5 (ragged up to 2049 pages): units of at most 128 pages, 17 for the longest row
     assert lib.delta_decode_num_splits(128, 8, 2049) == 17
     assert lib.delta_page_score_workspace_bytes(32, 32) == 32 * 32 * 4

@@ -43,8 +43,9 @@ def _run(c, noalloc):
 
 def test_noalloc_entry_point_matches_workspace_entry_point():
     cases = [
-        # the config-3 planner shape (page-major split, logits dump), then a smaller ragged one
-        make_case(batch=32, hq=32, hkv=8, kv_lens=8192, dtype=torch.bfloat16, seed=21, page_order="shuffle",
+        # a 16-row planner launch at the config-3 row shape (page-major split, logits dump), then a
+        # smaller ragged one
+        make_case(batch=16, hq=32, hkv=8, kv_lens=8192, dtype=torch.bfloat16, seed=21, page_order="shuffle",
                   device=DEV),
         make_case(batch=3, hq=28, hkv=4, kv_lens=[5000, 777, 12000], dtype=torch.bfloat16, seed=22, device=DEV),
     ]

@@ -612,6 +612,22 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     }
   };
 
+  // The new token's rotated k and v go into its cache slot from the LDS copy of the first wave
+  // of each kv head (rslot 0: 32 lanes, one 16-byte chunk each), once per (row, kv head) (split 0
+  // of a split row), as soon as that wave's page loop is done: the stores overlap the block's
+  // merge instead of following it.  (Issued inside the loop they cost more: stores share vmcnt
+  // with the page loads, so the next page's wait would also wait for them.)  No wave of the
+  // launch reads the slot's bytes from the cache (the waves attending that page take the row
+  // from LDS).
+  auto write_own_slot = [&]() {
+    if (ROPE && rslot == 0 && lane < 32 && ap_pid >= 0 && (int64_t)ap_pid < a.num_pages &&
+        (a.nsplit == 1 || split == 0)) {
+      const int which = lane >> 4, r = lane & 15;  // 0 = K, 1 = V; 16-byte chunk r
+      uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
+                      (int64_t)h * kHeadDim + 8 * r;
+      st128(dst, *reinterpret_cast<const u32x4 *>(tok_lds + which * (kHeadDim / 2) + 4 * r));
+    }
+  };
   u32x4 kf[4], vf[4];
   if (WITH_V) {
     // Attention: one page in flight (K and V) while the current one is processed.
@@ -625,6 +641,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       page_body(gi, kf, vf, pid, pidn, more);
       pid = pidn;
     }
+    if (ROPE) write_own_slot();
   } else {
     // K-only scorer: no V tiles or accumulators, so two pages of K are in flight -- pages
     // alternate between the register sets kf and kg, each reloaded two pages ahead.
@@ -645,21 +662,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     }
   }
 
-  // One block per (row, kv head group) writes the new token's rotated k and v into the cache
-  // slot, 16-byte chunk r % 16 of head head0 + r / 16, from the LDS slot of wave r / 16 (which
-  // works on that head); a block barrier after the waves' loops orders those LDS stores.
-  auto write_append_slot = [&]() {
-    if (ROPE && ap_pid >= 0 && (int64_t)ap_pid < a.num_pages && (a.nsplit == 1 || split == 0)) {
-      for (int ch = threadIdx.x; ch < 2 * hb * (kHeadDim / 8); ch += blockDim.x) {
-        const int which = ch >= hb * (kHeadDim / 8);  // 0 = K, 1 = V
-        const int r = which ? ch - hb * (kHeadDim / 8) : ch;
-        const uint32_t *src = rope_slots() + (r >> 4) * kHeadDim + which * (kHeadDim / 2) + 4 * (r & 15);
-        uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
-                        (int64_t)(head0 + (r >> 4)) * kHeadDim + 8 * (r & 15);
-        st128(dst, *reinterpret_cast<const u32x4 *>(src));
-      }
-    }
-  };
   // Per-token maxima of the row's logits in LDS (TOKMAX): max_g 2^(x_g log2 e - lse2_g).
   auto write_tokmax = [&]() {
     const float *lse2 = smem + tokmax_lds_header<G>() - 16;
@@ -728,7 +730,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       const float ov = L > 0.f ? A / L : 0.f;
       a.o[(int64_t)b * a.o_stride_b + (int64_t)(h * G + g) * a.o_stride_h + dd] = (uint16_t)E::from_float(ov);
     }
-    write_append_slot();
     return;
   }
 
@@ -817,7 +818,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       }
     }
   }
-  write_append_slot();
   if (TOKMAX) {
     __syncthreads();
     write_tokmax();

@@ -121,6 +121,13 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Scalar (s_load) read of a word the kernel never writes, at a wave-uniform index: the constant
+// address space makes the compiler use the scalar data cache path, whose waits (lgkmcnt) are
+// independent of the vector loads in flight.
+__device__ __forceinline__ int ld_scalar(const int32_t *p, int64_t i) {
+  typedef const __attribute__((address_space(4))) int32_t *cptr;
+  return ((cptr)p)[i];
+}
 
 // Wave-wide inclusive prefix sum of a 0/1 flag via ballot (wave64).
 __device__ __forceinline__ int wave_prefix_exclusive(bool flag, int *total) {

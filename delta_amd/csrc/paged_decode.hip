@@ -280,11 +280,14 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     j1 = ri.np;
   }
   // (ROPE) The append CSR's row bounds, requested with the row's own bounds: the slot's page
-  // id below then needs no round trip of its own before the page stream starts.
+  // id below then needs no round trip of its own before the page stream starts.  Scalar loads:
+  // their waits (lgkmcnt) never wait for page data, as a pending vector load before the page
+  // loop would make each page's test against the slot wait for all of its K and V.
   int64_t ap_q0 = 0, ap_q1 = 0;
   if (ROPE) {
-    ap_q0 = a.ap_indptr[b];
-    ap_q1 = a.ap_indptr[b + 1];
+    const int bu = uniform(b);
+    ap_q0 = ld_scalar(a.ap_indptr, bu);
+    ap_q1 = ld_scalar(a.ap_indptr, bu + 1);
   }
 
   // Query fragments (B operand of q.K) for the two 64-d halves sp: column t holds head t % 8
@@ -432,9 +435,9 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     // load, goes out right after the page ids: the first page's loads wait only for those.
     __builtin_amdgcn_sched_barrier(0);
     if (ap_q0 >= 0 && ap_q1 > ap_q0 && ap_q1 <= a.ap_indices_len) {
-      const int tp = (int)(ap_q1 - ap_q0 - 1) * kPageSize + ri.last - 1;  // the new token's position
+      const int tp = (int)(ap_q1 - ap_q0 - 1) * kPageSize + uniform(ri.last) - 1;  // the new token's position
       if (tp >= 0) {
-        ap_pid = a.ap_indices[ap_q0 + tp / kPageSize];
+        ap_pid = ld_scalar(a.ap_indices, ap_q0 + tp / kPageSize);
         ap_slot = tp % kPageSize;
       }
     }

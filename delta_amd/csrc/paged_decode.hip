@@ -1017,8 +1017,9 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 
 // Launch shape for a (batch, kv heads, max pages) problem, from its arguments only (so a
 // captured graph keeps a valid shape).  A block holds R waves per kv head over hb heads:
-// one wave per SIMD for head-major launches (4 waves), and R = max(1, 4 / Hkv) waves per head
-// for page-major ones, with split counts sized for 16-wave blocks.  Fewer waves per block
+// one wave per SIMD for unsplit head-major launches (4 waves) and for small ones whose waves
+// take at most 8 pages per unit, and R = max(1, 4 / Hkv) waves per head for page-major ones,
+// with split counts sized for 16-wave blocks.  Fewer waves per block
 // shorten the block's closing merge and the prologue every wave repeats, and a CU keeps
 // enough pages in flight regardless (a bare gather streams at full rate from 4 waves of one
 // page each):
@@ -1042,8 +1043,8 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   head-major with splits (grid (units, Hkv)) for attention launches of fewer than 256
 //     pairs (small batches): the launch still reaches 256 blocks, and each unit's partials
 //     cover one kv head, so the partials and the merge's reads are 1/Hkv of page-major's
-//     (config 4 subset: 20.6 -> 15.5 us); its 4-wave blocks take 4 pages per wave at
-//     config 4 (14.8 -> 14.1 us against 16 waves of one page; twice the splits: 16.2).
+//     (config 4 subset: 20.6 -> 15.5 us); 4-wave blocks take 4 pages per wave at config 4
+//     (14.8 -> 14.1 us against 16 waves of one page; twice the splits: 16.2).
 //     Dump launches (planner, scorer) keep page-major, which measured faster for them.
 //   Work units hold at most kMaxChunk pages (128 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
@@ -1069,12 +1070,10 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     if (ns < 1) ns = 1;
     if (ns > 1024) ns = 1024;
   }
-  if (unsplit || small) {
-    // Head-major blocks hold kHeadMajorWaves waves (one per SIMD): unsplit, or with the splits
-    // of a 16-wave plan (each wave then takes 4x the pages).
+  if (unsplit) {
     R = kHeadMajorWaves;
-    if (unsplit) ns = 1;
-  } else {
+    ns = 1;
+  } else if (!small) {
     R = kHeadMajorWaves / h > 1 ? kHeadMajorWaves / h : 1;
   }
   int64_t ch = max_pages > 0 ? ceil_div(max_pages, ns) : 1;
@@ -1082,6 +1081,11 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     ch = kMaxChunk;
     ns = ceil_div(max_pages, ch);
   }
+  // Small launches: 4-wave blocks while a wave's share of a unit stays at <= 8 pages (the
+  // config 2 and 4 subset launches), else 16 (the config-4 full attention, 128-page units:
+  // with 4 waves its full-cache engine step ran 5.4-5.6 -> 5.9-6.0 ms, though a launch timed
+  // alone was unchanged).
+  if (small && ceil_div(ch, (int64_t)kHeadMajorWaves) <= 8) R = kHeadMajorWaves;
   *nsplit = (int)ns;
   *waves = h * R;
   *hb = h;

@@ -53,9 +53,8 @@ struct DecodeArgs {
   float *dump;
   int64_t dump_stride_b, dump_stride_h;
   int dump_pages;   // pages per dump row the caller guarantees (max_pages_per_row)
-  float *part_acc;  // [unit][hkv][G][128]   (units < batch * nsplit)
-  float *part_ml;   // [unit][hkv][G][2]     (m in log2 units, l)
-  int32_t *unit_start;  // [batch]: first unit of each row (written by the row's unit 0)
+  float *part_acc;  // [row][split][hkv][G][128]   (split < nsplit; a row's units_of splits hold data)
+  float *part_ml;   // [row][split][hkv][G][2]     (m in log2 units, l)
   int batch, hq, hkv, nsplit;
   int chunk;        // pages per work unit (split launches)
   int hb;           // kv heads per block (hkv: page-major, 1: head-major)
@@ -273,12 +272,15 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     ri = row_info(a, b);
     j0 = split * a.chunk;
     j1 = split == nu - 1 ? ri.np : min(ri.np, j0 + a.chunk);
-    if (split == 0 && threadIdx.x == 0) a.unit_start[b] = unit;
   } else {
     b = blockIdx.y;
     ri = row_info(a, b);
     j1 = ri.np;
   }
+  // A split launch's partial slot (row, split), and whether this is the row's first split;
+  // both wave-uniform, so kept in scalar registers across the page loop.
+  const int pslot = uniform(b * a.nsplit + split);
+  const bool split0 = uniform(split) == 0;
   // (ROPE) The append CSR's row bounds, requested with the row's own bounds: the slot's page
   // id below then needs no round trip of its own before the page stream starts.  Scalar loads:
   // their waits (lgkmcnt) never wait for page data, as a pending vector load before the page
@@ -624,7 +626,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   // from LDS).
   auto write_own_slot = [&]() {
     if (ROPE && rslot == 0 && lane < 32 && ap_pid >= 0 && (int64_t)ap_pid < a.num_pages &&
-        (a.nsplit == 1 || split == 0)) {
+        (a.nsplit == 1 || split0)) {
       const int which = lane >> 4, r = lane & 15;  // 0 = K, 1 = V; 16-byte chunk r
       uint16_t *dst = a.kv_w + (((int64_t)ap_pid * 2 + which) * kPageSize + ap_slot) * (int64_t)a.hkv * kHeadDim +
                       (int64_t)h * kHeadDim + 8 * r;
@@ -813,7 +815,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
       if (TOKMAX) smem[tokmax_lds_header<G>() - 16 + g] = L > 0.f ? M + log2f(L) : -INFINITY;
     } else {
-      const int64_t pidx = ((int64_t)unit * a.hkv + hh) * G + g;
+      const int64_t pidx = ((int64_t)pslot * a.hkv + hh) * G + g;
       if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
       if (dd == 0) {
         a.part_ml[pidx * 2 + 0] = M;
@@ -864,10 +866,11 @@ __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_plan_tokmax_kerne
   decode_split_body<DT, G, true, false, ROPE, true>(a, smem);
 }
 
-// Combines the unit partials of one (row, q head): thread d of the block computes
+// Combines the split partials of one (row, q head): thread d of the block computes
 //   M = max_s m_s,  o[d] = sum_s A_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M),
 //   lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2
-// with the units' loads issued 16 at a time (all in flight together).
+// over the row's units_of splits.  Partials sit at (row, split), so the first 16 splits' loads
+// issue with the row bounds, not after them (splits the row does not have weigh nothing).
 template <int DT>
 __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
   using E = Elem<DT>;
@@ -875,19 +878,19 @@ __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, in
   const int hq = blockIdx.x % a.hq;
   const int h = hq / G, g = hq % G;
   const int dd = threadIdx.x;
-  const int u0 = a.unit_start[b];
   const int nu = units_of(a, b);
-  const int64_t stride = (int64_t)a.hkv * G;  // partial rows per unit
-  const int64_t p0 = ((int64_t)u0 * a.hkv + h) * G + g;
-  // Units in batches of 16 whose loads all issue together (clamped to the last unit, weight 0
-  // past it); the running sums move to a new maximum between batches.  One batch (<= 16
-  // units) is exactly the two-pass merge.
+  const int64_t stride = (int64_t)a.hkv * G;  // partial rows per split
+  const int64_t p0 = ((int64_t)b * a.nsplit * a.hkv + h) * G + g;
+  // Splits in batches of 16 whose loads all issue together (weight 0 past the row's last
+  // split; the first batch reads min(16, nsplit) slots regardless of the row's count); the
+  // running sums move to a new maximum between batches.  One batch (<= 16 splits) is exactly
+  // the two-pass merge.
   float M = -INFINITY, L = 0.f, A = 0.f;
-  for (int s0 = 0; s0 < nu; s0 += 16) {
+  auto merge16 = [&](int s0, int lim) {
     float mv[16], lv[16], av[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int64_t pidx = p0 + (int64_t)(s0 + i < nu ? s0 + i : nu - 1) * stride;
+      const int64_t pidx = p0 + (int64_t)(s0 + (i < lim ? i : 0)) * stride;
       mv[i] = a.part_ml[pidx * 2];
       lv[i] = a.part_ml[pidx * 2 + 1];
       av[i] = a.part_acc[pidx * kHeadDim + dd];
@@ -911,7 +914,9 @@ __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, in
       }
     }
     M = cm;
-  }
+  };
+  merge16(0, a.nsplit < 16 ? a.nsplit : 16);  // every row has at least one split
+  for (int s0 = 16; s0 < nu; s0 += 16) merge16(s0, nu - s0);
   a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(L > 0.f ? A / L : 0.f);
   if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
@@ -923,16 +928,20 @@ __global__ void __launch_bounds__(256) decode_merge_lse_kernel(DecodeArgs a, int
   if (idx >= a.batch * a.hq) return;
   const int b = idx / a.hq;
   const int hq = idx % a.hq;
-  const int u0 = a.unit_start[b];
   const int nu = units_of(a, b);
   const int64_t stride = (int64_t)a.hkv * G;
-  const int64_t p0 = ((int64_t)u0 * a.hkv + hq / G) * G + hq % G;
-  float M = -INFINITY;
-  for (int s = lane; s < nu; s += 64) M = fmaxf(M, a.part_ml[(p0 + s * stride) * 2]);
+  const int64_t p0 = ((int64_t)b * a.nsplit * a.hkv + hq / G) * G + hq % G;
+  // The first 64 splits' (m, l) load with the row bounds (lane s holds split s); further ones
+  // (rows of more than 64 splits) after them.
+  const bool have0 = lane < a.nsplit;
+  const int64_t q0 = p0 + (int64_t)(have0 ? lane : 0) * stride;
+  const float m0 = a.part_ml[q0 * 2], l0 = a.part_ml[q0 * 2 + 1];
+  float M = lane < nu ? m0 : -INFINITY;
+  for (int s = lane + 64; s < nu; s += 64) M = fmaxf(M, a.part_ml[(p0 + s * stride) * 2]);
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
   const float Mr = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  for (int s = lane; s < nu; s += 64) {
+  float L = lane < nu ? l0 * fast_exp2(m0 - Mr) : 0.f;
+  for (int s = lane + 64; s < nu; s += 64) {
     const int64_t pidx = p0 + s * stride;
     L = fmaf(a.part_ml[pidx * 2 + 1], fast_exp2(a.part_ml[pidx * 2] - Mr), L);
   }
@@ -1115,13 +1124,12 @@ int decode_num_splits(int batch, int hkv, int max_pages) {
   return ns > ns_dump ? ns : ns_dump;
 }
 
-// Workspace of a split launch: (m, l) for every (unit, q head), then acc, then each row's
-// first unit.  At most batch * nsplit units.
+// Workspace of a split launch: (m, l) for every (row, split, q head), then acc: batch * nsplit
+// slots, of which each row uses its units_of.
 size_t decode_workspace_bytes(int batch, int hq, int nsplit, bool with_acc) {
   if (nsplit <= 1) return 0;
   const size_t per = (with_acc ? kHeadDim : 0) + 2;
-  const size_t parts = ((size_t)batch * hq * nsplit * per * sizeof(float) + 255) & ~(size_t)255;
-  return parts + (((size_t)batch * sizeof(int32_t) + 255) & ~(size_t)255);
+  return ((size_t)batch * hq * nsplit * per * sizeof(float) + 255) & ~(size_t)255;
 }
 
 // Shared validation + launch used by the attention and the scorer entry points.
@@ -1203,7 +1211,6 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;
-  a.unit_start = nullptr;
   a.kv_w = nullptr;
   a.k_new = a.v_new = nullptr;
   a.k_new_stride = a.v_new_stride = 0;
@@ -1249,11 +1256,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
       return set_error(DELTA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
     if ((uintptr_t)workspace & 255u) return set_error(DELTA_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
     float *ws = (float *)workspace;
-    const size_t per = (with_acc ? kHeadDim : 0) + 2;
     a.part_ml = ws;
     a.part_acc = ws + (size_t)batch * hq * a.nsplit * 2;
-    a.unit_start = (int32_t *)((char *)workspace +
-                               ((((size_t)batch * hq * a.nsplit * per * sizeof(float)) + 255) & ~(size_t)255));
   }
   if (mode == kScoreOnly && !lse && a.nsplit > 1)
     return set_error(DELTA_ERR_INVALID, "%s: scorer needs an lse buffer", who);

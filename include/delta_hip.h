@@ -74,7 +74,7 @@ int delta_abi_version(void);
 int delta_decode_num_splits(int batch, int num_kv_heads, int max_pages_per_row);
 
 /* Bytes of workspace delta_paged_decode needs: 0 when the shape runs unsplit,
- * else the per-unit partials and each row's first unit (no initial contents
+ * else the split partials, one slot per (row, split) (no initial contents
  * needed; calls that share a workspace must not overlap). */
 size_t delta_paged_decode_workspace_bytes(int batch, int num_qo_heads, int num_kv_heads,
                                           int max_pages_per_row);

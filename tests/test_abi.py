@@ -68,19 +68,18 @@ def test_queries_without_gpu(lib):
     assert lib.delta_decode_num_splits(1, 8, 4) == 1
     assert lib.delta_paged_decode_workspace_bytes(1024, 32, 8, 2048) == 0
     assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 128) == 0
-    # partials (m, l, acc[128]) per (row, q head, split)
-    # partials (m, l, acc) per (unit, q head) + each row's first unit (256-byte aligned)
-    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 1025) == 32 * 32 * 9 * 130 * 4 + 256
+    # partials (m, l, acc[128]) per (row, split, q head), 256-byte aligned
+    assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 1025) == 32 * 32 * 9 * 130 * 4
     # config 5 (ragged up to 2049 pages): units of at most 128 pages, 17 for the longest row
     assert lib.delta_decode_num_splits(128, 8, 2049) == 17
     assert lib.delta_page_score_workspace_bytes(32, 32) == 32 * 32 * 4
-    # the larger of: (m, l) per (unit, q head) + each row's first unit + the lse buffer (dump path),
+    # the larger of: (m, l) per (row, split, q head) + the lse buffer (dump path),
     # and the LDS scorer's per-(kv head, token) maxima [B][Hkv][max_pages*16] (config 3 fits)
     assert lib.delta_page_score_needs_dump(32, 32, 8, 513) == 0
     assert lib.delta_page_score_kv_workspace_bytes(32, 32, 8, 513) == 32 * 8 * 513 * 16 * 4
     assert lib.delta_page_score_needs_dump(8, 32, 8, 1024) == 1      # config 2: 64 (row, head) pairs
     assert lib.delta_page_score_needs_dump(32, 64, 8, 513) == 1      # G = 8: 263 KB of logits per row
-    assert lib.delta_page_score_kv_workspace_bytes(8, 32, 8, 1024) == 8 * 32 * 32 * 2 * 4 + 256 + 8 * 32 * 4
+    assert lib.delta_page_score_kv_workspace_bytes(8, 32, 8, 1024) == 8 * 32 * 32 * 2 * 4 + 8 * 32 * 4
     assert lib.delta_page_score_kv_workspace_bytes(1024, 32, 8, 2048) == 1024 * 32 * 4
 
 

@@ -128,6 +128,10 @@ __device__ __forceinline__ int ld_scalar(const int32_t *p, int64_t i) {
   typedef const __attribute__((address_space(4))) int32_t *cptr;
   return ((cptr)p)[i];
 }
+__device__ __forceinline__ float ld_scalar(const float *p, int64_t i) {
+  typedef const __attribute__((address_space(4))) float *cptr;
+  return ((cptr)p)[i];
+}
 
 // Wave-wide inclusive prefix sum of a 0/1 flag via ballot (wave64).
 __device__ __forceinline__ int wave_prefix_exclusive(bool flag, int *total) {

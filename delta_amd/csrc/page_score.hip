@@ -9,8 +9,9 @@
 // buffer (backend.py:384-389); they contribute exp(-inf) = 0 and are not read.
 //
 // Score kernel: grid (ceil(max_pages*16 / 256), batch), 256 threads, one
-// token per thread; per head a fully coalesced 1 KiB read of the dump; the
-// 16-token page sum is a DPP reduction inside each 16-lane row.
+// token per thread; per head a fully coalesced 1 KiB read of the dump, the
+// reads of up to 64 heads in flight together; the 16-token page sum is a DPP
+// reduction inside each 16-lane row.
 //
 // HBM bytes per launch (algorithmic): the dump rows up to kv_len (read once),
 // lse, page table, scores.
@@ -74,34 +75,44 @@ __global__ void __launch_bounds__(256) dump_lse_kernel(const float *dump, int64_
   }
 }
 
+// One token per thread; the max over q heads of exp2(logit log2e - lse log2e), then the 16-lane
+// page sum.  Two loads per lane bring the first NH heads' lse values (lane i: head i) and the
+// row bounds (lanes 0-2); then each pass requests the logits of NH heads as independent loads,
+// so a block waits two memory round trips for hq <= NH.  Heads past hq - 1 repeat head hq - 1,
+// which leaves the max unchanged.  Blocks wholly past the row's kv_len load no logits.
+template <int NH>
 __global__ void __launch_bounds__(kScoreThreads)
     legacy_softmax_score_kernel(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
                                 const int32_t *kv_indptr, const int32_t *last, float *scores,
                                 int64_t score_stride, int hq, int max_pages) {
-  __shared__ float s_lse2[kMaxHeads];
+  static_assert(NH == 32 || NH == 64, "lse of head h0 + i sits in lane i");
   const int b = blockIdx.y;
-  for (int h = threadIdx.x; h < hq; h += kScoreThreads) {
-    const float v = lse[(int64_t)b * hq + h];
-    s_lse2[h] = v * kLog2e;
-  }
-  __syncthreads();
-  const int n = min(row_kv_len(kv_indptr, last, b), max_pages * kPageSize);
   const int tok = blockIdx.x * kScoreThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int32_t *bsrc = lane == 0 ? kv_indptr + b : lane == 1 ? kv_indptr + b + 1 : last + b;
+  const int bw = *bsrc;
+  const float *lse_b = lse + (int64_t)b * hq;
+  float lv = lse_b[min(lane & (NH - 1), hq - 1)];
+  asm volatile("" ::"v"(bw), "v"(lv));  // both loads in flight together
+  int np = __builtin_amdgcn_readlane(bw, 1) - __builtin_amdgcn_readlane(bw, 0);
+  np = np < 0 ? 0 : np;
+  int lp = __builtin_amdgcn_readlane(bw, 2);
+  lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+  const int n = min(np > 0 ? (np - 1) * kPageSize + lp : 0, max_pages * kPageSize);
   const float *col = dump + (int64_t)b * sdb + tok;
   float best = 0.f;
-  if (tok < n) {
-    int h = 0;
-    for (; h + 4 <= hq; h += 4) {
-      const float x0 = col[(int64_t)(h + 0) * sdh];
-      const float x1 = col[(int64_t)(h + 1) * sdh];
-      const float x2 = col[(int64_t)(h + 2) * sdh];
-      const float x3 = col[(int64_t)(h + 3) * sdh];
-      best = fmaxf(best, fast_exp2(x0 * kLog2e - s_lse2[h + 0]));
-      best = fmaxf(best, fast_exp2(x1 * kLog2e - s_lse2[h + 1]));
-      best = fmaxf(best, fast_exp2(x2 * kLog2e - s_lse2[h + 2]));
-      best = fmaxf(best, fast_exp2(x3 * kLog2e - s_lse2[h + 3]));
+  if ((int)blockIdx.x * kScoreThreads < n) {
+    for (int h0 = 0; h0 < hq; h0 += NH) {
+      if (h0 > 0) lv = lse_b[min(h0 + (lane & (NH - 1)), hq - 1)];
+      if (tok < n) {
+        float x[NH];
+#pragma unroll
+        for (int i = 0; i < NH; ++i)
+          x[i] = __builtin_nontemporal_load(col + (int64_t)min(h0 + i, hq - 1) * sdh);
+#pragma unroll
+        for (int i = 0; i < NH; ++i) best = fmaxf(best, fast_exp2(x[i] * kLog2e - readlane(lv, i) * kLog2e));
+      }
     }
-    for (; h < hq; ++h) best = fmaxf(best, fast_exp2(col[(int64_t)h * sdh] * kLog2e - s_lse2[h]));
   }
   const float page_sum = row16_sum(best);
   const int page = tok >> 4;
@@ -135,8 +146,13 @@ int launch_scores(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
                   const int32_t *kv_indptr, const int32_t *last, float *scores, int64_t score_stride,
                   int batch, int hq, int max_pages, hipStream_t stream, const char *who) {
   dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
-  hipLaunchKernelGGL(legacy_softmax_score_kernel, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse,
-                     kv_indptr, last, scores, score_stride, hq, max_pages);
+  // Heads per pass: every head in one pass up to 64 (32 when that covers them).
+  if (hq <= 32)
+    hipLaunchKernelGGL(legacy_softmax_score_kernel<32>, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse,
+                       kv_indptr, last, scores, score_stride, hq, max_pages);
+  else
+    hipLaunchKernelGGL(legacy_softmax_score_kernel<64>, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse,
+                       kv_indptr, last, scores, score_stride, hq, max_pages);
   return check_launch(who);
 }
 

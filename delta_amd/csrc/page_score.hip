@@ -121,19 +121,29 @@ __global__ void __launch_bounds__(kScoreThreads)
 
 // Page scores from the LDS scorer's per-(kv head, token) maxima tm [batch][hkv][sh]: one token per
 // thread, the max over the hkv values (the max over all q heads of the token's probability),
-// then the same 16-lane page sum as legacy_softmax_score_kernel.
+// then the same 16-lane page sum as legacy_softmax_score_kernel.  One load brings the row bounds
+// (lanes 0-2); then the kMaxWaves kv heads' maxima are requested together (heads past hkv - 1
+// repeat head hkv - 1, which leaves the max unchanged).
 __global__ void __launch_bounds__(kScoreThreads)
     tokmax_score_kernel(const float *tm, int64_t sb, int64_t sh, int hkv, const int32_t *kv_indptr,
                         const int32_t *last, float *scores, int64_t score_stride, int max_pages) {
   const int b = blockIdx.y;
-  const int n = min(row_kv_len(kv_indptr, last, b), max_pages * kPageSize);
+  const int lane = threadIdx.x & 63;
+  const int32_t *bsrc = lane == 0 ? kv_indptr + b : lane == 1 ? kv_indptr + b + 1 : last + b;
+  const int bw = *bsrc;
+  asm volatile("" ::"s"(tm), "s"(sb), "s"(sh), "s"(hkv));  // the arguments arrive while the bounds load
+  int np = __builtin_amdgcn_readlane(bw, 1) - __builtin_amdgcn_readlane(bw, 0);
+  np = np < 0 ? 0 : np;
+  int lp = __builtin_amdgcn_readlane(bw, 2);
+  lp = lp < 0 ? 0 : (lp > kPageSize ? kPageSize : lp);
+  const int n = min(np > 0 ? (np - 1) * kPageSize + lp : 0, max_pages * kPageSize);
   const int tok = blockIdx.x * kScoreThreads + threadIdx.x;
   const float *col = tm + (int64_t)b * sb + tok;
   float best = 0.f;
   if (tok < n) {
     float v[kMaxWaves];
 #pragma unroll
-    for (int kh = 0; kh < kMaxWaves; ++kh) v[kh] = kh < hkv ? __builtin_nontemporal_load(col + kh * sh) : 0.f;
+    for (int kh = 0; kh < kMaxWaves; ++kh) v[kh] = __builtin_nontemporal_load(col + min(kh, hkv - 1) * sh);
 #pragma unroll
     for (int kh = 0; kh < kMaxWaves; ++kh) best = fmaxf(best, v[kh]);
   }

@@ -175,6 +175,12 @@ def gather_probe():
     lib.delta_probe_gather_floor.restype = ctypes.c_int
     lib.delta_probe_gather_floor.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                              ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.delta_probe_gather_split.restype = ctypes.c_int
+    lib.delta_probe_gather_split.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                             ctypes.c_void_p]
+    lib.delta_probe_empty.restype = ctypes.c_int
+    lib.delta_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -397,6 +403,36 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
         timed(lambda c, d, l, s, i, p: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
                                                      c.kv_last_page_len, mp, scores=s)),
         ntok_full * row_kv + B * hq * 128 * esz + sum(npages) * 4 + B * mp * 4)
+    probe = gather_probe()
+    if probe is not None and B * hkv < 256 and c.k_per_row is None:
+        # Floors under a split subset launch (fewer than 256 (row, kv head) pairs): a bare gather
+        # of the same pages on the same split grid, and that gather followed by an empty launch of
+        # the merge's shape (the second launch's fixed cost in a graph).  The split count and
+        # unit size restate the small-launch plan of paged_decode.hip's decode_plan.
+        ns = max(1, min(-(-4096 // (B * hkv * 16)), max(1, kmax // 16), 1024))
+        chunk = -(-kmax // ns)
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+        stream_ptr = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+        def gather(c, d, l, s, i, p):
+            if probe.delta_probe_gather_split(ctypes.c_void_p(c.kv_cache.data_ptr()),
+                                              ctypes.c_int64(c.kv_cache.shape[0]), ctypes.c_void_p(p.data_ptr()),
+                                              ctypes.c_void_p(i.data_ptr()), B, hkv, ns, chunk,
+                                              ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
+                raise RuntimeError("gather probe failed")
+
+        def gather_empty(*lay):
+            gather(*lay)
+            if probe.delta_probe_empty(B * hq, ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
+                raise RuntimeError("empty probe failed")
+        sel_bytes = sum(nsel) * 16 * 2 * row_kv
+        add(f"gather floor (split grid {B * ns}x{hkv})", timed(gather), sel_bytes)
+        add("gather floor + empty launch", timed(gather_empty), sel_bytes)
+
+        def empty(*lay):
+            if probe.delta_probe_empty(B * hq, ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
+                raise RuntimeError("empty probe failed")
+        add("empty launch", timed(empty), 0)
     del layers, c
     torch.cuda.empty_cache()
     return res

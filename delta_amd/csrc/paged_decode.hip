@@ -12,9 +12,10 @@
 //   blocks in proportion to their pages (blocks past the last unit exit at once).  Wave w
 //   works on kv head w % Hkv and takes every R-th page of the unit, so the Hkv waves of one
 //   page slot read all heads of the same page (its K and V are each one contiguous
-//   16 * Hkv * 256-byte run).  Head-major (hb = 1), grid = (Hkv, batch): the 16 waves of a
-//   (row, kv head) block take its pages round robin, with no split.  The choice per shape
-//   is decode_plan's.
+//   16 * Hkv * 256-byte run).  Head-major (hb = 1), grid = (Hkv, batch): the waves of a
+//   (row, kv head) block take its pages round robin, with no split; small batches split
+//   head-major blocks too, grid = (batch * num_splits, Hkv), block x = unit (row x / num_splits,
+//   split x % num_splits), no packing.  The choice per shape is decode_plan's.
 //   Per page and wave (details at decode_split_body): q.K and P.V on MFMA, online
 //   softmax in the log2 domain; page ids preloaded 64 per register, the next page's
 //   K and V always in flight.
@@ -58,6 +59,7 @@ struct DecodeArgs {
   int batch, hq, hkv, nsplit;
   int chunk;        // pages per work unit (split launches)
   int hb;           // kv heads per block (hkv: page-major, 1: head-major)
+  int direct;       // split launch whose block x is unit (row x / nsplit, split x % nsplit)
   float sm_scale;
   // Decode steps with the new token's RoPE and KV append fused in (the *_append entry
   // points): q is the un-rotated query, row b's new token (k_new, v_new rows b) sits at
@@ -268,8 +270,19 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
   const int unit = blockIdx.x;
   if (a.nsplit > 1) {
     int nu;
-    if (!find_unit(a, unit, lane, &b, &split, &nu)) return;  // past the last unit: whole block
-    ri = row_info(a, b);
+    if (a.direct) {
+      // Every row owns nsplit block slots: the row is known from the block index, so its bounds,
+      // q and page ids load with no scan before them; slots past the row's units exit.
+      b = uniform(unit / a.nsplit);
+      split = uniform(unit - b * a.nsplit);
+      ri = row_info(a, b);
+      nu = (ri.np + a.chunk - 1) / a.chunk;
+      nu = nu < 1 ? 1 : (nu > a.nsplit ? a.nsplit : nu);
+      if (split >= nu) return;  // whole block
+    } else {
+      if (!find_unit(a, unit, lane, &b, &split, &nu)) return;  // past the last unit: whole block
+      ri = row_info(a, b);
+    }
     j0 = split * a.chunk;
     j1 = split == nu - 1 ? ri.np : min(ri.np, j0 + a.chunk);
   } else {
@@ -1208,6 +1221,9 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
     waves = kHeadMajorWaves;
     a.chunk = max_pages;
   }
+  // Head-major split launches (small batches: fewer than 256 (row, kv head) pairs) map blocks to
+  // units directly; page-major ones pack a ragged batch's units at the front of the grid.
+  a.direct = a.nsplit > 1 && a.hb == 1;
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;

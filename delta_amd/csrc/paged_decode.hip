@@ -27,6 +27,7 @@
 //
 // HBM bytes per launch (algorithmic): K and V of every attended token once,
 // q and o once, the page indices once (+ the fp32 logits when dumping).
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -60,6 +61,8 @@ struct DecodeArgs {
   int chunk;        // pages per work unit (split launches)
   int hb;           // kv heads per block (hkv: page-major, 1: head-major)
   int direct;       // split launch whose block x is unit (row x / nsplit, split x % nsplit)
+  int bal_w;        // unsplit head-major launch over more (row, kv head) blocks than CUs: rows per
+                    // round of the balanced row order (balanced_row); 0 = block y takes row y
   float sm_scale;
   // Decode steps with the new token's RoPE and KV append fused in (the *_append entry
   // points): q is the un-rotated query, row b's new token (k_new, v_new rows b) sits at
@@ -142,6 +145,38 @@ __device__ __forceinline__ int units_of(const DecodeArgs &a, int b) {
   const RowInfo r = row_info(a, b);
   const int n = (r.np + a.chunk - 1) / a.chunk;
   return n < 1 ? 1 : (n > a.nsplit ? a.nsplit : n);
+}
+
+// Row of block y of an unsplit head-major launch whose (row, kv head) blocks outnumber the CUs.
+// Blocks are dealt to XCDs round robin and each XCD's blocks to its CUs in order, so the blocks
+// of rows y, y + bal_w, y + 2 bal_w, ... (bal_w = CUs / Hkv) share CUs and a CU's time is the
+// sum of its rows' pages.  Ragged rows are therefore ranked by page count (descending, ties by
+// row) and dealt in rounds of bal_w, every other round reversed, so each CU's rows sum to about
+// the same.  Config-5 shape (128 rows of 32-256 pages, Hkv = 8): 221.6 us as given, 187.0 us in
+// this order, 184.8 us with all rows equal.  Every block ranks all rows itself (B <= 512):
+// `lds` holds B + 1 ints; the block's waves leave in step, so the LDS is free afterwards.
+__device__ int balanced_row(const DecodeArgs &a, int y, int *lds) {
+  const int B = a.batch;
+  for (int r = threadIdx.x; r < B; r += blockDim.x) lds[r] = row_info(a, r).np;
+  __syncthreads();
+  const int W = a.bal_w;
+  const int rnd = y / W;
+  const int i = y - rnd * W;
+  const int n_r = B - rnd * W < W ? B - rnd * W : W;
+  const int want = rnd * W + ((rnd & 1) ? n_r - 1 - i : i);
+  for (int r = threadIdx.x; r < B; r += blockDim.x) {
+    const int cr = lds[r];
+    int rank = 0;
+    for (int u = 0; u < B; ++u) {
+      const int cu = lds[u];
+      rank += (cu > cr || (cu == cr && u < r)) ? 1 : 0;
+    }
+    if (rank == want) lds[B] = r;  // ranks are a permutation: exactly one row matches
+  }
+  __syncthreads();
+  const int b = uniform(lds[B]);
+  __syncthreads();
+  return b;
 }
 
 // Row, split and unit count of unit u (every wave of the block computes the same answer):
@@ -286,7 +321,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     j0 = split * a.chunk;
     j1 = split == nu - 1 ? ri.np : min(ri.np, j0 + a.chunk);
   } else {
-    b = blockIdx.y;
+    b = a.bal_w > 0 ? balanced_row(a, blockIdx.y, reinterpret_cast<int *>(smem)) : (int)blockIdx.y;
     ri = row_info(a, b);
     j1 = ri.np;
   }
@@ -982,32 +1017,35 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
   const size_t sm_plan = rope ? (size_t)rope_lds_offset<G, true, true>(waves) * sizeof(float) + rope_lds
                               : (merge > tiles + dumps ? merge : tiles + dumps);
   const size_t sm_score = dumps_score > (size_t)waves * G * 2 * sizeof(float) ? dumps_score : (size_t)waves * G * 2 * sizeof(float);
+  // balanced_row's row table (B + 1 ints at the start of the LDS) fits in every launch's LDS.
+  const size_t bal = a.bal_w > 0 ? (size_t)(a.batch + 1) * sizeof(int) : 0;
+  auto lds = [bal](size_t sm) { return sm > bal ? sm : bal; };
   switch (mode) {
     case kAttn:
       if (rope)
-        hipLaunchKernelGGL((paged_decode_full_kernel<DT, G, true>), grid, block, sm_attn, stream, a);
+        hipLaunchKernelGGL((paged_decode_full_kernel<DT, G, true>), grid, block, lds(sm_attn), stream, a);
       else
-        hipLaunchKernelGGL((paged_decode_full_kernel<DT, G, false>), grid, block, sm_attn, stream, a);
+        hipLaunchKernelGGL((paged_decode_full_kernel<DT, G, false>), grid, block, lds(sm_attn), stream, a);
       break;
     case kAttnSubset:
       if (rope)
-        hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G, true>), grid, block, sm_attn, stream, a);
+        hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G, true>), grid, block, lds(sm_attn), stream, a);
       else
-        hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G, false>), grid, block, sm_attn, stream, a);
+        hipLaunchKernelGGL((paged_decode_subset_kernel<DT, G, false>), grid, block, lds(sm_attn), stream, a);
       break;
     case kAttnDump:
       if (rope)
-        hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, true>), grid, block, sm_plan, stream, a);
+        hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, true>), grid, block, lds(sm_plan), stream, a);
       else
-        hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, false>), grid, block, sm_plan, stream, a);
+        hipLaunchKernelGGL((paged_decode_plan_kernel<DT, G, false>), grid, block, lds(sm_plan), stream, a);
       break;
     case kScoreTokmax:
       hipLaunchKernelGGL((page_score_tokmax_kernel<DT, G>), grid, block,
-                         (size_t)(tokmax_lds_header<G>() + a.dump_pages * G * kPageSize) * sizeof(float), stream, a);
+                         lds((size_t)(tokmax_lds_header<G>() + a.dump_pages * G * kPageSize) * sizeof(float)), stream, a);
       break;
     case kAttnTokmax: {
-      const size_t sm = (size_t)(tokmax_lds_header<G>() + tokmax_logit_floats<G, true>(a.dump_pages)) * sizeof(float) +
-                        (rope ? rope_lds : 0);
+      const size_t sm = lds((size_t)(tokmax_lds_header<G>() + tokmax_logit_floats<G, true>(a.dump_pages)) *
+                                sizeof(float) + (rope ? rope_lds : 0));
       if (rope)
         hipLaunchKernelGGL((paged_decode_plan_tokmax_kernel<DT, G, true>), grid, block, sm, stream, a);
       else
@@ -1015,7 +1053,7 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
       break;
     }
     default:
-      hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, sm_score, stream, a);
+      hipLaunchKernelGGL((page_score_kv_kernel<DT, G>), grid, block, lds(sm_score), stream, a);
       break;
   }
 }
@@ -1071,6 +1109,20 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   Work units hold at most kMaxChunk pages (128 per wave at Hkv = 8), so a ragged batch is cut
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
+constexpr int kBalanceMaxRows = 512;  // balanced_row ranks every row in each block
+
+// Compute units of the current device (256 on MI355X), cached per device.
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
 constexpr int64_t kHeadMajorPageHeads = 262144;
 constexpr int kMaxChunk = 128;
 
@@ -1224,6 +1276,11 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   // Head-major split launches (small batches: fewer than 256 (row, kv head) pairs) map blocks to
   // units directly; page-major ones pack a ragged batch's units at the front of the grid.
   a.direct = a.nsplit > 1 && a.hb == 1;
+  // Unsplit head-major launches with more blocks than CUs deal ragged rows to CUs evenly.
+  const int cus = device_cus();
+  a.bal_w = (a.nsplit == 1 && a.hb == 1 && (int64_t)batch * hkv > cus && batch <= kBalanceMaxRows)
+                ? (cus / hkv > 0 ? cus / hkv : 1)
+                : 0;
   a.sm_scale = sm_scale;
   a.part_acc = nullptr;
   a.part_ml = nullptr;

@@ -287,6 +287,61 @@ def test_ragged_work_units(plan_pages):
     assert torch.all(d[:, :, written:] == 12345.0)
 
 
+@pytest.mark.parametrize("batch,hq,hkv,trailing,maxp", [
+    (40, 40, 8, False, 30),   # 320 blocks: rounds of 32 rows, the second one partial and reversed
+    (96, 8, 4, True, 30),     # rounds of 64 rows, trailing empty pages
+    (300, 2, 1, False, 30),   # rounds of 256 rows, a partial reversed round of 44
+    (500, 1, 1, False, 1),    # one-page rows: the row table is larger than the scorers' own LDS
+])
+def test_balanced_row_order(batch, hq, hkv, trailing, maxp):
+    """Unsplit head-major launches whose (row, kv head) blocks outnumber the CUs (B * Hkv > 256
+    on MI355X) take their rows in a balanced order: rows ranked by page count (ties by row) and
+    dealt in rounds of CUs / Hkv, every other round reversed.  Every row must still be attended
+    exactly once, so every row's output, lse, dump and page scores are checked against the
+    oracle: the attention launch with and without the dump, the subset launch over the same
+    pages, the planner and the K-only scorer with their logits on chip.  Many rows share a page
+    count (ties in the ranking)."""
+    gen = torch.Generator().manual_seed(61)
+    if maxp > 1:
+        lens = (torch.randint(1, maxp, (batch,), generator=gen) * 16 + torch.randint(0, 16, (batch,), generator=gen))
+    else:
+        lens = torch.randint(1, 17, (batch,), generator=gen)
+    lens = lens.tolist()
+    lens[0] = 1
+    c = make_case(batch=batch, hq=hq, hkv=hkv, kv_lens=lens, seed=62, page_order="randperm", k=4, L=2,
+                  trailing_empty_page=trailing)
+    g = gpu(c)
+    B, mp = batch, c.max_pages
+    dump = torch.full((B, hq, mp * 16), 12345.0, device=DEV)
+    lse = torch.empty(B, hq, device=DEV)
+    o = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                       lse=lse, logits_dump=dump)
+    o_nd = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp)
+    o_sub = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                           subset=True)
+    o_chip, s_chip = K.paged_decode_scores(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len,
+                                           max_pages_per_row=mp)
+    s_k = K.page_score(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, mp)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = O.paged_decode_attention(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                                              c.sm_scale)
+    for b in range(B):
+        for what, got in (("dump launch", o), ("no dump", o_nd), ("subset", o_sub), ("planner on chip", o_chip)):
+            assert_attn_close(got[b], o_ref[b], f"{what}, row {b}")
+    assert torch.equal(o_nd, o_sub)
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
+    x_ref = O.dump_logits(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, c.sm_scale, mp * 16)
+    valid = torch.isfinite(x_ref)
+    d = dump.cpu()
+    assert ((d[valid] - x_ref[valid]).abs() / (1 + x_ref[valid].abs())).max().item() < 1e-4
+    ref = O.legacy_softmax_page_scores(x_ref, B, mp, compute_dtype=torch.float64).double()
+    for what, s in (("planner on chip", s_chip), ("K-only scorer", s_k)):
+        s = s.cpu().double()
+        rel = (s - ref).abs() / ref.abs().clamp_min(1e-30)
+        rel[ref == 0] = s[ref == 0].abs()
+        assert rel.max().item() < 1e-4, f"{what}: rel err {rel.max().item()}"
+
+
 def test_sparse_equals_full_when_budget_covers_all():
     c = config_case(3, scale=0.25, batch=4)
     g = gpu(c)

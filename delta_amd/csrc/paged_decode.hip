@@ -153,11 +153,25 @@ __device__ __forceinline__ int units_of(const DecodeArgs &a, int b) {
 // sum of its rows' pages.  Ragged rows are therefore ranked by page count (descending, ties by
 // row) and dealt in rounds of bal_w, every other round reversed, so each CU's rows sum to about
 // the same.  Config-5 shape (128 rows of 32-256 pages, Hkv = 8): 221.6 us as given, 187.0 us in
-// this order, 184.8 us with all rows equal.  Every block ranks all rows itself (B <= 512):
-// `lds` holds B + 1 ints; the block's waves leave in step, so the LDS is free afterwards.
-__device__ int balanced_row(const DecodeArgs &a, int y, int *lds) {
+// this order, 184.8 us with all rows equal.  Every block ranks all rows itself (B <= 512) on one
+// key per row, (pages << 9) | (511 - row), and keeps every row's bounds in LDS, so the chosen
+// row's come from there.  `lds` holds 5 B + 1 ints; the block's waves leave in step, so the LDS
+// is free afterwards.  Returns the row; *ri gets its bounds.
+__device__ int balanced_row(const DecodeArgs &a, int y, int *lds, RowInfo *ri) {
   const int B = a.batch;
-  for (int r = threadIdx.x; r < B; r += blockDim.x) lds[r] = row_info(a, r).np;
+  int64_t *p0 = reinterpret_cast<int64_t *>(lds);  // [B] (the dynamic LDS starts 16-byte aligned)
+  int *key = lds + 2 * B;                          // [B]
+  int *np = lds + 3 * B;                           // [B]
+  int *last = lds + 4 * B;                         // [B]
+  int *win = lds + 5 * B;
+  for (int r = threadIdx.x; r < B; r += blockDim.x) {
+    const RowInfo x = row_info(a, r);
+    // Distinct keys (the row in the low bits); page counts past 2^21 - 1 rank as equal.
+    key[r] = ((x.np < (1 << 21) ? x.np : (1 << 21) - 1) << 9) | (511 - r);
+    np[r] = x.np;
+    last[r] = x.last;
+    p0[r] = x.p0;
+  }
   __syncthreads();
   const int W = a.bal_w;
   const int rnd = y / W;
@@ -165,16 +179,19 @@ __device__ int balanced_row(const DecodeArgs &a, int y, int *lds) {
   const int n_r = B - rnd * W < W ? B - rnd * W : W;
   const int want = rnd * W + ((rnd & 1) ? n_r - 1 - i : i);
   for (int r = threadIdx.x; r < B; r += blockDim.x) {
-    const int cr = lds[r];
+    const int kr = key[r];
     int rank = 0;
-    for (int u = 0; u < B; ++u) {
-      const int cu = lds[u];
-      rank += (cu > cr || (cu == cr && u < r)) ? 1 : 0;
-    }
-    if (rank == want) lds[B] = r;  // ranks are a permutation: exactly one row matches
+    for (int u = 0; u < B; ++u) rank += key[u] > kr ? 1 : 0;
+    if (rank == want) *win = r;  // the keys are distinct: exactly one row matches
   }
   __syncthreads();
-  const int b = uniform(lds[B]);
+  const int b = uniform(*win);
+  RowInfo x;
+  x.p0 = p0[b];
+  x.np = np[b];
+  x.last = last[b];
+  x.kv_len = x.np > 0 ? (x.np - 1) * kPageSize + x.last : 0;
+  *ri = x;
   __syncthreads();
   return b;
 }
@@ -321,8 +338,12 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     j0 = split * a.chunk;
     j1 = split == nu - 1 ? ri.np : min(ri.np, j0 + a.chunk);
   } else {
-    b = a.bal_w > 0 ? balanced_row(a, blockIdx.y, reinterpret_cast<int *>(smem)) : (int)blockIdx.y;
-    ri = row_info(a, b);
+    if (a.bal_w > 0) {
+      b = balanced_row(a, blockIdx.y, reinterpret_cast<int *>(smem), &ri);
+    } else {
+      b = blockIdx.y;
+      ri = row_info(a, b);
+    }
     j1 = ri.np;
   }
   // A split launch's partial slot (row, split), and whether this is the row's first split;
@@ -1017,8 +1038,8 @@ void launch_split(const DecodeArgs &a, int waves, int mode, hipStream_t stream) 
   const size_t sm_plan = rope ? (size_t)rope_lds_offset<G, true, true>(waves) * sizeof(float) + rope_lds
                               : (merge > tiles + dumps ? merge : tiles + dumps);
   const size_t sm_score = dumps_score > (size_t)waves * G * 2 * sizeof(float) ? dumps_score : (size_t)waves * G * 2 * sizeof(float);
-  // balanced_row's row table (B + 1 ints at the start of the LDS) fits in every launch's LDS.
-  const size_t bal = a.bal_w > 0 ? (size_t)(a.batch + 1) * sizeof(int) : 0;
+  // balanced_row's row tables (5 B + 1 ints at the start of the LDS) fit in every launch's LDS.
+  const size_t bal = a.bal_w > 0 ? (size_t)(5 * a.batch + 1) * sizeof(int) : 0;
   auto lds = [bal](size_t sm) { return sm > bal ? sm : bal; };
   switch (mode) {
     case kAttn:
@@ -1110,6 +1131,7 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //   into many equal units instead of one share per row sized by its longest row.
 constexpr int kHeadMajorPairs = 256;
 constexpr int kBalanceMaxRows = 512;  // balanced_row ranks every row in each block
+constexpr int kBalanceMinPages = 32;  // shorter rows: the ranking would cost more than the balance gains
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus() {
@@ -1278,7 +1300,8 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   a.direct = a.nsplit > 1 && a.hb == 1;
   // Unsplit head-major launches with more blocks than CUs deal ragged rows to CUs evenly.
   const int cus = device_cus();
-  a.bal_w = (a.nsplit == 1 && a.hb == 1 && (int64_t)batch * hkv > cus && batch <= kBalanceMaxRows)
+  a.bal_w = (a.nsplit == 1 && a.hb == 1 && (int64_t)batch * hkv > cus && batch <= kBalanceMaxRows &&
+             max_pages >= kBalanceMinPages)
                 ? (cus / hkv > 0 ? cus / hkv : 1)
                 : 0;
   a.sm_scale = sm_scale;

@@ -287,27 +287,26 @@ def test_ragged_work_units(plan_pages):
     assert torch.all(d[:, :, written:] == 12345.0)
 
 
-@pytest.mark.parametrize("batch,hq,hkv,trailing,maxp", [
-    (40, 40, 8, False, 30),   # 320 blocks: rounds of 32 rows, the second one partial and reversed
-    (96, 8, 4, True, 30),     # rounds of 64 rows, trailing empty pages
-    (300, 2, 1, False, 30),   # rounds of 256 rows, a partial reversed round of 44
-    (500, 1, 1, False, 1),    # one-page rows: the row table is larger than the scorers' own LDS
+@pytest.mark.parametrize("batch,hq,hkv,trailing,lo,hi", [
+    (40, 40, 8, False, 1, 60),    # 320 blocks: rounds of 32 rows, the second one partial and reversed
+    (96, 8, 4, True, 1, 60),      # rounds of 64 rows, trailing empty pages
+    (300, 2, 1, False, 1, 60),    # rounds of 256 rows, a partial reversed round of 44
+    (500, 1, 1, False, 32, 33),   # two page counts (ties everywhere); the row tables outgrow the
+                                  # scorers' own LDS
 ])
-def test_balanced_row_order(batch, hq, hkv, trailing, maxp):
+def test_balanced_row_order(batch, hq, hkv, trailing, lo, hi):
     """Unsplit head-major launches whose (row, kv head) blocks outnumber the CUs (B * Hkv > 256
-    on MI355X) take their rows in a balanced order: rows ranked by page count (ties by row) and
-    dealt in rounds of CUs / Hkv, every other round reversed.  Every row must still be attended
-    exactly once, so every row's output, lse, dump and page scores are checked against the
-    oracle: the attention launch with and without the dump, the subset launch over the same
-    pages, the planner and the K-only scorer with their logits on chip.  Many rows share a page
-    count (ties in the ranking)."""
+    on MI355X) and whose rows reach 32 pages take their rows in a balanced order: rows ranked by
+    page count (ties by row) and dealt in rounds of CUs / Hkv, every other round reversed, each
+    block reading its row's bounds from the ranking's LDS tables.  Every row must still be
+    attended exactly once, so every row's output, lse, dump and page scores are checked against
+    the oracle: the attention launch with and without the dump, the subset launch over the same
+    pages, the planner and the K-only scorer with their logits on chip."""
     gen = torch.Generator().manual_seed(61)
-    if maxp > 1:
-        lens = (torch.randint(1, maxp, (batch,), generator=gen) * 16 + torch.randint(0, 16, (batch,), generator=gen))
-    else:
-        lens = torch.randint(1, 17, (batch,), generator=gen)
-    lens = lens.tolist()
-    lens[0] = 1
+    lens = (torch.randint(lo - 1, hi, (batch,), generator=gen) * 16
+            + torch.randint(1, 17, (batch,), generator=gen)).tolist()
+    lens[0] = 1 if lo == 1 else lens[0]
+    lens[1] = hi * 16  # the longest row: max_pages >= 32
     c = make_case(batch=batch, hq=hq, hkv=hkv, kv_lens=lens, seed=62, page_order="randperm", k=4, L=2,
                   trailing_empty_page=trailing)
     g = gpu(c)

@@ -196,13 +196,17 @@ __device__ int balanced_row(const DecodeArgs &a, int y, int *lds, RowInfo *ri) {
   return b;
 }
 
-// Row, split and unit count of unit u (every wave of the block computes the same answer):
-// a running inclusive scan of units_of over 64 rows at a time.  False past the last unit.
+// Row, split and unit count of unit u (every wave of the block computes the same answer).
+// Units run in two groups: first every row's full units (all but its last, `chunk` pages each),
+// numbered row by row, then each row's last unit (at most `chunk` pages unless the row outgrew
+// the plan), row b at F + b, F = the number of full units.  Blocks start in grid order, so the
+// short last units of a ragged batch fill the launch's tail instead of whole units of the last
+// rows.  A running inclusive scan over 64 rows at a time; false past the last unit.
 __device__ __forceinline__ bool find_unit(const DecodeArgs &a, int u, int lane, int *row, int *split, int *nu) {
   int base = 0;
   for (int r0 = 0; r0 < a.batch; r0 += 64) {
     const int r = r0 + lane;
-    const int n = r < a.batch ? units_of(a, r) : 0;
+    const int n = r < a.batch ? units_of(a, r) - 1 : 0;  // full units of row r
     int incl = n;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -216,12 +220,17 @@ __device__ __forceinline__ bool find_unit(const DecodeArgs &a, int u, int lane, 
       const int start = base + __shfl(incl - n, l, 64);
       *row = r0 + l;
       *split = u - start;
-      *nu = __shfl(n, l, 64);
+      *nu = __shfl(n, l, 64) + 1;
       return true;
     }
     base += total;
   }
-  return false;
+  const int b = u - base;  // the last units, one per row
+  if (b >= a.batch) return false;
+  *row = b;
+  *nu = units_of(a, b);
+  *split = *nu - 1;
+  return true;
 }
 
 // Pages of logits a wave stages in LDS before writing them out.  Interleaving the dump's HBM

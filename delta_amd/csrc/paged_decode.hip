@@ -39,6 +39,13 @@ namespace {
 
 constexpr int kMaxWaves = 16;  // waves per block (a block never exceeds one CU's 16 slots at <= 128 VGPRs)
 constexpr int kHeadMajorWaves = 4;  // waves per block of an unsplit head-major launch (decode_plan)
+constexpr int kMergeGroups = 4;     // 128-thread groups of a merge block (16 splits each per round)
+
+// Groups of a merge block for `nsplit` splits: one per 16 splits, at most kMergeGroups.
+inline int merge_groups(int nsplit) {
+  const int n = (nsplit + 15) / 16;
+  return n < 1 ? 1 : (n > kMergeGroups ? kMergeGroups : n);
+}
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -816,6 +823,29 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
     return;
   }
 
+  // One-wave blocks of a split attention launch (small batches) store their partial straight
+  // from registers: lane (c, t) holds O[g = 4c + r][d = 16 n + t] in acc[n][r], lanes c = 0, t < G
+  // hold (m, l) of head t.  No block merge, no barrier.
+  if constexpr (WITH_V && !WITH_DUMP && !TOKMAX) {
+    if (nw == 1 && a.nsplit > 1) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int g = 4 * c + r;
+        if (g < G) {
+          const int64_t pidx = ((int64_t)pslot * a.hkv + h) * G + g;
+#pragma unroll
+          for (int n = 0; n < 8; ++n) a.part_acc[pidx * kHeadDim + 16 * n + t] = acc[n][r];
+        }
+      }
+      if (c == 0 && t < G) {
+        const int64_t pidx = ((int64_t)pslot * a.hkv + h) * G + t;
+        a.part_ml[pidx * 2 + 0] = m;
+        a.part_ml[pidx * 2 + 1] = l;
+      }
+      return;
+    }
+  }
+
   // Merge the block's waves in LDS.  Attention launches have a merge area of their own past
   // the V tiles, so each wave stores its (m, l, acc) as soon as it leaves the loop; the dump
   // launches reuse the V tiles' space once every wave left it.
@@ -944,25 +974,30 @@ __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_plan_tokmax_kerne
   decode_split_body<DT, G, true, false, ROPE, true>(a, smem);
 }
 
-// Combines the split partials of one (row, q head): thread d of the block computes
+// Combines the split partials of one (row, q head): thread d of a 128-thread group computes
 //   M = max_s m_s,  o[d] = sum_s A_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M),
 //   lse = (M + log2 sum_s l_s 2^(m_s - M)) ln 2
-// over the row's units_of splits.  Partials sit at (row, split), so the first 16 splits' loads
-// issue with the row bounds, not after them (splits the row does not have weigh nothing).
+// over the row's units_of splits.  A block holds ngrp = merge_groups(nsplit) groups (up to 4):
+// group q merges the batches of 16 splits that start at 16 q, 16 (q + ngrp), ..., and the
+// groups' sums then combine through LDS, so up to 64 splits cost one round of loads.  Partials
+// sit at (row, split), so each group's first batch issues its loads with the row bounds, not
+// after them (splits the row does not have weigh nothing).
 template <int DT>
-__global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
+__global__ void __launch_bounds__(kMergeGroups * kHeadDim) decode_merge_kernel(DecodeArgs a, int G) {
   using E = Elem<DT>;
+  __shared__ float s_m[kMergeGroups], s_l[kMergeGroups], s_a[kMergeGroups][kHeadDim];
   const int b = blockIdx.x / a.hq;
   const int hq = blockIdx.x % a.hq;
   const int h = hq / G, g = hq % G;
-  const int dd = threadIdx.x;
+  const int dd = threadIdx.x % kHeadDim;
+  const int grp = threadIdx.x / kHeadDim;
+  const int ngrp = blockDim.x / kHeadDim;
   const int nu = units_of(a, b);
   const int64_t stride = (int64_t)a.hkv * G;  // partial rows per split
   const int64_t p0 = ((int64_t)b * a.nsplit * a.hkv + h) * G + g;
-  // Splits in batches of 16 whose loads all issue together (weight 0 past the row's last
-  // split; the first batch reads min(16, nsplit) slots regardless of the row's count); the
-  // running sums move to a new maximum between batches.  One batch (<= 16 splits) is exactly
-  // the two-pass merge.
+  // Batches of 16 splits whose loads all issue together (weight 0 past the row's last split;
+  // a group's first batch reads min(16, nsplit - 16 q) slots regardless of the row's count); the
+  // running sums move to a new maximum between batches.
   float M = -INFINITY, L = 0.f, A = 0.f;
   auto merge16 = [&](int s0, int lim) {
     float mv[16], lv[16], av[16];
@@ -978,11 +1013,9 @@ __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, in
     for (int i = 0; i < 16; ++i)
       if (s0 + i < nu) cm = fmaxf(cm, mv[i]);
     const float cmr = cm == -INFINITY ? 0.f : cm;
-    if (s0 > 0) {
-      const float al = fast_exp2(M - cmr);
-      L *= al;
-      A *= al;
-    }
+    const float al = fast_exp2(M - cmr);  // 0 while nothing is merged (M = -inf)
+    L *= al;
+    A *= al;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if (s0 + i < nu) {
@@ -993,8 +1026,29 @@ __global__ void __launch_bounds__(kHeadDim) decode_merge_kernel(DecodeArgs a, in
     }
     M = cm;
   };
-  merge16(0, a.nsplit < 16 ? a.nsplit : 16);  // every row has at least one split
-  for (int s0 = 16; s0 < nu; s0 += 16) merge16(s0, nu - s0);
+  const int first = 16 * grp;  // < nsplit: merge_groups gives no group past the last split
+  merge16(first, a.nsplit - first < 16 ? a.nsplit - first : 16);
+  for (int s0 = first + 16 * ngrp; s0 < nu; s0 += 16 * ngrp) merge16(s0, nu - s0);
+  if (ngrp > 1) {
+    if (dd == 0) {
+      s_m[grp] = M;
+      s_l[grp] = L;
+    }
+    s_a[grp][dd] = A;
+    __syncthreads();
+    if (grp != 0) return;
+    float MM = -INFINITY;
+    for (int q = 0; q < ngrp; ++q) MM = fmaxf(MM, s_m[q]);
+    const float Mr = MM == -INFINITY ? 0.f : MM;
+    L = 0.f;
+    A = 0.f;
+    for (int q = 0; q < ngrp; ++q) {
+      const float sc = fast_exp2(s_m[q] - Mr);
+      L = fmaf(s_l[q], sc, L);
+      A = fmaf(s_a[q][dd], sc, A);
+    }
+    M = MM;
+  }
   a.o[(int64_t)b * a.o_stride_b + (int64_t)hq * a.o_stride_h + dd] = (uint16_t)E::from_float(L > 0.f ? A / L : 0.f);
   if (dd == 0 && a.lse != nullptr) a.lse[(int64_t)b * a.hq + hq] = L > 0.f ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
@@ -1186,11 +1240,22 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     ch = kMaxChunk;
     ns = ceil_div(max_pages, ch);
   }
-  // Small launches: 4-wave blocks while a wave's share of a unit stays at <= 8 pages (the
-  // config 2 and 4 subset launches), else 16 (the config-4 full attention, 128-page units:
-  // with 4 waves its full-cache engine step ran 5.4-5.6 -> 5.9-6.0 ms, though a launch timed
-  // alone was unchanged).
-  if (small && ceil_div(ch, (int64_t)kHeadMajorWaves) <= 8) R = kHeadMajorWaves;
+  // Small launches whose units give each of 4 waves at most 8 pages (the config 2 and 4 subset
+  // launches) run 4-wave blocks; when 4x their split count still fits one 16-split merge batch
+  // (config 2: 4 -> 16 splits) they run one-wave blocks with 4x the splits instead, each wave
+  // storing its partial from registers with no closing block merge (config-2 subset 17.4 -> 16.6
+  // us; at config 4, 16 -> 64 splits, the merge's 4x partials cost more than the block merge
+  // saves: 13.6 -> 14.2 us).  Others keep 16 waves (the config-4 full attention, 128-page units:
+  // with 4 waves its full-cache engine step ran 5.4-5.6 -> 5.9-6.0 ms, though a launch timed alone
+  // was unchanged).
+  if (small && ceil_div(ch, (int64_t)kHeadMajorWaves) <= 8) {
+    R = kHeadMajorWaves;
+    if (ns * kHeadMajorWaves <= 16 && ns * kHeadMajorWaves <= max_pages) {
+      ns *= kHeadMajorWaves;
+      ch = ceil_div(max_pages, ns);
+      R = 1;
+    }
+  }
   *nsplit = (int)ns;
   *waves = h * R;
   *hb = h;
@@ -1375,9 +1440,11 @@ int run_decode(const void *q, int64_t q_stride_b, int64_t q_stride_h, const void
   if (rc || a.nsplit == 1) return rc;
   if (with_acc) {
     if (dtype == DELTA_BF16)
-      hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
+      hipLaunchKernelGGL(decode_merge_kernel<DELTA_BF16>, dim3(batch * hq), dim3(kHeadDim * merge_groups(a.nsplit)), 0,
+                         stream, a, G);
     else
-      hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hq), dim3(kHeadDim), 0, stream, a, G);
+      hipLaunchKernelGGL(decode_merge_kernel<DELTA_FP16>, dim3(batch * hq), dim3(kHeadDim * merge_groups(a.nsplit)), 0,
+                         stream, a, G);
   } else {
     const int n = batch * hq;
     hipLaunchKernelGGL(decode_merge_lse_kernel, dim3((n + 3) / 4), dim3(256), 0, stream, a, G);

@@ -171,6 +171,7 @@ __device__ int balanced_row(const DecodeArgs &a, int y, int *lds, RowInfo *ri) {
   int *np = lds + 3 * B;                           // [B]
   int *last = lds + 4 * B;                         // [B]
   int *win = lds + 5 * B;
+  if (threadIdx.x == 0) *win = y;  // replaced by the ranking below (kept in range regardless)
   for (int r = threadIdx.x; r < B; r += blockDim.x) {
     const RowInfo x = row_info(a, r);
     // Distinct keys (the row in the low bits); page counts past 2^21 - 1 rank as equal.
@@ -192,7 +193,8 @@ __device__ int balanced_row(const DecodeArgs &a, int y, int *lds, RowInfo *ri) {
     if (rank == want) *win = r;  // the keys are distinct: exactly one row matches
   }
   __syncthreads();
-  const int b = uniform(*win);
+  int b = uniform(*win);
+  b = b < 0 ? 0 : (b >= B ? B - 1 : b);
   RowInfo x;
   x.p0 = p0[b];
   x.np = np[b];

@@ -9,7 +9,8 @@
 //   ascending j (132-134) as physical ids from the row's block table (147-150).
 //
 // Algorithm per row (one block of 256 or 1024 threads): fp32 keys map to order-preserving uint32
-// (+0/-0 folded); a 4-pass 8-bit radix select finds the k-th largest key T and
+// (+0/-0 folded); an 8-bit radix select (up to 4 passes; it stops once every key of the k-th
+// key's bin is taken) finds the k-th largest key T and
 // how many keys equal to T are taken (r); one ordered pass then marks
 // key > T, or key == T among the first r such pages, and compacts the marked
 // pages in ascending j with ballot prefix sums -- the output is sorted by
@@ -225,7 +226,11 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
     prefix |= (uint32_t)s_digit << shift;
     pmask |= 0xFFu << shift;
     remaining = s_remaining;
+    const bool bin_taken = remaining == s_eq;
     __syncthreads();
+    // Every key of the k-th key's bin is taken: the selection is exactly the keys whose digits so
+    // far are >= the prefix, i.e. key >= T with T = prefix (lower bits zero) -- no further pass.
+    if (bin_taken) break;
   }
   const uint32_t T = prefix;
   const int take_eq = remaining;  // how many keys == T are selected (smallest j first)

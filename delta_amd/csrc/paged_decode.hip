@@ -1243,8 +1243,9 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
     ns = ceil_div(max_pages, ch);
   }
   // Small launches whose units give each of 4 waves at most 8 pages (the config 2 and 4 subset
-  // launches) run 4-wave blocks; when 4x their split count still fits one 16-split merge batch
-  // (config 2: 4 -> 16 splits) they run one-wave blocks with 4x the splits instead, each wave
+  // launches) run 4-wave blocks; when they split and 4x their split count still fits one 16-split
+  // merge batch (config 2: 4 -> 16 splits) they run one-wave blocks with 4x the splits instead
+  // (an unsplit launch keeps its blocks: no merge launch), each wave
   // storing its partial from registers with no closing block merge (config-2 subset 17.4 -> 16.6
   // us; at config 4, 16 -> 64 splits, the merge's 4x partials cost more than the block merge
   // saves: 13.6 -> 14.2 us).  Others keep 16 waves (the config-4 full attention, 128-page units:
@@ -1252,7 +1253,7 @@ void decode_plan(int batch, int hkv, int max_pages, bool dump, int *nsplit, int 
   // was unchanged).
   if (small && ceil_div(ch, (int64_t)kHeadMajorWaves) <= 8) {
     R = kHeadMajorWaves;
-    if (ns * kHeadMajorWaves <= 16 && ns * kHeadMajorWaves <= max_pages) {
+    if (ns > 1 && ns * kHeadMajorWaves <= 16 && ns * kHeadMajorWaves <= max_pages) {
       ns *= kHeadMajorWaves;
       ch = ceil_div(max_pages, ns);
       R = 1;

@@ -65,7 +65,7 @@ def test_queries_without_gpu(lib):
     assert lib.delta_decode_num_splits(8, 8, 128) == 32        # config 2
     assert lib.delta_decode_num_splits(4, 4, 4096) == 64       # config 4: R = 4
     assert lib.delta_decode_num_splits(4, 4, 256) == 32        # >= 2 pages per wave
-    assert lib.delta_decode_num_splits(1, 8, 4) == 1
+    assert lib.delta_decode_num_splits(1, 8, 4) == 1           # unsplit: no one-wave conversion
     assert lib.delta_paged_decode_workspace_bytes(1024, 32, 8, 2048) == 0
     assert lib.delta_paged_decode_workspace_bytes(32, 32, 8, 128) == 0
     # partials (m, l, acc[128]) per (row, split, q head), 256-byte aligned

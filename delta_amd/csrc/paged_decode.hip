@@ -1180,8 +1180,9 @@ void launch_split_g(const DecodeArgs &a, int G, int waves, int mode, hipStream_t
 //     no merge launch (config-3 full attention 170.6 -> 159.6 us against page-major units
 //     and their merge).  Past that size, where a ragged batch's longest rows would leave
 //     most blocks idle at the end, page-major work units balance better (config 5 full
-//     attention 1545 us page-major, 1739 us head-major).  These blocks hold 4 waves (one per SIMD):
-//     32 KiB of pages in flight per CU already stream at full rate (a bare gather of the
+//     attention 1545 us page-major, 1739 us head-major; 1508 us with the full units
+//     first).  These blocks hold 4 waves (one per SIMD): 32 KiB of pages in flight per CU
+//     already stream at full rate (a bare gather of the
 //     config-3 subset pages: 41.4 us with 4 waves of one page each, 42.0 with 8, 42.2 with
 //     16), while the block's closing merge of its waves' partials and the fused RoPE
 //     prologue, which every wave repeats, shrink with the wave count (subset launch 44.8 ->

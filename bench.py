@@ -177,8 +177,8 @@ def gather_probe():
                                              ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.delta_probe_gather_split.restype = ctypes.c_int
     lib.delta_probe_gather_split.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
-                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                             ctypes.c_void_p]
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_void_p, ctypes.c_void_p]
     lib.delta_probe_empty.restype = ctypes.c_int
     lib.delta_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
@@ -410,6 +410,9 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
         # the merge's shape (the second launch's fixed cost in a graph).  The split count and
         # unit size restate the small-launch plan of paged_decode.hip's decode_plan.
         ns = max(1, min(-(-4096 // (B * hkv * 16)), max(1, kmax // 16), 1024))
+        waves = 4
+        if ns > 1 and ns * 4 <= 16 and ns * 4 <= kmax:  # the one-wave plan (4x the splits)
+            ns, waves = ns * 4, 1
         chunk = -(-kmax // ns)
         sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
         stream_ptr = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -417,7 +420,7 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
         def gather(c, d, l, s, i, p):
             if probe.delta_probe_gather_split(ctypes.c_void_p(c.kv_cache.data_ptr()),
                                               ctypes.c_int64(c.kv_cache.shape[0]), ctypes.c_void_p(p.data_ptr()),
-                                              ctypes.c_void_p(i.data_ptr()), B, hkv, ns, chunk,
+                                              ctypes.c_void_p(i.data_ptr()), B, hkv, ns, chunk, waves,
                                               ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
                 raise RuntimeError("gather probe failed")
 
@@ -426,7 +429,7 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
             if probe.delta_probe_empty(B * hq, ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
                 raise RuntimeError("empty probe failed")
         sel_bytes = sum(nsel) * 16 * 2 * row_kv
-        add(f"gather floor (split grid {B * ns}x{hkv})", timed(gather), sel_bytes)
+        add(f"gather floor (split grid {B * ns}x{hkv}, {waves}-wave blocks)", timed(gather), sel_bytes)
         add("gather floor + empty launch", timed(gather_empty), sel_bytes)
 
         def empty(*lay):

@@ -53,21 +53,22 @@ __global__ void __launch_bounds__(kWaves * 64)
 }
 
 // The split grid of the small decode launches (fewer than 256 (row, kv head) pairs): block =
-// (work unit u = row * nsplit + split, kv head), kWaves waves taking the unit's pages
-// [split * chunk, +chunk) round robin, one page in flight ahead, as the split attention
-// launches do.  Blocks past a row's last page exit at once.
+// (work unit u = row * nsplit + split, kv head), blockDim / 64 waves (4, or 1 for the one-wave
+// plan) taking the unit's pages [split * chunk, +chunk) round robin, one page in flight ahead,
+// as the split attention launches do.  Blocks past a row's last page exit at once.
 __global__ void __launch_bounds__(kWaves * 64)
     gather_split_kernel(const uint16_t *kv, int64_t num_pages, const int32_t *indptr, const int32_t *indices,
                         int hkv, int nsplit, int chunk, uint32_t *sink) {
   const int b = blockIdx.x / nsplit, split = blockIdx.x % nsplit, h = blockIdx.y;
+  const int nw = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane >> 4, t = lane & 15;
   const int64_t row = (int64_t)hkv * kHeadDim, page = 2 * kPageSize * row;
   const int p0 = indptr[b], np = indptr[b + 1] - p0;
   const int j0 = split * chunk + wave, j1 = min(np, (split + 1) * chunk);
-  const int cnt = j1 > j0 ? (j1 - j0 + kWaves - 1) / kWaves : 0;
+  const int cnt = j1 > j0 ? (j1 - j0 + nw - 1) / nw : 0;
   int ids = 0;
-  if (lane < cnt) ids = indices[p0 + j0 + kWaves * lane];
+  if (lane < cnt) ids = indices[p0 + j0 + nw * lane];
   if (ids < 0 || (int64_t)ids >= num_pages) ids = 0;
   u32x4 r[8];
   auto issue = [&](int it) {
@@ -111,12 +112,12 @@ extern "C" __attribute__((visibility("default"))) int delta_probe_gather_floor(
 
 extern "C" __attribute__((visibility("default"))) int delta_probe_gather_split(
     const void *kv_cache, int64_t num_pages, const int32_t *kv_indptr, const int32_t *kv_indices, int batch,
-    int num_kv_heads, int nsplit, int chunk, void *sink, hipStream_t stream) {
+    int num_kv_heads, int nsplit, int chunk, int waves, void *sink, hipStream_t stream) {
   if (batch <= 0) return 0;
   if (!kv_cache || !kv_indptr || !kv_indices || !sink || num_pages <= 0 || num_kv_heads <= 0 || nsplit <= 0 ||
-      chunk <= 0 || chunk > 64 * delta::kWaves || ((uintptr_t)kv_cache & 15u))
+      chunk <= 0 || (waves != 1 && waves != delta::kWaves) || chunk > 64 * waves || ((uintptr_t)kv_cache & 15u))
     return 1;
-  hipLaunchKernelGGL(delta::gather_split_kernel, dim3(batch * nsplit, num_kv_heads), dim3(delta::kWaves * 64), 0,
+  hipLaunchKernelGGL(delta::gather_split_kernel, dim3(batch * nsplit, num_kv_heads), dim3(waves * 64), 0,
                      stream, (const uint16_t *)kv_cache, num_pages, kv_indptr, kv_indices, num_kv_heads, nsplit,
                      chunk, (uint32_t *)sink);
   return hipGetLastError() == hipSuccess ? 0 : 2;

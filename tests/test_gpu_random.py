@@ -27,11 +27,13 @@ def close_attn(got, want, what):
     assert err <= 2e-2 and cos > 0.999, f"{what}: err {err} cos {cos}"
 
 
-def draw(seed):
+def draw(seed, large=False):
     r = random.Random(seed)
     hkv = r.choice([1, 2, 4, 8])
     G = r.randint(1, 8)
-    B = r.randint(1, 40)
+    # large: more (row, kv head) blocks than CUs, so unsplit launches take the balanced row order
+    lo = -(-257 // hkv)
+    B = r.randint(lo, max(200, lo + 40)) if large else r.randint(1, 40)
     lens = []
     for _ in range(B):
         n = r.randint(1, 1200)
@@ -45,7 +47,17 @@ def draw(seed):
 
 @pytest.mark.parametrize("seed", range(16))
 def test_random_decode_chain(seed):
-    p = draw(1000 + seed)
+    _decode_chain(draw(1000 + seed), seed)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_decode_chain_large_batch(seed):
+    """The same chain with 257 to 1600 (row, kv head) blocks: the planner, full and subset
+    launches take the balanced row order wherever their rows reach 32 pages."""
+    _decode_chain(draw(3000 + seed, large=True), 3000 + seed)
+
+
+def _decode_chain(p, seed):
     c = make_case(batch=p["batch"], hq=p["hq"], hkv=p["hkv"], kv_lens=p["kv_lens"], dtype=p["dtype"], seed=p["seed"],
                   page_order=p["page_order"], trailing_empty_page=p["trailing_empty_page"], k=1, L=p["L"])
     g = c.to(DEV)

@@ -11,6 +11,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -21,13 +22,14 @@ SOURCES = ["capi.hip", "paged_decode.hip", "page_score.hip", "page_select.hip",
            "page_metadata.hip", "kv_rope.hip", "step_utils.hip",
            "skinny_gemm.hip", "prefill.hip"]
 
-HIPCC_FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+COMPILE_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "--offload-arch=gfx950",
     # Packed fp32 instructions off (v_pk_{add,mul,fma}_f32 are avoided on this pool).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]
+LINK_FLAGS = ["-shared", "-fPIC", "--offload-arch=gfx950"]
 
 
 def hipcc() -> str:
@@ -37,51 +39,43 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build(verbose: bool = False, extra_flags=None) -> Path:
-    """Compile every HIP source into one shared library; returns its path."""
-    srcs = [str(CSRC / s) for s in SOURCES]
-    fd, tmp = tempfile.mkstemp(prefix=".delta_hip.", suffix=".so.tmp", dir=str(PKG_DIR))
-    os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), "-o", tmp, *srcs]
+# hipcc's host pass warns about the device-only target feature: harmless.
+_NOISE = "is not a recognized feature for this target"
+
+
+def _run(cmd, verbose: bool, what: str) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass warns about the device-only target feature: harmless.
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in proc.stderr.splitlines() if _NOISE not in l)
     if proc.returncode != 0:
-        try:
-            os.unlink(tmp)
-        except OSError:
-            pass
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed on {what} ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    build_probe(verbose)
-    return LIB_PATH
 
 
-PROBE_SOURCES = ["probe_gather.hip"]
-PROBE_PATH = PKG_DIR / "_delta_probe.so"
-
-
-def build_probe(verbose: bool = False) -> Path:
-    """The measurement probe bench.py loads beside the library (``_delta_probe.so``)."""
-    fd, tmp = tempfile.mkstemp(prefix=".delta_probe.", suffix=".so.tmp", dir=str(PKG_DIR))
-    os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *[str(CSRC / s) for s in PROBE_SOURCES]]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
+def build(verbose: bool = False, extra_flags=None, jobs: int = 0) -> Path:
+    """Compile every HIP source (one object each, ``jobs`` at a time; default: one per CPU up
+    to 8) and link them into one shared library; returns its path."""
+    jobs = jobs or min(8, len(SOURCES), os.cpu_count() or 1)
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="delta_hip_build.") as tmpdir:
+        objs = [os.path.join(tmpdir, Path(s).stem + ".o") for s in SOURCES]
+        cmds = [[cc, *COMPILE_FLAGS, *(extra_flags or []), "-c", str(CSRC / s), "-o", o]
+                for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            futs = [pool.submit(_run, cmd, verbose, s) for cmd, s in zip(cmds, SOURCES)]
+            for f in futs:
+                f.result()
+        fd, tmp = tempfile.mkstemp(prefix=".delta_hip.", suffix=".so.tmp", dir=str(PKG_DIR))
+        os.close(fd)
         try:
+            _run([cc, *LINK_FLAGS, "-o", tmp, *objs], verbose, "the link")
+        except Exception:
             os.unlink(tmp)
-        except OSError:
-            pass
-        raise RuntimeError(f"hipcc failed on the probe ({proc.returncode}):\n{proc.stderr}")
-    os.replace(tmp, PROBE_PATH)
-    return PROBE_PATH
+            raise
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
 
 
 if __name__ == "__main__":

@@ -100,62 +100,94 @@ def _ulp32(x: float) -> float:
     return float(np.spacing(np.float32(abs(x))))
 
 
-@pytest.mark.parametrize("config", [2, 3, 4])
-def test_full_size_selection_matches_oracle_chain(config):
-    """End-to-end selection parity at the full BASELINE size: the GPU chain (planner dump + lse
-    -> scores -> radix select) against the oracle's own chain (fp64 logits rounded to fp32 ->
-    fp64 del3_legacy_softmax scores -> v2 selection), backend.py:887-904 and
-    page_selector_v2.py:113-188.  Two fp32 summation orders can only disagree on pages whose
-    keys straddle the k-th key closer than the scores' own error, so every differing page must
-    lie within twice the row's measured score error (plus an fp32 ulp) of the oracle's k-th key.
+# (config, planner route): the dump route (planner launch with the logits dump, then the
+# two-pass score kernel) everywhere, and the on-chip route (attention and page scores in one
+# pass, plain and with the decode token's RoPE + append fused in, the launch the engine's
+# config-3 step makes) where the rows' logits fit on chip.
+SELECTION_ROUTES = [(2, "dump"), (3, "dump"), (4, "dump"), (3, "on_chip"), (3, "on_chip_append")]
+
+
+def _planner_scores(c, route):
+    """Page scores of ``c``'s planner layer through ``route``; returns (scores, q the scores
+    were computed from, the cache after the launch)."""
+    B, hq = c.q.shape[:2]
+    hkv = c.kv_cache.shape[3]
+    mp = c.max_pages
+    lse = torch.empty(B, hq, device=DEV)
+    if route == "dump":
+        dump = torch.empty((B, hq, mp * 16), device=DEV)
+        K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
+                       lse=lse, logits_dump=dump)
+        s = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+        return s, c.q
+    append = route.endswith("append")
+    assert K.paged_decode_scores_supported(B, hq, hkv, mp, append), f"{route} does not apply at this shape"
+    ap, q_ref = None, c.q
+    if append:
+        # the decode token of every row at its last position: rotated k and v written into the
+        # slot, q rotated in the launch (the same rotation as delta_rope, tested bit for bit)
+        g = torch.Generator(device=DEV).manual_seed(77)
+        kn = torch.randn((B, hkv, 128), generator=g, device=DEV).to(c.q.dtype)
+        vn = torch.randn((B, hkv, 128), generator=g, device=DEV).to(c.q.dtype)
+        offs = torch.tensor([n - 1 for n in c.kv_lens], dtype=torch.int32, device=DEV)
+        ap = K.DecodeAppend(kn, vn, offs, c.kv_indptr, c.kv_indices, rope_scale=1.0, rope_theta=500000.0)
+        q_ref = K.rope(c.q, kn, torch.arange(B + 1, dtype=torch.int32, device=DEV), offs, rope_scale=1.0,
+                       rope_theta=500000.0)[0]
+    _, s = K.paged_decode_scores(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len,
+                                 max_pages_per_row=mp, lse=lse, append=ap)
+    return s, q_ref
+
+
+@pytest.mark.parametrize("config,route", SELECTION_ROUTES)
+def test_full_size_selection_matches_oracle_chain(config, route):
+    """End-to-end selection parity at the full BASELINE size, bit-exact: the GPU chain (planner
+    scores through ``route`` -> radix select) against the oracle's own chain (fp64 logits rounded
+    to fp32 -> fp64 del3_legacy_softmax scores -> v2 selection), backend.py:887-904 and
+    page_selector_v2.py:113-188.  Every row's selected pages must be identical.  Should a row
+    differ, the message says how far each differing page's key lies from the k-th key relative
+    to the row's score error (two fp32 summation orders can only swap pages closer than that).
     Sparse attention is always checked: the kernel over the oracle's selection against the
     oracle's sparse attention."""
     import math
     c = config_case(config, device=DEV)
     B, hq = c.q.shape[:2]
     mp, k, L = c.max_pages, c.k, c.L
-    dump = torch.empty((B, hq, mp * 16), device=DEV)
-    lse = torch.empty(B, hq, device=DEV)
-    K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices, c.kv_last_page_len, max_pages_per_row=mp,
-                   lse=lse, logits_dump=dump)
-    s = K.page_scores_from_logits(dump, c.kv_indptr, c.kv_last_page_len, mp, lse=lse)
+    s, q_ref = _planner_scores(c, route)
     idx, ip = K.select_pages(s, c.kv_indptr, c.block_table, k, L)
     torch.cuda.synchronize()
-    del dump
     cc = c.to("cpu")
-    x = O.dump_logits(cc.q, cc.kv_cache, cc.kv_indptr, cc.kv_indices, cc.kv_last_page_len, cc.sm_scale, mp * 16)
+    q_ref = q_ref.cpu()
+    x = O.dump_logits(q_ref, cc.kv_cache, cc.kv_indptr, cc.kv_indices, cc.kv_last_page_len, cc.sm_scale, mp * 16)
     ref_s = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
     del x
+    got_s = s.cpu().double()
+    assert_scores_close(got_s, ref_s, f"config {config} {route} scores")
     counts = cc.kv_indptr[1:] - cc.kv_indptr[:-1]
     want_i, want_p = O.select_pages(ref_s.float(), counts, cc.block_table, k, L)
     keys = O.prepare_scores(ref_s.float(), counts, L)
-    got_s = s.cpu().double()
     got_i, got_p = idx.cpu(), ip.cpu()
     assert got_p.tolist() == want_p.tolist()
-    rows_diff, pages_diff, worst = 0, 0, 0.0
+    report = []
+    pages_diff = 0
     for b in range(B):
         a = set(got_i[int(got_p[b]):int(got_p[b + 1])].tolist())
         r = set(want_i[int(want_p[b]):int(want_p[b + 1])].tolist())
         if a == r:
             continue
-        rows_diff += 1
         pages_diff += len(a - r)
         err = (got_s[b] - ref_s[b]).abs().max().item()
         kb = sorted(keys[b].tolist(), reverse=True)
         thr = kb[min(k, int(counts[b])) - 1]
         bt = cc.block_table[b].tolist()
-        for page in a ^ r:
-            j = bt.index(page)
-            gap = abs(float(keys[b, j]) - thr)
-            worst = max(worst, gap / max(err, 1e-30))
-            assert math.isfinite(thr) and gap <= 2 * err + _ulp32(thr), \
-                f"config {config} row {b} page {j}: key {float(keys[b, j])} is {gap:.3e} from the k-th key, " \
-                f"score error {err:.3e}"
-    print(f"[selection-parity] config {config}: {pages_diff} of {int(want_p[-1])} selected pages differ from the "
-          f"oracle's own chain, in {rows_diff} of {B} rows (worst gap / score error {worst:.2f})")
-    o_sp = K.paged_decode(c.q, c.kv_cache, want_p.to(DEV), want_i.to(DEV), c.kv_last_page_len, max_pages_per_row=k,
-                          subset=True)
-    o_ref, _ = O.paged_decode_attention(cc.q, cc.kv_cache, want_p, want_i, cc.kv_last_page_len, cc.sm_scale)
+        gaps = [abs(float(keys[b, bt.index(p)]) - thr) for p in a ^ r]
+        report.append(f"row {b}: {len(a - r)} pages, gaps to the k-th key {max(gaps):.3e} "
+                      f"(score error {err:.3e}, {max(gaps) / max(err, 1e-30):.2f}x; fp32 ulp {_ulp32(thr):.1e}; "
+                      f"k-th key finite: {math.isfinite(thr)})")
+    assert pages_diff == 0, (f"config {config} {route}: {pages_diff} of {int(want_p[-1])} selected pages differ "
+                             f"from the oracle's own chain: " + "; ".join(report))
+    o_sp = K.paged_decode(q_ref.to(DEV), c.kv_cache, want_p.to(DEV), want_i.to(DEV), c.kv_last_page_len,
+                          max_pages_per_row=k, subset=True)
+    o_ref, _ = O.paged_decode_attention(q_ref, cc.kv_cache, want_p, want_i, cc.kv_last_page_len, cc.sm_scale)
     assert_attn_close(o_sp, o_ref, f"config {config} sparse attention over the oracle's selection")
 
 

@@ -17,6 +17,9 @@ Also measured, in the same process:
     page indices, + the logits for the scorers);
   * the decode step of BASELINE config 4 end to end (Qwen2.5-7B shape, batch 4,
     64 k context), selective and full cache;
+  * the reference's own speed recipe end to end (DeepSeek-R1-Distill-Qwen-1.5B shape,
+    batch 64, full layers 0 1 2 14 22: three planner layers per step), selective and
+    full cache at 2 k, 8 k and 16 k context;
   * a CPU baseline: the oracle's PyTorch-CPU restatement of the same math,
     composed per step from per-op timings on a bounded sample.
 
@@ -25,7 +28,6 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import math
 import os
@@ -103,6 +105,55 @@ def engine_config4(torch, warmup: int, steps: int) -> dict:
             "speedup_vs_full_cache": round(ms_full / ms, 3)}
 
 
+RECIPE_CONTEXTS = (2048, 8192, 16384)
+
+
+def engine_recipe(torch, warmup: int, steps: int, contexts=RECIPE_CONTEXTS) -> dict:
+    """The reference's own speed recipe (run_reasoni_speed_compare.sh:16-28): a random-init
+    DeepSeek-R1-Distill-Qwen-1.5B-shaped model (28 layers, 12 q / 2 kv heads, qkv bias, bf16),
+    batch 64, max_len 18432, subset 64 pages, compression ratio 1, full layers 0 1 2 14 22 (so
+    layers 2, 14 and 22 are planners, each re-selecting the pages of the subset layers after it,
+    model.py:177-196), one hipGraph per step; selective and full-cache decode at several
+    contexts of the generation the recipe runs (its prompts are 4 tokens, so the context at a
+    step is the step index)."""
+    from delta_amd.backend import LMBackend
+    from delta_amd import ops
+    B, max_len, budget_pages = 64, 18432, 64
+    extra = 2 * (warmup + steps) + 16
+    eng = LMBackend(dtype=torch.bfloat16, device="cuda:0", cuda_graph_decode=True)
+    eng.load_model("random:DeepSeek-R1-Distill-Qwen-1.5B", seed=0)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = [0, 1, 2, 14, 22]
+    cfg.subset_cache_size = budget_pages
+    cfg.compression_ratio = 1.0
+    cfg.L = 8
+    eng.setup_caches(max_batch_size=B, max_seq_length=max_len)
+    roles = eng.layer_roles
+    out = {"workload": "reference speed recipe: DeepSeek-R1-Distill-Qwen-1.5B-shaped decode step, B=64, "
+                       "max_len 18432, 64-page budget (L=8, compression ratio 1), full layers [0,1,2,14,22] "
+                       "(planners at 2, 14, 22), one hipGraph per step",
+           "planner_layers": [i for i, r in enumerate(roles) if r == "plan"],
+           "planner_logits_on_chip": eng._plan_on_chip(), "contexts": {}}
+    for ctx in contexts:
+        eng.enable_selective_cache = True
+        eng.prepare_synthetic_decode(ctx, decode_budget=extra, seed=0)
+        ms = time_steps(torch, eng, warmup, steps)
+        eng.enable_selective_cache = False
+        eng._decode_graph = None
+        ms_full = time_steps(torch, eng, warmup, steps)
+        out["contexts"][str(ctx)] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 2),
+                                     "full_cache_ms_per_step": round(ms_full, 4),
+                                     "full_cache_tokens_per_s": round(B / ms_full * 1e3, 2),
+                                     "speedup_vs_full_cache": round(ms_full / ms, 3)}
+        log(f"  recipe ctx {ctx}: selective {ms:.3f} ms/step, full cache {ms_full:.3f} ms/step "
+            f"({ms_full / ms:.2f}x)")
+    ops.set_active_backend(None)
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def time_steps(torch, eng, warmup: int, steps: int) -> float:
     """ms per decode step over ``steps`` graph replays (after ``warmup`` replays)."""
     eng.decode_steps(warmup)
@@ -164,24 +215,6 @@ def warm_up(torch, run, seconds: float = 0.25):
     while time.perf_counter() - t0 < seconds:
         run()
     torch.cuda.synchronize()
-
-
-def gather_probe():
-    """The measurement probe library (``delta_amd/_delta_probe.so``), or None when not built."""
-    path = os.path.join(ROOT, "delta_amd", "_delta_probe.so")
-    if not os.path.exists(path):
-        return None
-    lib = ctypes.CDLL(path)
-    lib.delta_probe_gather_floor.restype = ctypes.c_int
-    lib.delta_probe_gather_floor.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
-                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    lib.delta_probe_gather_split.restype = ctypes.c_int
-    lib.delta_probe_gather_split.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
-                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                             ctypes.c_void_p, ctypes.c_void_p]
-    lib.delta_probe_empty.restype = ctypes.c_int
-    lib.delta_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    return lib
 
 
 def kernel_roofline(torch, reps: int = 60, n_rot: int = 30):
@@ -269,20 +302,6 @@ def kernel_roofline(torch, reps: int = 60, n_rot: int = 30):
         timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, p, i, c.kv_last_page_len,
                                                        max_pages_per_row=c.k, subset=True)),
         ntok_sub * 2 * row_kv + qo + B * c.k * 4, "K+V of the 128 selected pages/row, q, o, page ids")
-    probe = gather_probe()
-    if probe is not None:
-        sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
-
-        def floor(c, d, l, s, i, p):
-            rc = probe.delta_probe_gather_floor(
-                ctypes.c_void_p(c.kv_cache.data_ptr()), ctypes.c_int64(c.kv_cache.shape[0]),
-                ctypes.c_void_p(p.data_ptr()), ctypes.c_void_p(i.data_ptr()), B, hkv,
-                ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-            if rc:
-                raise RuntimeError(f"gather probe failed ({rc})")
-        # whole pages of the same selection, no arithmetic: the floor under the subset launch
-        add("gather floor (subset pages, no arithmetic)", timed(floor), B * c.k * 16 * 2 * row_kv,
-            "a bare gather of the subset launch's pages (K+V, whole pages) with its grid: the access pattern's own time")
     add("paged_decode_full_kernel",
         timed(lambda c, d, l, s, i, p: K.paged_decode(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
                                                        c.kv_last_page_len, max_pages_per_row=mp)),
@@ -403,39 +422,6 @@ def config_kernels(torch, config: int, reps: int = 12, n_rot: int = 2):
         timed(lambda c, d, l, s, i, p: K.page_score(c.q, c.kv_cache, c.kv_indptr, c.kv_indices,
                                                      c.kv_last_page_len, mp, scores=s)),
         ntok_full * row_kv + B * hq * 128 * esz + sum(npages) * 4 + B * mp * 4)
-    probe = gather_probe()
-    if probe is not None and B * hkv < 256 and c.k_per_row is None:
-        # Floors under a split subset launch (fewer than 256 (row, kv head) pairs): a bare gather
-        # of the same pages on the same split grid, and that gather followed by an empty launch of
-        # the merge's shape (the second launch's fixed cost in a graph).  The split count and
-        # unit size restate the small-launch plan of paged_decode.hip's decode_plan.
-        ns = max(1, min(-(-4096 // (B * hkv * 16)), max(1, kmax // 16), 1024))
-        waves = 4
-        if ns > 1 and ns * 4 <= 16 and ns * 4 <= kmax:  # the one-wave plan (4x the splits)
-            ns, waves = ns * 4, 1
-        chunk = -(-kmax // ns)
-        sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
-        stream_ptr = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-        def gather(c, d, l, s, i, p):
-            if probe.delta_probe_gather_split(ctypes.c_void_p(c.kv_cache.data_ptr()),
-                                              ctypes.c_int64(c.kv_cache.shape[0]), ctypes.c_void_p(p.data_ptr()),
-                                              ctypes.c_void_p(i.data_ptr()), B, hkv, ns, chunk, waves,
-                                              ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
-                raise RuntimeError("gather probe failed")
-
-        def gather_empty(*lay):
-            gather(*lay)
-            if probe.delta_probe_empty(B * hq, ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
-                raise RuntimeError("empty probe failed")
-        sel_bytes = sum(nsel) * 16 * 2 * row_kv
-        add(f"gather floor (split grid {B * ns}x{hkv}, {waves}-wave blocks)", timed(gather), sel_bytes)
-        add("gather floor + empty launch", timed(gather_empty), sel_bytes)
-
-        def empty(*lay):
-            if probe.delta_probe_empty(B * hq, ctypes.c_void_p(sink.data_ptr()), stream_ptr()):
-                raise RuntimeError("empty probe failed")
-        add("empty launch", timed(empty), 0)
     del layers, c
     torch.cuda.empty_cache()
     return res
@@ -636,6 +622,10 @@ def main():
                     help="skip the end-to-end decode step at BASELINE config 4")
     ap.add_argument("--engine-config4-only", action="store_true",
                     help="only the config-4 decode step (selective and full cache; for kernel traces)")
+    ap.add_argument("--no-engine-recipe", action="store_true",
+                    help="skip the reference speed recipe's decode step (DeepSeek-R1-Distill-Qwen-1.5B shape)")
+    ap.add_argument("--engine-recipe-only", action="store_true",
+                    help="only the reference speed recipe's decode step, selective and full cache")
     ap.add_argument("--kernel-reps", type=int, default=60)
     ap.add_argument("--configs-only", action="store_true",
                     help="only the kernel-level measurements at BASELINE configs 2, 4 and 5 (for rocprofv3 runs)")
@@ -665,6 +655,10 @@ def main():
         log(f"  selective {eng4['ms_per_step']:.3f} ms/step ({eng4['tokens_per_s']} tokens/s), full cache "
             f"{eng4['full_cache_ms_per_step']:.3f} ms/step: {eng4['speedup_vs_full_cache']}x")
         print(json.dumps({"engine_config4": eng4}), flush=True)
+        return
+    if args.engine_recipe_only:
+        log("engine at the reference speed recipe (DeepSeek-R1-Distill-Qwen-1.5B shape, B=64)")
+        print(json.dumps({"engine_recipe": engine_recipe(torch, args.warmup, args.steps)}), flush=True)
         return
     if args.configs_only:
         out = {}
@@ -743,6 +737,15 @@ def main():
             eng4 = {"error": repr(exc)}
             log(f"  failed: {exc!r}")
         torch.cuda.empty_cache()
+    recipe = None
+    if not args.no_engine_recipe:
+        log("engine at the reference speed recipe (DeepSeek-R1-Distill-Qwen-1.5B shape, B=64)")
+        try:
+            recipe = engine_recipe(torch, args.warmup, args.steps)
+        except Exception as exc:  # reported in the line, never fatal for the headline number
+            recipe = {"error": repr(exc)}
+            log(f"  failed: {exc!r}")
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
@@ -768,7 +771,6 @@ def main():
         "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": dom["frac"], "traffic": profiled_traffic("paged_decode_subset_kernel<ROPE>"),
                      "algorithmic_bytes": dom["bytes"],
-                     "gather_floor_us": kern.get("gather floor (subset pages, no arithmetic)", {}).get("us"),
                      "kernel": "paged_decode_subset_kernel<ROPE> (delta_paged_decode_subset_append, the launch "
                                "of every selective layer in a decode step)"},
         "cpu_baseline": cpu,
@@ -778,6 +780,7 @@ def main():
         "prefill": prefill,
         "kernels_other_configs": others,
         "engine_config4": eng4,
+        "engine_recipe": recipe,
     }
     print(json.dumps(line), flush=True)
 

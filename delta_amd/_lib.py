@@ -12,7 +12,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_delta_hip.so"
 
 DELTA_BF16 = 0
 DELTA_FP16 = 1
-ABI_VERSION = 200  # delta_abi_version() of the library these signatures describe
+ABI_VERSION = 201  # delta_abi_version() of the library these signatures describe
 
 _P = c_void_p
 
@@ -80,7 +80,7 @@ SIGNATURES = {
     "delta_pack_page_indices": (c_int, [
         _P, c_int, _P, _P, _P, _P, _P, c_int64, _P, c_int, c_int, c_int, c_int, _P]),
     "delta_decode_page_info": (c_int, [
-        _P, _P, _P, c_int, c_int, c_int, c_double, c_int, _P, _P, _P, _P, _P, _P, _P, _P]),
+        _P, _P, _P, c_int, c_int, c_int, _P, c_double, c_int, _P, _P, _P, _P, _P, _P, _P, _P]),
     "delta_append_kv": (c_int, [
         _P, c_int64, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int,
         c_int, c_int, _P]),
@@ -120,14 +120,20 @@ def load() -> ctypes.CDLL:
                 f"delta_amd HIP library missing at {LIB_PATH}; build it with "
                 "`python -m delta_amd.build` (there is no CPU fallback)")
         lib = ctypes.CDLL(str(LIB_PATH))
+        # The version first: a stale library may lack entry points these bindings name.
+        ver_fn = getattr(lib, "delta_abi_version", None)
+        ver = None
+        if ver_fn is not None:
+            ver_fn.restype = c_int
+            ver_fn.argtypes = []
+            ver = ver_fn()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {ver}, these bindings expect {ABI_VERSION}: rebuild it "
+                               "with `python -m delta_amd.build`")
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        ver = lib.delta_abi_version()
-        if ver != ABI_VERSION:
-            raise RuntimeError(f"{LIB_PATH} has ABI {ver}, these bindings expect {ABI_VERSION}: rebuild it "
-                               "with `python -m delta_amd.build`")
         _lib = lib
     return _lib
 

@@ -136,6 +136,13 @@ class LMBackend:
         self._decode_graph_failed: Optional[str] = None
         self._decode_graph_stats = defaultdict(int)
         self._decode_graph_fallback_reasons = defaultdict(int)
+        self._decode_graph_capture_errors = {}
+        self._decode_graph_capture_time_s = defaultdict(float)
+        # delta_impl_profile: named device sections timed with HIP events (backend.py:105-107)
+        self._delta_impl_profile_ms = defaultdict(float)
+        self._delta_impl_profile_counts = defaultdict(int)
+        self._delta_impl_profile_pending = []
+        self._profile_paused = False  # the capture's warm-up bodies are not steps
         self._pending_events = []
         self._step_records = []
         self._using_subset_cache_this_step = False
@@ -144,12 +151,14 @@ class LMBackend:
     def set_tokenizer(self, tokenizer):
         self.tokenizer = tokenizer
 
-    def load_model(self, checkpoints, use_tp: bool = False, rank_group=None, group=None, seed: int = 0):
+    def load_model(self, checkpoints, use_tp: bool = False, rank_group=None, group=None, seed: int = 0,
+                   **shape_overrides):
         """Load a model (backend.py:227-228 -> utils.py:209-231).
 
         ``checkpoints`` is either a ``model.pth`` state dict (loaded with
         ``weights_only=True``; its parent directory names the shape, as in the
-        reference) or ``"random:<shape>"`` for a seeded random-init model.  A state dict
+        reference) or ``"random:<shape>"`` for a seeded random-init model, whose
+        ``ModelArgs`` fields ``shape_overrides`` may change (e.g. ``n_layer``).  A state dict
         loads strictly, as the reference's does (utils.py:217-221): separate wq/wk/wv and
         w1/w3 tensors are merged by the modules' load hooks, and a missing or unknown key
         raises instead of leaving a parameter at its random init.
@@ -158,8 +167,11 @@ class LMBackend:
             raise NotImplementedError("tensor parallelism is out of scope for this one-GPU path")
         ck = str(checkpoints)
         if ck.startswith("random:"):
-            self.model = build_random_model(ck[len("random:"):], self.device, self.dtype, seed=seed)
+            self.model = build_random_model(ck[len("random:"):], self.device, self.dtype, seed=seed,
+                                            **shape_overrides)
             return
+        if shape_overrides:
+            raise ValueError("shape overrides apply to random-init models only; a checkpoint names its shape")
         path = Path(ck)
         model = build_random_model(path.parent.name, self.device, self.dtype, seed=seed)
         state = torch.load(str(path), mmap=True, weights_only=True)
@@ -192,6 +204,7 @@ class LMBackend:
         self.num_pages = self.max_num_pages + max_batch_size
         self.scratch_pages = torch.arange(self.max_num_pages, self.num_pages, dtype=torch.int32)
         self.page_pool = PagePool(self.max_num_pages, seed=0)
+        self._synthetic_pages: List[int] = []  # held by prepare_synthetic_decode
         self.scheduler = BatchSlots(max_batch_size, self.page_pool, verbose=self.is_main_process)
 
         self.enable_selective_cache = bool(getattr(cfg, "enable_selective_cache", False))
@@ -214,6 +227,10 @@ class LMBackend:
         self.page_selector = PageSelectorV2(B, self.pages_per_slot, True, self.k_eff,
                                            self.compression_ratio, self.L, dev,
                                            position_bias_scale=1e-7 if self.enable_delta_v2_position_bias else 0.0)
+        # Per-row subset budgets (``set_subset_budgets``): read by the metadata and selection
+        # launches when switched on, so a captured step takes new values on every replay.
+        self.k_per_row = torch.full((B,), self.k_eff, **i32)
+        self._per_row_budgets = False
         self.use_subset_flag = torch.zeros(1, **i32)
         self.qo_indptr = torch.arange(B + 1, **i32)
         self.static_tokens = torch.zeros((1, B), dtype=torch.long, device=dev)
@@ -237,6 +254,39 @@ class LMBackend:
         self.layer_roles = list(self.model.layer_roles)
         ops.set_active_backend(self)
         self._decode_graph = None
+
+    def set_subset_budgets(self, pages=None) -> None:
+        """Give each slot its own subset budget in pages, or go back to the global
+        ``subset_cache_size`` with ``None``.  An extension: the reference selects one global k
+        per step, ``min(pages, k)`` per row (page_selector_v2.py:136-164); a per-row budget is
+        what BASELINE config 5's ``max(512, len/8)``-token rule needs.  Each budget lies in
+        [1, subset_cache_size] (the cap the subset attention launch is planned for).  Row b's
+        subset is then min(pages_b, budget_b) pages, in the ``use_subset`` gate's totals, the
+        default subset CSR and the selection.  New values take effect on the next step, replayed
+        or eager; switching the per-row budgets on or off captures the step again."""
+        if self.cachelens is None:
+            raise RuntimeError("setup_caches() first")
+        if pages is None:
+            if self._per_row_budgets:
+                self._decode_graph = None
+            self._per_row_budgets = False
+            return
+        vals = [int(x) for x in (pages.tolist() if isinstance(pages, torch.Tensor) else pages)]
+        if len(vals) != self.batch_size:
+            raise ValueError(f"need {self.batch_size} per-row budgets, got {len(vals)}")
+        bad = [v for v in vals if v < 1 or v > self.k_eff]
+        if bad:
+            raise ValueError(f"per-row budgets must lie in [1, {self.k_eff}] pages (the subset_cache_size cap); "
+                             f"got {bad[0]}")
+        with torch.inference_mode():
+            self.k_per_row.copy_(torch.tensor(vals, dtype=torch.int32))
+        if not self._per_row_budgets:
+            self._decode_graph = None
+        self._per_row_budgets = True
+
+    def _row_budgets(self):
+        """The per-row budget tensor when per-row budgets are on, else None (global k)."""
+        return self.k_per_row if self._per_row_budgets else None
 
     # ----------------------------------------------------------- op bodies
     def rope_params(self) -> dict:
@@ -267,18 +317,19 @@ class LMBackend:
     def attn_full(self, q, kv_cache, append=None):
         st = self._step
         if st.mode == "prefill":  # several query tokens per row: causal prefill kernel
-            return K.paged_prefill(q, kv_cache, st.qo_indptr, st.kv_indptr, st.kv_indices, st.kv_last,
-                                   max_qo_len=st.max_qo)
-        return K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                              max_pages_per_row=st.max_pages, workspace=self.workspace, append=append)
+            return self._profile_cuda_section("delta_prefill_attention", lambda: K.paged_prefill(
+                q, kv_cache, st.qo_indptr, st.kv_indptr, st.kv_indices, st.kv_last, max_qo_len=st.max_qo))
+        return self._profile_cuda_section("delta_full_attention", lambda: K.paged_decode(
+            q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last, max_pages_per_row=st.max_pages,
+            workspace=self.workspace, append=append))
 
     def attn_subset(self, q, kv_cache, append=None):
         if not (self.enable_selective_cache and self._decode_mode()):
             return self.attn_full(q, kv_cache, append=append)
         sel = self.page_selector
-        return K.paged_decode(q, kv_cache, sel.paged_subset_kv_indptr, sel.paged_subset_kv_indices,
-                              self._step.kv_last, max_pages_per_row=self.k_eff, workspace=self.workspace,
-                              subset=True, append=append)
+        return self._profile_cuda_section("delta_subset_attention", lambda: K.paged_decode(
+            q, kv_cache, sel.paged_subset_kv_indptr, sel.paged_subset_kv_indices, self._step.kv_last,
+            max_pages_per_row=self.k_eff, workspace=self.workspace, subset=True, append=append))
 
     def _plan_on_chip(self) -> bool:
         return self.plan_scores_on_chip and not self.enable_delta_debug_page_selection_parity
@@ -291,20 +342,29 @@ class LMBackend:
         st = self._step
         sel = self.page_selector
         B = q.shape[0]
+        prof = self._profile_cuda_section
         if self._plan_on_chip():
-            o, _ = K.paged_decode_scores(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                                         max_pages_per_row=st.max_pages, lse=self.lse, scores=self.page_scores,
-                                         workspace=self.workspace, append=append)
+            # attention and page scores in one pass: one section for both
+            o, _ = prof("delta_planner_attention_scores", lambda: K.paged_decode_scores(
+                q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last, max_pages_per_row=st.max_pages, lse=self.lse,
+                scores=self.page_scores, workspace=self.workspace, append=append))
         else:
-            o = K.paged_decode(q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last,
-                               max_pages_per_row=st.max_pages, lse=self.lse, logits_dump=self.dump,
-                               workspace=self.workspace, append=append)
-            K.page_scores_from_logits(self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse,
-                                      scores=self.page_scores, batch=B, workspace=self.workspace)
-        K.select_pages(self.page_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,
-                       pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
-                       use_subset=self.use_subset_flag, out_indices=sel.paged_subset_kv_indices,
-                       out_indptr=sel.paged_subset_kv_indptr)
+            o = prof("delta_planner_attention_dump", lambda: K.paged_decode(
+                q, kv_cache, st.kv_indptr, st.kv_indices, st.kv_last, max_pages_per_row=st.max_pages, lse=self.lse,
+                logits_dump=self.dump, workspace=self.workspace, append=append))
+
+        def replan():  # backend.py:787-853: page scores (dump path), then the v2 selection
+            if not self._plan_on_chip():
+                prof("delta_page_score", lambda: K.page_scores_from_logits(
+                    self.dump, st.kv_indptr, st.kv_last, self.pages_per_slot, lse=self.lse, scores=self.page_scores,
+                    batch=B, workspace=self.workspace))
+            prof("delta_page_select", lambda: K.select_pages(
+                self.page_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,
+                pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
+                k_per_row=self._row_budgets(), use_subset=self.use_subset_flag,
+                out_indices=sel.paged_subset_kv_indices, out_indptr=sel.paged_subset_kv_indptr))
+
+        prof("delta_replan_total", replan)
         return o
 
     def _debug_check_selection(self, st, B):
@@ -314,7 +374,7 @@ class LMBackend:
         sel = self.page_selector
         ri, rp = K.select_pages(ref_scores, st.kv_indptr, sel._block_table, self.k_eff, self.L,
                                 pos_bias_scale=sel.position_bias_scale, batch=B, max_pages=self.pages_per_slot,
-                                use_subset=self.use_subset_flag,
+                                k_per_row=self._row_budgets(), use_subset=self.use_subset_flag,
                                 out_indices=torch.empty_like(sel.paged_subset_kv_indices))
         n = int(rp[B])
         if not torch.equal(rp[:B + 1], sel.paged_subset_kv_indptr[:B + 1]) or \
@@ -342,10 +402,11 @@ class LMBackend:
         bt = self.slot_block_table.cpu()
         counts = [(n + 1) // PAGE_SIZE + 1 for n in lens]
         last = [(n + 1) % PAGE_SIZE for n in lens]
+        ks = self.k_per_row.tolist() if self._per_row_budgets else [k] * B
         full_tot = sum(c for c, a in zip(counts, act) if a)
-        sub_tot = sum(min(c, k) for c, a in zip(counts, act) if a)
+        sub_tot = sum(min(c, kb) for c, kb, a in zip(counts, ks, act) if a)
         use = bool(self.enable_selective_cache and sub_tot > 0 and full_tot / sub_tot > self.compression_ratio)
-        sub_counts = [min(c, k) if use else c for c in counts]
+        sub_counts = [min(c, kb) if use else c for c, kb in zip(counts, ks)]
         ip, sub_ip = [0], [0]
         ind, sub_ind = [], []
         for b in range(B):
@@ -407,11 +468,11 @@ class LMBackend:
         """One decode step for all slots; only device work (capturable)."""
         B = self.batch_size
         sel = self.page_selector
-        K.decode_page_info(self.cachelens, self.slot_block_table, B, self.k_eff, self.compression_ratio,
-                           self.enable_selective_cache, sel.paged_kv_indptr, sel.paged_kv_indices,
-                           sel.paged_kv_last_page_len, row_block_table=sel._block_table,
-                           subset_indices=sel.paged_subset_kv_indices, subset_indptr=sel.paged_subset_kv_indptr,
-                           use_subset=self.use_subset_flag, active=self.active)
+        self._profile_cuda_section("delta_decode_page_info", lambda: K.decode_page_info(
+            self.cachelens, self.slot_block_table, B, self.k_eff, self.compression_ratio, self.enable_selective_cache,
+            sel.paged_kv_indptr, sel.paged_kv_indices, sel.paged_kv_last_page_len, row_block_table=sel._block_table,
+            subset_indices=sel.paged_subset_kv_indices, subset_indptr=sel.paged_subset_kv_indptr,
+            use_subset=self.use_subset_flag, active=self.active, k_per_row=self._row_budgets()))
         self._step = self._decode_csr()
         try:
             tokens = self.model(self.static_tokens, self.cachelens, self.qo_indptr, sel.paged_kv_indices,
@@ -424,13 +485,18 @@ class LMBackend:
         return tokens
 
     def _capture_decode_graph(self):
+        t0 = time.perf_counter()
         stream = torch.cuda.Stream(device=self.device)
         saved_tokens = self.static_tokens.clone()
         stream.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(stream):
-            for _ in range(2):  # warm-up (workspaces, BLAS handles); no cachelens advance
-                self._decode_body(advance=False)
-                self.static_tokens.copy_(saved_tokens)
+        self._profile_paused = True
+        try:
+            with torch.cuda.stream(stream):
+                for _ in range(2):  # warm-up (workspaces, BLAS handles); no cachelens advance
+                    self._decode_body(advance=False)
+                    self.static_tokens.copy_(saved_tokens)
+        finally:
+            self._profile_paused = False
         torch.cuda.current_stream(self.device).wait_stream(stream)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -438,6 +504,7 @@ class LMBackend:
         self._decode_graph = graph
         self._decode_graph_on_chip = self._plan_on_chip()
         self._decode_graph_stats["captures"] += 1
+        self._decode_graph_capture_time_s["decode_step"] += time.perf_counter() - t0
 
     def sync_host_lens(self):
         """Re-read ``cachelens`` / ``active`` from the device into the host mirror (after a
@@ -469,6 +536,7 @@ class LMBackend:
                 self._decode_graph_failed = repr(exc)
                 self._decode_graph_stats["capture_failures"] += 1
                 self._decode_graph_fallback_reasons["capture_failed"] += 1
+                self._decode_graph_capture_errors["decode_step"] = repr(exc)
                 if self.is_main_process:
                     print(f"[hip graph decode] capture failed, running eagerly: {exc}")
         debug = self.enable_delta_debug_fast_decode_page_info_parity or (
@@ -477,18 +545,22 @@ class LMBackend:
             before = self.cachelens.clone() if debug else None
             if use_graph and self._decode_graph is not None:
                 try:
-                    self._decode_graph.replay()
+                    # one section per replay: a replayed step cannot be split into its parts
+                    self._profile_cuda_section("delta_decode_step_graph", self._decode_graph.replay)
                     self._decode_graph_stats["replays"] += 1
                 except Exception as exc:  # replay failure -> eager from here on (backend.py:1172-1181)
                     self._decode_graph = None
                     self._decode_graph_failed = repr(exc)
                     self._decode_graph_stats["replay_failures"] += 1
                     self._decode_graph_fallback_reasons["replay_failed"] += 1
+                    self._decode_graph_capture_errors["replay"] = repr(exc)
                     if self.is_main_process:
                         print(f"[hip graph decode] replay failed, running eagerly: {exc}")
                     self._decode_body(advance=True)
             else:
-                self._decode_body(advance=True)
+                if use_graph:  # the graph is off for this engine (capture failed or disabled)
+                    self._decode_graph_fallback_reasons["no_graph_eager_step"] += 1
+                self._profile_cuda_section("delta_decode_step_eager", lambda: self._decode_body(advance=True))
             if debug:
                 self._debug_checks_after_step(before)
         for b in range(self.batch_size):
@@ -505,18 +577,25 @@ class LMBackend:
         or one length per slot): pages for ``kv_len + decode_budget`` tokens from the page
         pool, seeded N(0, fill_std) K/V in every layer, random current tokens.  With
         ``k_outlier_channels`` = n, n seeded head-dim channels of every layer's K are scaled by
-        ``k_outlier_scale`` (per-channel outliers).  Used by the benchmark and tests (no
-        prompts, no prefill)."""
+        ``k_outlier_scale`` (per-channel outliers).  The pages an earlier call took go back to
+        the pool first.  Used by the benchmark and tests (no prompts, no prefill)."""
         B = self.batch_size
         lens = [int(kv_len)] * B if isinstance(kv_len, int) else [int(x) for x in kv_len]
         if len(lens) != B:
             raise ValueError(f"need {B} context lengths, got {len(lens)}")
-        bt = self.slot_block_table.cpu()
-        for b, n in enumerate(lens):
+        for n in lens:
             need = (n + decode_budget) // PAGE_SIZE + 1
             if need > self.pages_per_slot:
                 raise ValueError(f"{n} + {decode_budget} tokens need {need} pages > {self.pages_per_slot}")
-            bt[b, :need] = torch.tensor(self.page_pool.take(need), dtype=torch.int32)
+        if self._synthetic_pages:
+            self.page_pool.give_back(self._synthetic_pages)
+            self._synthetic_pages = []
+        bt = self.slot_block_table.cpu()
+        for b, n in enumerate(lens):
+            need = (n + decode_budget) // PAGE_SIZE + 1
+            pages = self.page_pool.take(need)
+            self._synthetic_pages.extend(pages)
+            bt[b, :need] = torch.tensor(pages, dtype=torch.int32)
         self.slot_block_table.copy_(bt)
         self._slot_pages = [(n + decode_budget) // PAGE_SIZE + 1 for n in lens]
         self._host_lens = list(lens)
@@ -586,6 +665,8 @@ class LMBackend:
             if not self.scheduler.any_active():
                 break
             self._forward(i)
+            if self.enable_delta_impl_profile:
+                self._flush_delta_impl_profile_events()
         if self.is_main_process:
             self._print_final_stats()
         return self.get_detailed_results()
@@ -608,6 +689,42 @@ class LMBackend:
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
         return ev
+
+    def _profile_cuda_section(self, name: str, fn):
+        """Run ``fn``; with ``delta_impl_profile`` on, time its device work between two HIP events
+        on the current stream under ``name`` (backend.py:1570-1578).  While a decode step is
+        being captured the section runs untimed (events recorded into a capture would become
+        graph nodes); a replayed step is timed whole as ``delta_decode_step_graph``, so the
+        per-section breakdown of a decode step comes from eager steps (``cuda_graph_decode``
+        off)."""
+        if not self.enable_delta_impl_profile or self._profile_paused or torch.cuda.is_current_stream_capturing():
+            return fn()
+        start = self._record_event()
+        out = fn()
+        end = self._record_event()
+        self._delta_impl_profile_pending.append((name, start, end))
+        self._delta_impl_profile_counts[name] += 1
+        return out
+
+    def _flush_delta_impl_profile_events(self):
+        """Add the finished sections' times into the totals (backend.py:1580-1585); waits for
+        the device."""
+        if not self._delta_impl_profile_pending:
+            return
+        torch.cuda.synchronize(self.device)
+        for name, start, end in self._delta_impl_profile_pending:
+            self._delta_impl_profile_ms[name] += start.elapsed_time(end)
+        self._delta_impl_profile_pending.clear()
+
+    def delta_impl_profile_summary(self) -> dict:
+        """``{section: {"count", "total_ms", "avg_ms"}}`` of the sections timed so far."""
+        self._flush_delta_impl_profile_events()
+        out = {}
+        for name in sorted(self._delta_impl_profile_counts):
+            n = self._delta_impl_profile_counts[name]
+            tot = self._delta_impl_profile_ms.get(name, 0.0)
+            out[name] = {"count": n, "total_ms": tot, "avg_ms": tot / n if n else 0.0}
+        return out
 
     def _forward(self, step_index: int):
         slots = self._active_slots()
@@ -637,7 +754,8 @@ class LMBackend:
         else:
             self._using_subset_cache_this_step = False
             ev1 = self._record_event()
-            next_tokens, qo_lengths = self._prefill_forward(slots, reqs)
+            next_tokens, qo_lengths = self._profile_cuda_section("delta_prefill_step",
+                                                                 lambda: self._prefill_forward(slots, reqs))
             ev2 = self._record_event()
         for r, t in zip(reqs, next_tokens):
             r.record(int(t))
@@ -704,9 +822,23 @@ class LMBackend:
         print(f"Total requests: {len(self.scheduler.requests)}")
         print(f"Total tokens: {total_tokens:,}")
         print(f"Tokens per second: {total_tokens / max(total_time, 1e-9):.2f}")
-        if self.enable_cuda_graph_decode:
-            print(f"HIP graph decode: {dict(self._decode_graph_stats)}"
-                  + (f" (capture failed: {self._decode_graph_failed})" if self._decode_graph_failed else ""))
+        if self.enable_cuda_graph_decode:  # backend.py:2199-2215
+            st = self._decode_graph_stats
+            print("\nHIP Graph Decode:")
+            for key in ("captures", "replays", "capture_failures", "replay_failures"):
+                print(f"  {key.replace('_', ' ')}: {st.get(key, 0)}")
+            if self._decode_graph_capture_time_s:
+                print(f"  capture time by graph: "
+                      f"{ {k: round(v, 3) for k, v in self._decode_graph_capture_time_s.items()} }")
+            if self._decode_graph_fallback_reasons:
+                print(f"  fallback reasons: {dict(self._decode_graph_fallback_reasons)}")
+            if self._decode_graph_capture_errors:
+                print(f"  capture errors: {self._decode_graph_capture_errors}")
+        prof = self.delta_impl_profile_summary() if self.enable_delta_impl_profile else {}
+        if prof:  # backend.py:2232-2238
+            print("\nDELTA Implementation Profile:")
+            for name, r in prof.items():
+                print(f"  {name:<32s} avg {r['avg_ms']:8.3f} ms  total {r['total_ms']:10.1f} ms  ({r['count']} calls)")
         if self._step_records:
             n = len(self._step_records)
             for key in ("collect_pages_ms", "model_forward_ms", "postprocess_ms", "step_total_ms"):
@@ -721,7 +853,21 @@ class LMBackend:
                         "max_length": self.max_length, "page_size": PAGE_SIZE,
                         "selective_cache": self.enable_selective_cache, "num_steps": n,
                         "cuda_graph_decode": self.enable_cuda_graph_decode,
-                        "cuda_graph_decode_stats": dict(self._decode_graph_stats)}
+                        "cuda_graph_decode_stats": dict(self._decode_graph_stats),
+                        "cuda_graph_decode_fallback_reasons": dict(self._decode_graph_fallback_reasons),
+                        "cuda_graph_decode_capture_errors": dict(self._decode_graph_capture_errors),
+                        "cuda_graph_decode_capture_time_s": dict(self._decode_graph_capture_time_s),
+                        "delta_impl_profile": bool(self.enable_delta_impl_profile),
+                        "delta_impl_profile_ms": dict(self._delta_impl_profile_ms),
+                        "delta_impl_profile_counts": dict(self._delta_impl_profile_counts),
+                        "delta_fused_page_scores": self.enable_delta_fused_page_scores,
+                        "delta_fixed_selector": self.enable_delta_fixed_selector,
+                        "delta_debug_page_selection_parity": self.enable_delta_debug_page_selection_parity,
+                        "delta_subset_plan_reuse": self.enable_delta_subset_plan_reuse,
+                        "delta_dump_buffer_dtype": self.delta_dump_buffer_dtype,
+                        "delta_page_score_impl": self.delta_page_score_impl,
+                        "planner_logits_on_chip": self._plan_on_chip() if self.enable_selective_cache else False,
+                        "per_row_budgets": self._per_row_budgets}
                 path.write_text(json.dumps({"meta": meta, "steps": self._step_records}, indent=2))
                 print(f"  Step timings saved to: {path}")
         print("=" * 60)

@@ -14,7 +14,10 @@
 // block recomputes its row offset from the counts of the rows before it.
 // Idle slots (active[b] == 0) keep their CSR entries (one scratch page) but are
 // left out of the gate's page totals, which the reference sums over its active
-// rows only (backend.py:2047-2067, 2104-2109).
+// rows only (backend.py:2047-2067, 2104-2109).  With per-row budgets
+// (k_per_row, an extension: the reference has one global subset_cache_size),
+// row b's subset count is min(pages_b, k_per_row[b]) in the gate's totals and
+// in the default subset CSR, as the selector counts it.
 #include "delta_common.h"
 
 namespace delta {
@@ -47,6 +50,7 @@ struct PageInfoArgs {
   const int32_t *active;  // [batch] or null (every row active)
   const int32_t *slot_bt;
   int batch, pages_per_slot, k;
+  const int32_t *k_per_row;  // [batch] or null (every row takes k)
   double compression_ratio;
   int selective;
   int32_t *kv_indptr, *kv_indices, *last_page_len, *row_bt, *subset_indices, *subset_indptr, *use_subset;
@@ -65,6 +69,13 @@ __device__ __forceinline__ void row_pages(const PageInfoArgs &a, int b, int *np,
   *last = lp;
 }
 
+// Row b's subset budget in pages (the selector's row_budget: clamped to [0, pages_per_slot]).
+__device__ __forceinline__ int row_budget(const PageInfoArgs &a, int b) {
+  int kb = a.k_per_row ? a.k_per_row[b] : a.k;
+  kb = kb < 0 ? 0 : kb;
+  return kb > a.pages_per_slot ? a.pages_per_slot : kb;
+}
+
 __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
   __shared__ long long s_red[4][4];
   const int b = blockIdx.x;
@@ -73,7 +84,8 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
   for (int i = tid; i < a.batch; i += 256) {
     int np, lp;
     row_pages(a, i, &np, &lp);
-    const int sc = np < a.k ? np : a.k;
+    const int kb = row_budget(a, i);
+    const int sc = np < kb ? np : kb;
     if (a.active == nullptr || a.active[i] != 0) {
       full_tot += np;
       sub_tot += sc;
@@ -106,7 +118,8 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
   row_pages(a, b, &np, &lp);
   // use_subset gate (backend.py:2104-2109); when it is off the subset CSR is the full CSR.
   const bool gate = a.selective && sub_tot > 0 && ((double)full_tot / (double)sub_tot) > a.compression_ratio;
-  const int sc = gate ? (np < a.k ? np : a.k) : np;
+  const int kb = row_budget(a, b);
+  const int sc = gate ? (np < kb ? np : kb) : np;
   const long long sb = gate ? sub_before : full_before;
   if (tid == 0) {
     a.kv_indptr[b + 1] = (int32_t)(full_before + np);
@@ -157,7 +170,8 @@ extern "C" DELTA_EXPORT int delta_pack_page_indices(const int32_t *slot_block_ta
 
 extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, const int32_t *active,
                                                    const int32_t *slot_block_table, int batch, int pages_per_slot,
-                                                   int k, double compression_ratio, int selective, int32_t *kv_indptr, int32_t *kv_indices,
+                                                   int k, const int32_t *k_per_row, double compression_ratio,
+                                                   int selective, int32_t *kv_indptr, int32_t *kv_indices,
                                                    int32_t *kv_last_page_len, int32_t *row_block_table,
                                                    int32_t *subset_indices, int32_t *subset_indptr,
                                                    int32_t *use_subset, delta_stream_t stream) {
@@ -176,6 +190,7 @@ extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, con
   a.batch = batch;
   a.pages_per_slot = pages_per_slot;
   a.k = k < 0 ? 0 : k;
+  a.k_per_row = k_per_row;
   a.compression_ratio = compression_ratio;
   a.selective = selective;
   a.kv_indptr = kv_indptr;

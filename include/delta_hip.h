@@ -352,9 +352,14 @@ int delta_pack_page_indices(const int32_t *slot_block_table, int num_slots,
  * min(pages, k) pages when the gate is on and the full CSR when it is off (the
  * reference rebinds the subset lists to the full ones, backend.py:2111-2150),
  * so subset_indices needs batch * pages_per_slot entries.  Rows whose page
- * count would exceed pages_per_slot are clamped (callers bound their rows). */
+ * count would exceed pages_per_slot are clamped (callers bound their rows).
+ * k_per_row (int32 [batch], optional; an extension, the reference has one
+ * global k) gives row b the budget k_per_row[b] in place of k, clamped to
+ * [0, pages_per_slot] as delta_select_pages clamps it: the gate's subset total
+ * and the default subset CSR then count min(pages, k_per_row[b]) for row b. */
 int delta_decode_page_info(const int32_t *cachelens, const int32_t *active,
-                           const int32_t *slot_block_table, int batch, int pages_per_slot, int k, double compression_ratio,
+                           const int32_t *slot_block_table, int batch, int pages_per_slot, int k,
+                           const int32_t *k_per_row, double compression_ratio,
                            int selective, int32_t *kv_indptr, int32_t *kv_indices,
                            int32_t *kv_last_page_len, int32_t *row_block_table,
                            int32_t *subset_indices, int32_t *subset_indptr,

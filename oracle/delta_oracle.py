@@ -345,7 +345,7 @@ def pack_page_indices(slot_block_table: torch.Tensor, active_slots: torch.Tensor
             row_block_table[r, :c] = vals
 
 
-def decode_page_info(cachelens: torch.Tensor, pages_per_row_alloc: int, k: int,
+def decode_page_info(cachelens: torch.Tensor, pages_per_row_alloc: int, k,
                      page_size: int = PAGE_SIZE):
     """Per-row page counts for one decode step, as ``_collect_decode_page_info_fast``.
 
@@ -354,13 +354,16 @@ def decode_page_info(cachelens: torch.Tensor, pages_per_row_alloc: int, k: int,
     ``kv_len = cachelens + 1``, ``page_count = kv_len // 16 + 1`` and
     ``last_page_len = kv_len % 16`` (a full page leaves a fresh empty page).
     ``subset_count = min(page_count, k)``, ``subset_start = page_count - subset_count``.
+    ``k`` is the global ``subset_cache_size`` or, for this build's per-row budgets (an
+    extension), one budget per row (negative budgets count as 0).
     """
     kv_len = cachelens.to(torch.int64) + 1
     page_count = kv_len // page_size + 1
     if int(page_count.max()) > pages_per_row_alloc:
         raise RuntimeError("row outgrew its page allocation")
     last = kv_len % page_size
-    subset_count = torch.clamp(page_count, max=k)
+    kk = torch.clamp(torch.as_tensor(k, dtype=torch.int64), min=0)
+    subset_count = torch.minimum(page_count, kk)
     subset_start = page_count - subset_count
     return page_count, last, subset_count, subset_start
 
@@ -372,22 +375,25 @@ def use_subset_decision(full_total: int, subset_total: int, compression_ratio: f
                 and (full_total / subset_total) > compression_ratio)
 
 
-def decode_step_gate(cachelens, active, k: int, compression_ratio: float,
+def decode_step_gate(cachelens, active, k, compression_ratio: float,
                      enable_selective_cache: bool = True, page_size: int = PAGE_SIZE) -> bool:
     """The decode step's ``use_subset`` decision over its active rows only.
 
     backend.py:2047-2067 loops over ``active_slots``: each row's ``page_count`` (after
     ``plan(1, 16)``) goes into ``full_total`` and ``min(page_count, subset_cache_size)``
     into ``subset_total``; backend.py:2104-2109 then compares their ratio.  Slots with
-    ``active[b] == 0`` take no part.
+    ``active[b] == 0`` take no part.  ``k`` is the global budget or one budget per row (this
+    build's per-row extension: row b then adds ``min(page_count, k[b])``).
     """
+    per_row = not isinstance(k, (int, float))
     full_total = subset_total = 0
     for b in range(len(cachelens)):
         if int(active[b]) == 0:
             continue
         pc = (int(cachelens[b]) + 1) // page_size + 1
+        kb = max(int(k[b]) if per_row else int(k), 0)
         full_total += pc
-        subset_total += min(pc, int(k))
+        subset_total += min(pc, kb)
     return use_subset_decision(full_total, subset_total, compression_ratio, enable_selective_cache)
 
 

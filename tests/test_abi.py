@@ -49,7 +49,7 @@ def test_no_undeclared_exports(lib):
 
 
 def test_queries_without_gpu(lib):
-    assert lib.delta_abi_version() == 200
+    assert lib.delta_abi_version() == 201
     assert lib.delta_last_error() == b""
     # split heuristic: deterministic, >= 1; the larger of the attention and the dump plans.
     # Page-major splits are sized for 16-wave blocks (Hkv heads x R waves): up to 4096 waves in

@@ -19,7 +19,7 @@ def make_engine(selective=True, graph=False, B=3, max_len=512, full_layers=(0, 1
                 n_layer=None, **backend_kw):
     from delta_amd.backend import LMBackend
     eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=graph, **backend_kw)
-    eng.load_model("random:tiny-test", seed=1)
+    eng.load_model("random:tiny-test", seed=1, **({} if n_layer is None else {"n_layer": n_layer}))
     cfg = eng.model.config
     cfg.enable_selective_cache = selective
     cfg.full_cache_layers = list(full_layers)
@@ -543,3 +543,291 @@ def test_config3_llama3_8b_engine_step_matches_oracle():
     ops.set_active_backend(None)
     del eng
     torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------------ several planner layers
+# The reference's speed recipe makes several planners per step (run_reasoni_speed_compare.sh:
+# full layers 0 1 2 14 22 -> planners 2, 14, 22; model.py:177-196): each one rewrites the subset
+# CSR, which the subset layers after it read.  Full layers (0, 1, 3) of a 6-layer model give the
+# roles full / plan / subset / plan / subset / subset.
+MULTI_ROLES = ["full", "plan", "subset", "plan", "subset", "subset"]
+SCALE = 1 / 128 ** 0.5
+
+
+def _spy_planner_selections(eng):
+    """Wrap ``attn_plan`` so each planner layer's selection (the subset CSR right after the
+    layer) is copied as it is made; eager steps only."""
+    taken = []
+    orig = eng.attn_plan
+    B = eng.batch_size
+
+    def spy(q, kv_cache, append=None):
+        o = orig(q, kv_cache, append=append)
+        sel = eng.page_selector
+        ip = sel.paged_subset_kv_indptr[:B + 1].cpu()
+        taken.append((ip, sel.paged_subset_kv_indices[:int(ip[-1])].cpu()))
+        return o
+
+    eng.attn_plan = spy
+    return taken
+
+
+def _oracle_chain_selection(q, cache, ip, ind, last, k, L):
+    """The oracle's own chain for one planner layer: fp64 logits rounded to fp32, fp64
+    del3_legacy_softmax scores, v2 selection (backend.py:887-904, page_selector_v2.py:113-188)."""
+    counts = ip[1:] - ip[:-1]
+    mp = int(counts.max())
+    bt = O.block_table_from_csr(ip, ind, mp)
+    x = O.dump_logits(q, cache, ip, ind, last, SCALE, mp * 16)
+    s = O.legacy_softmax_page_scores(x, q.shape[0], mp, compute_dtype=torch.float64)
+    want_i, want_p = O.select_pages(s.float(), counts, bt, k, L)
+    return want_i, want_p, s, bt
+
+
+@pytest.mark.parametrize("B,on_chip", [(5, False), (128, True)])
+def test_multi_planner_step_matches_oracle(B, on_chip):
+    """One eager decode step with two planner layers: each planner's selection equals the
+    oracle's chain from that layer's own rotated q and cache, bit for bit; each subset layer
+    attends the selection of the planner before it (layer 2 planner 1's, layers 4 and 5 planner
+    3's), within the attention tolerance; the two selections differ, so the second one is what
+    layers 4 and 5 read.  Both planner routes: the logits dump (B = 5) and logits on chip (B =
+    128: 256 (row, kv head) blocks, with two idle slots)."""
+    eng = make_engine(B=B, max_len=512, k=6, L=2, full_layers=(0, 1, 3), n_layer=6)
+    assert eng.layer_roles == MULTI_ROLES
+    assert eng._plan_on_chip() == on_chip
+    lens = [20 + (97 * i) % 420 for i in range(B)]
+    eng.prepare_synthetic_decode(lens, decode_budget=16, seed=31)
+    if B > 8:
+        eng._release_slot(3)
+        eng._release_slot(64)
+    for layer in eng.model.layers:
+        layer.attention.record = []
+    taken = _spy_planner_selections(eng)
+    eng.decode_steps(1, use_graph=False)
+    torch.cuda.synchronize()
+    assert len(taken) == 2 and int(eng.use_subset_flag) == 1
+    ip, ind, last, _ = _csr(eng)
+    rec = [l.attention.record[0] for l in eng.model.layers]
+    caches = [l.attention.kv_cache.kv_cache.cpu() for l in eng.model.layers]
+    for li in range(6):
+        if MULTI_ROLES[li] in ("full", "plan"):
+            ref, _ = O.paged_decode_attention(rec[li][0].cpu(), caches[li], ip, ind, last, SCALE)
+            assert_close(rec[li][1], ref, f"layer {li} ({MULTI_ROLES[li]})")
+    for t, li in enumerate((1, 3)):
+        want_i, want_p, s, bt = _oracle_chain_selection(rec[li][0].cpu(), caches[li], ip, ind, last, eng.k_eff, eng.L)
+        got_p, got_i = taken[t]
+        assert got_p.tolist() == want_p.tolist(), f"planner layer {li}: indptr"
+        if got_i.tolist() != want_i.tolist():
+            keys = O.prepare_scores(s.float(), ip[1:] - ip[:-1], eng.L)
+            msg = []
+            for b in range(B):
+                a = set(got_i[int(got_p[b]):int(got_p[b + 1])].tolist())
+                r = set(want_i[int(want_p[b]):int(want_p[b + 1])].tolist())
+                if a != r:
+                    thr = sorted(keys[b].tolist(), reverse=True)[eng.k_eff - 1]
+                    gaps = [abs(float(keys[b, bt[b].tolist().index(p)]) - thr) for p in a ^ r]
+                    msg.append(f"row {b} gap {max(gaps):.3e} (k-th key {thr:.6e})")
+            raise AssertionError(f"planner layer {li}: selection differs from the oracle chain: " + "; ".join(msg))
+    assert not torch.equal(taken[0][1], taken[1][1]), "the two planners chose the same pages"
+    for li, t in ((2, 0), (4, 1), (5, 1)):
+        sp, si = taken[t]
+        ref, _ = O.paged_decode_attention(rec[li][0].cpu(), caches[li], sp, si, last, SCALE)
+        assert_close(rec[li][1], ref, f"layer {li} (subset after planner {(1, 3)[t]})")
+    # what the step leaves in the subset CSR is the last planner's selection
+    sel = eng.page_selector
+    assert torch.equal(sel.paged_subset_kv_indptr[:B + 1].cpu(), taken[1][0])
+    assert torch.equal(sel.paged_subset_kv_indices[:int(taken[1][0][-1])].cpu(), taken[1][1])
+
+
+@pytest.mark.parametrize("ratio", [1.0, 1e9])
+def test_multi_planner_graph_replays_match_eager(ratio):
+    """Two planner layers inside one captured step: 12 graph replays, with eager work between
+    them, equal 12 eager steps from the same state bit for bit -- tokens, the subset CSR the
+    step leaves, and every layer's cache (the appended K/V).  With the gate off (ratio 1e9) the
+    planners select nothing, the subset CSR is the full CSR and the subset layers attend every
+    page, as the reference's unplanned step does (backend.py:560-580, 2104-2109)."""
+    eng = make_engine(graph=True, B=4, k=6, L=2, full_layers=(0, 1, 3), n_layer=6, ratio=ratio)
+    assert eng.layer_roles == MULTI_ROLES
+    eng.prepare_synthetic_decode([15, 16, 31, 200], decode_budget=40, seed=32)
+    snap = _snapshot(eng)
+    B = eng.batch_size
+    sel = eng.page_selector
+
+    def subset_csr():
+        ip = sel.paged_subset_kv_indptr[:B + 1].clone()
+        return ip, sel.paged_subset_kv_indices[:int(ip[-1])].clone()
+
+    eager = []
+    for _ in range(12):
+        tok = eng.decode_steps(1, use_graph=False).clone()
+        eager.append((tok, *subset_csr()))
+    eager_caches = [l.attention.kv_cache.kv_cache.clone() for l in eng.model.layers]
+    assert int(eng.use_subset_flag) == (1 if ratio == 1.0 else 0)
+    if ratio != 1.0:
+        ip, ind, _, _ = _csr(eng)
+        assert torch.equal(eager[-1][1].cpu(), ip) and torch.equal(eager[-1][2].cpu(), ind)
+    _restore(eng, snap)
+    for i in range(12):
+        tok = eng.decode_steps(1, use_graph=True).clone()
+        a = torch.randn(256, 256, device=DEV)
+        (a @ a).sum().item()
+        ip, ind = subset_csr()
+        assert torch.equal(tok, eager[i][0]), f"replay {i}: tokens differ from the eager step"
+        assert torch.equal(ip, eager[i][1]) and torch.equal(ind, eager[i][2]), f"replay {i}: subset CSR differs"
+    assert eng._decode_graph_failed is None and eng._decode_graph_stats["replays"] == 12
+    for li, (l, c) in enumerate(zip(eng.model.layers, eager_caches)):
+        assert torch.equal(l.attention.kv_cache.kv_cache, c), f"layer {li} cache differs"
+    if ratio != 1.0:  # gate off: every subset layer attends the full CSR
+        for layer in eng.model.layers:
+            layer.attention.record = []
+        eng.decode_steps(1, use_graph=False)
+        torch.cuda.synchronize()
+        ip, ind, last, _ = _csr(eng)
+        for li in (2, 4, 5):
+            q, o = eng.model.layers[li].attention.record[0]
+            ref, _ = O.paged_decode_attention(q.cpu(), eng.model.layers[li].attention.kv_cache.kv_cache.cpu(), ip,
+                                              ind, last, SCALE)
+            assert_close(o, ref, f"layer {li} with the gate off")
+
+
+# ------------------------------------------------------------------ aux surface
+def test_delta_impl_profile_sections():
+    """delta_impl_profile (backend.py:1570-1585, call sites 537-578, 789-853): every eager decode
+    step times its named device sections with HIP events; a replayed step is timed whole (its
+    parts cannot be split) and the capture's warm-up bodies are not counted.  Two planners and
+    three subset layers per step (full layers 0, 1, 3 of 6)."""
+    eng = make_engine(B=5, k=6, L=2, full_layers=(0, 1, 3), n_layer=6, graph=True, delta_impl_profile=True)
+    eng.prepare_synthetic_decode([40, 150, 260, 370, 480], decode_budget=16, seed=51)
+    eng.decode_steps(2, use_graph=False)
+    prof = eng.delta_impl_profile_summary()
+    want = {"delta_decode_step_eager": 2, "delta_decode_page_info": 2, "delta_full_attention": 2,
+            "delta_planner_attention_dump": 4, "delta_page_score": 4, "delta_page_select": 4,
+            "delta_replan_total": 4, "delta_subset_attention": 6}
+    assert {k: v["count"] for k, v in prof.items()} == want
+    assert all(v["total_ms"] > 0 for v in prof.values())
+    assert prof["delta_replan_total"]["total_ms"] >= prof["delta_page_select"]["total_ms"]
+    parts = sum(prof[n]["total_ms"] for n in ("delta_decode_page_info", "delta_full_attention",
+                                              "delta_planner_attention_dump", "delta_replan_total",
+                                              "delta_subset_attention"))
+    assert parts <= prof["delta_decode_step_eager"]["total_ms"]
+    eng.decode_steps(3, use_graph=True)
+    prof = eng.delta_impl_profile_summary()
+    assert prof["delta_decode_step_graph"]["count"] == 3
+    assert prof["delta_subset_attention"]["count"] == 6 and prof["delta_decode_step_eager"]["count"] == 2
+    # the on-chip planner (B * Hkv >= 256) times attention and scores as one section
+    eng2 = make_engine(B=128, k=6, L=2, delta_impl_profile=True)
+    eng2.prepare_synthetic_decode([30 + i for i in range(128)], decode_budget=16, seed=52)
+    eng2.decode_steps(1, use_graph=False)
+    prof2 = eng2.delta_impl_profile_summary()
+    assert prof2["delta_planner_attention_scores"]["count"] == 1 and "delta_page_score" not in prof2
+    assert prof2["delta_page_select"]["count"] == 1
+
+
+def test_final_stats_report_graph_fallbacks_and_profile(tmp_path, monkeypatch, capsys):
+    """_print_final_stats prints and saves what the reference does (backend.py:2199-2238,
+    2251-2275): captures, replays, capture time, fallback reasons and capture errors, and the
+    delta_impl_profile table; here the capture fails, so every decode step falls back to eager
+    and says so."""
+    import json
+    monkeypatch.setenv("DELTA_STEP_LOG_DIR", str(tmp_path))
+    eng = make_engine(B=2, max_len=256, k=4, graph=True, delta_impl_profile=True)
+
+    def refuse():
+        raise RuntimeError("capture refused")
+
+    eng._capture_decode_graph = refuse
+    eng.add_requests([torch.tensor([1, 2, 3, 4]), torch.tensor([5, 6, 7])], [40, 30], [])
+    eng.run_scheduler_loop()
+    out = capsys.readouterr().out
+    for text in ("HIP Graph Decode:", "capture failures: 1", "fallback reasons", "capture errors",
+                 "DELTA Implementation Profile:", "delta_decode_step_eager", "delta_prefill_step"):
+        assert text in out, text
+    meta = json.loads(next(tmp_path.glob("step_timings_*.json")).read_text())["meta"]
+    assert meta["cuda_graph_decode_fallback_reasons"]["capture_failed"] == 1
+    assert meta["cuda_graph_decode_fallback_reasons"]["no_graph_eager_step"] > 0
+    assert "capture refused" in meta["cuda_graph_decode_capture_errors"]["decode_step"]
+    assert meta["delta_impl_profile"] is True
+    assert meta["delta_impl_profile_counts"]["delta_prefill_step"] >= 1
+    assert meta["delta_impl_profile_counts"]["delta_decode_step_eager"] > 0
+    assert set(meta["delta_impl_profile_ms"]) == set(meta["delta_impl_profile_counts"])
+    # a healthy graph engine reports its capture time
+    eng2 = make_engine(B=2, max_len=256, k=4, graph=True)
+    eng2.add_requests([torch.tensor([1, 2, 3, 4])], [30], [])
+    eng2.run_scheduler_loop()
+    out = capsys.readouterr().out
+    assert "capture time by graph" in out and eng2._decode_graph_capture_time_s["decode_step"] > 0
+
+
+# ------------------------------------------------------------------ per-row budgets
+def test_per_row_budgets_through_the_engine():
+    """set_subset_budgets (an extension: the reference's k is global, page_selector_v2.py:136-164):
+    each row keeps min(pages, budget) pages.  One eager step with two planners is checked row by
+    row against the oracle chain with each row's own k; the gate counts the per-row totals
+    (O.decode_step_gate); then 10 graph replays equal 10 eager steps bit for bit, with the
+    budgets changed between steps 4 and 5 (values only: the captured step reads them live)."""
+    B = 6
+    eng = make_engine(graph=True, B=B, k=8, L=2, full_layers=(0, 1, 3), n_layer=6, ratio=1.0)
+    lens = [30, 120, 210, 300, 390, 470]
+    eng.prepare_synthetic_decode(lens, decode_budget=24, seed=41)
+    budgets = [1, 8, 3, 5, 8, 2]
+    with pytest.raises(ValueError, match="per-row budgets must lie in"):
+        eng.set_subset_budgets([0, 8, 3, 5, 8, 2])
+    with pytest.raises(ValueError, match="per-row budgets must lie in"):
+        eng.set_subset_budgets([9, 8, 3, 5, 8, 2])
+    eng.set_subset_budgets(budgets)
+    for layer in eng.model.layers:
+        layer.attention.record = []
+    taken = _spy_planner_selections(eng)
+    cl0 = eng.cachelens.cpu().tolist()
+    eng.decode_steps(1, use_graph=False)
+    torch.cuda.synchronize()
+    assert int(eng.use_subset_flag) == int(O.decode_step_gate(cl0, [1] * B, budgets, 1.0))
+    ip, ind, last, _ = _csr(eng)
+    counts = ip[1:] - ip[:-1]
+    rec = [l.attention.record[0] for l in eng.model.layers]
+    caches = [l.attention.kv_cache.kv_cache.cpu() for l in eng.model.layers]
+    for t, li in enumerate((1, 3)):
+        got_p, got_i = taken[t]
+        assert (got_p[1:] - got_p[:-1]).tolist() == [min(int(c), kb) for c, kb in zip(counts, budgets)]
+        q = rec[li][0].cpu()
+        bt = O.block_table_from_csr(ip, ind, int(counts.max()))
+        x = O.dump_logits(q, caches[li], ip, ind, last, SCALE, int(counts.max()) * 16)
+        s = O.legacy_softmax_page_scores(x, B, int(counts.max()), compute_dtype=torch.float64).float()
+        for b in range(B):
+            wi, _ = O.select_pages(s[b:b + 1], counts[b:b + 1], bt[b:b + 1], budgets[b], eng.L)
+            assert got_i[int(got_p[b]):int(got_p[b + 1])].tolist() == wi.tolist(), f"planner {li} row {b}"
+    for li, t in ((2, 0), (4, 1), (5, 1)):
+        sp, si = taken[t]
+        ref, _ = O.paged_decode_attention(rec[li][0].cpu(), caches[li], sp, si, last, SCALE)
+        assert_close(rec[li][1], ref, f"layer {li} over per-row budgets")
+    eng.attn_plan = type(eng).attn_plan.__get__(eng)  # drop the spy
+    for layer in eng.model.layers:
+        layer.attention.record = None
+    # graph replays == eager steps, budgets changed mid-way
+    snap = _snapshot(eng)
+    sel = eng.page_selector
+    budgets2 = [8, 2, 2, 7, 1, 4]
+
+    def run(use_graph):
+        eng.set_subset_budgets(budgets)
+        outs = []
+        for i in range(10):
+            if i == 5:
+                eng.set_subset_budgets(budgets2)
+            tok = eng.decode_steps(1, use_graph=use_graph).clone()
+            p = sel.paged_subset_kv_indptr[:B + 1].clone()
+            outs.append((tok, p, sel.paged_subset_kv_indices[:int(p[-1])].clone()))
+        return outs, [l.attention.kv_cache.kv_cache.clone() for l in eng.model.layers]
+
+    eager, eager_caches = run(False)
+    _restore(eng, snap)
+    replay, replay_caches = run(True)
+    assert eng._decode_graph_stats["captures"] == 1 and eng._decode_graph_stats["replays"] == 10
+    for i, (a, b) in enumerate(zip(eager, replay)):
+        assert all(torch.equal(x, y) for x, y in zip(a, b)), f"step {i}: replay differs from eager"
+    last_counts = (eager[-1][1][1:] - eager[-1][1][:-1]).tolist()
+    assert all(c <= kb for c, kb in zip(last_counts, budgets2))
+    for x, y in zip(eager_caches, replay_caches):
+        assert torch.equal(x, y)
+    eng.set_subset_budgets(None)
+    assert not eng._per_row_budgets and eng._decode_graph is None

@@ -448,6 +448,39 @@ def test_decode_page_info_gate_counts_active_rows(active_rows):
             assert sub_p.cpu().tolist() == [0] + torch.cumsum(torch.tensor(sc), 0).tolist()
 
 
+def test_decode_page_info_per_row_budgets():
+    """k_per_row (an extension of the reference's global k): row b's subset is its last
+    min(pages_b, k_b) pages and the gate sums min(pages_b, k_b) over the active rows, as
+    O.decode_page_info / O.decode_step_gate count them; budgets clamp to [0, pages_per_slot]
+    as the selector clamps them; idle rows keep their entries but leave the totals."""
+    gen = torch.Generator().manual_seed(10)
+    B, pps = 6, 40
+    cachelens = torch.tensor([15, 40, 300, 95, 0, 500], dtype=torch.int32)
+    kpr = torch.tensor([1, 8, 4, 0, 3, 99], dtype=torch.int32)     # 99 clamps to pages_per_slot
+    active = torch.tensor([1, 1, 1, 1, 0, 1], dtype=torch.int32)
+    slot_bt = torch.randint(0, 1 << 20, (B, pps), generator=gen, dtype=torch.int32)
+    ind = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    ip = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    last = torch.zeros(B, dtype=torch.int32, device=DEV)
+    sub_i = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    sub_p = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    flag = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    pc, lp, sc, ss = O.decode_page_info(cachelens, pps, torch.clamp(kpr, max=pps))
+    for ratio in (1.0, 1.57, 1.58, 1e9):  # active totals 63 / 40 = 1.575
+        K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, 7, ratio, True, ip, ind, last, None, sub_i,
+                           sub_p, flag, active=active.to(DEV), k_per_row=kpr.to(DEV))
+        torch.cuda.synchronize()
+        want = O.decode_step_gate(cachelens.tolist(), active.tolist(), torch.clamp(kpr, max=pps).tolist(), ratio)
+        assert int(flag) == int(want), ratio
+        assert last.cpu().tolist() == lp.tolist()
+        cnt = sc.tolist() if want else pc.tolist()
+        start = ss.tolist() if want else [0] * B
+        sp = [0] + torch.cumsum(torch.tensor(cnt), 0).tolist()
+        assert sub_p.cpu().tolist() == sp, ratio
+        for b in range(B):
+            assert sub_i[sp[b]:sp[b + 1]].cpu().tolist() == slot_bt[b, start[b]:int(pc[b])].tolist(), (ratio, b)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_append_kv(dtype):
     c = make_case(batch=3, hq=8, hkv=4, kv_lens=[17, 32, 50], seed=9, dtype=dtype, trailing_empty_page=True)

@@ -81,6 +81,26 @@ def test_decode_step_gate_counts_active_rows_only():
     assert not O.decode_step_gate([14], [1], 1, 1.5)         # 15 tokens -> 1 page
 
 
+def test_per_row_budgets_in_page_info_and_gate():
+    """Per-row budgets (this build's extension): each row's subset count is min(pages, k_b).
+    Hand-counted: rows of 15, 40, 300 and 95 cached tokens hold 2, 3, 19 and 7 pages after the
+    decode token (kv_len // 16 + 1); budgets 1, 8, 4, 0 give subset counts 1, 3, 4, 0 and
+    starts 1, 0, 15, 7.  Gate: 31 pages over 8 subset pages = 3.875."""
+    cl = torch.tensor([15, 40, 300, 95], dtype=torch.int32)
+    pc, last, sc, ss = O.decode_page_info(cl, 100, k=torch.tensor([1, 8, 4, 0]))
+    assert pc.tolist() == [2, 3, 19, 7] and last.tolist() == [0, 9, 13, 0]
+    assert sc.tolist() == [1, 3, 4, 0] and ss.tolist() == [1, 0, 15, 7]
+    assert O.decode_page_info(cl, 100, k=torch.tensor([-5, 8, 4, 0]))[2].tolist() == [0, 3, 4, 0]
+    act = [1, 1, 1, 1]
+    assert O.decode_step_gate(cl.tolist(), act, [1, 8, 4, 0], 3.87)
+    assert not O.decode_step_gate(cl.tolist(), act, [1, 8, 4, 0], 3.875)
+    # row 2 idle: 12 pages over 4 = 3.0
+    assert O.decode_step_gate(cl.tolist(), [1, 1, 0, 1], [1, 8, 4, 0], 2.99)
+    assert not O.decode_step_gate(cl.tolist(), [1, 1, 0, 1], [1, 8, 4, 0], 3.0)
+    # a global budget equal for every row matches the per-row form
+    assert O.decode_step_gate(cl.tolist(), act, [5] * 4, 2.0) == O.decode_step_gate(cl.tolist(), act, 5, 2.0)
+
+
 # ---------------------------------------------------------------- dump logits
 
 def test_dump_logits_bruteforce():

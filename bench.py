@@ -629,6 +629,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=60)
     ap.add_argument("--configs-only", action="store_true",
                     help="only the kernel-level measurements at BASELINE configs 2, 4 and 5 (for rocprofv3 runs)")
+    ap.add_argument("--configs", default="2,4,5",
+                    help="which of BASELINE configs 2, 4, 5 --configs-only measures (comma separated)")
     ap.add_argument("--cpu-baseline-only", action="store_true",
                     help="only the CPU baseline (runs without a GPU)")
     ap.add_argument("--kernels-only", action="store_true",
@@ -662,7 +664,7 @@ def main():
         return
     if args.configs_only:
         out = {}
-        for cfg in (2, 4, 5):
+        for cfg in sorted({int(x) for x in args.configs.split(",")} & {2, 4, 5}):
             out[f"config{cfg}"] = config_kernels(torch, cfg, reps=args.kernel_reps // 4 or 1)
             for k, v in out[f"config{cfg}"].items():
                 if isinstance(v, dict):

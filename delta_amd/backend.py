@@ -513,6 +513,12 @@ class LMBackend:
         self._host_active = [int(x) for x in self.active.tolist()]
 
     def _check_decode_budget(self, n: int):
+        if self.enable_delta_debug_fast_decode_page_info_parity:
+            # the guard trusts the host mirror; in debug mode check it against the device first
+            lens, act = self.cachelens.tolist(), self.active.tolist()
+            if lens != self._host_lens or act != self._host_active:
+                raise RuntimeError("host copy of cachelens/active differs from the device: call sync_host_lens() "
+                                   "after writing them directly")
         for b in range(self.batch_size):
             if self._host_active[b]:
                 need = (self._host_lens[b] + n) // PAGE_SIZE + 1

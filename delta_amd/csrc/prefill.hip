@@ -10,8 +10,11 @@
 // (token, q head) pairs of TW = 32 / G tokens (rows past TW * G idle when G does not divide
 // 32), with its q in registers.  The block sweeps the row's kv tokens 64 at a time (four pages,
 // two 32-token sub-tiles) up to its last token's position: each step's K and V (16 KiB each for
-// one head) are loaded once per block, 16 bytes per thread, into double-buffered padded LDS
-// tiles (the next step in flight in registers) and read by every wave.  Per wave and sub-tile:
+// one head) are loaded once per block, 16 bytes per thread, into padded LDS tiles (three
+// buffers; the next step in flight in registers) and read by every wave.  Waves 0-3 run each
+// step whole; waves 4-7, the second wave of each SIMD, run half a step behind (P.V of the
+// previous step, then S and softmax of this one, the previous step's V still in its buffer), so
+// the two waves of a SIMD are not both in their softmax at once.  Per wave and sub-tile:
 //   S^T = K Q^T : 8 v_mfma_f32_32x32x16 over d, A = the tile's K rows from LDS
 //         (lane%32 = kv token, d in 16 ks + 8 (lane / 32) + [0, 8)), B = the wave's q (same d
 //         split, n = lane%32 = query row); D leaves lane l with its row n = l%32 and the 16 kv
@@ -45,6 +48,7 @@ constexpr int kKvStep = 32 * kSub;  // kv tokens per step
 constexpr int kPgStep = kKvStep / 16;  // pages per step
 constexpr int kRowP = 136;      // padded K tile row (elements): conflict-free 16-byte row reads
 constexpr int kRowPV = 160;     // padded V tile row (elements), read transposed
+constexpr int kBufs = 3;        // LDS step buffers (late waves read a step after the next barrier)
 
 struct PrefillArgs {
   const uint16_t *q;
@@ -120,7 +124,7 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   constexpr int kTile = kKvStep * kRowP;      // the K tile (elements); the V tile follows
   constexpr int kTileV = kKvStep * kRowPV;
   // Two step buffers, each K then V (padded rows), shared by the block's waves.
-  __shared__ uint16_t tiles[2][kTile + kTileV];
+  __shared__ uint16_t tiles[kBufs][kTile + kTileV];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hl = lane >> 5, n = lane & 31;
@@ -214,13 +218,13 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
                          : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto stage = [&](int j) {  // the ring (step j) into tiles[j & 1]; V rows past kv_len as zeros
+  auto stage = [&](int j) {  // the ring (step j) into tiles[j % kBufs]; V rows past kv_len as zeros
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
       const int ci = threadIdx.x + r * kPW * 64;
       const int which = ci / (kKvStep * 16), row = (ci >> 4) % kKvStep, c16 = ci & 15;
       const bool keep = which == 0 || j * kKvStep + row < kv_len;
-      st128(&tiles[j & 1][(which ? kTile + row * kRowPV : row * kRowP) + 8 * c16], keep ? ring[r] : u32x4{0u, 0u, 0u, 0u});
+      st128(&tiles[j % kBufs][(which ? kTile + row * kRowPV : row * kRowP) + 8 * c16], keep ? ring[r] : u32x4{0u, 0u, 0u, 0u});
     }
   };
   if (nsteps > 0) {
@@ -241,117 +245,137 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   const int q16 = lane >> 4, t16 = lane & 15;
   const int vtr_off = kTile + (4 * hl + (t16 >> 2)) * kRowPV + 16 * (q16 & 1) + 4 * (t16 & 3);
 
-  for (int j = 0; j < nsteps; ++j) {
-    __syncthreads();  // step j is in tiles[j & 1]; tiles[(j + 1) & 1] is free
-    if (kPgStep * j >= cbase + 64) {  // the id window moves on
+  // One step for the wave: S^T = K Q^T, the online softmax (accumulators rescaled when the
+  // reference maximum moves) and P^T packed into pc.
+  auto score_step = [&](int j, const uint16_t *tk, u32x4 (&pc)[2 * kSub]) {
+    f32x16 S[kSub];
+#pragma unroll
+    for (int sb = 0; sb < kSub; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S[sb][i] = 0.f;
+    // K fragments one ks ahead of the MFMAs that use them.
+    auto kfrag = [&](int sb, int ks) { return *reinterpret_cast<const u32x4 *>(tk + (32 * sb + n) * kRowP + 16 * ks + 8 * hl); };
+    u32x4 kc[kSub];
+#pragma unroll
+    for (int sb = 0; sb < kSub; ++sb) kc[sb] = kfrag(sb, 0);
+    // Raised wave priority over each MFMA run: of the SIMD's two waves, the one with MFMAs
+    // to issue goes first, which pushes the other into its softmax meanwhile (~1 %).
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      u32x4 kn[kSub];
+      if (ks < 7) {
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb) kn[sb] = kfrag(sb, ks + 1);
+      }
+#pragma unroll
+      for (int sb = 0; sb < kSub; ++sb) S[sb] = MF::run(kc[sb], qf[ks], S[sb]);
+      if (ks < 7) {
+#pragma unroll
+        for (int sb = 0; sb < kSub; ++sb) kc[sb] = kn[sb];
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    // Masks only where the step crosses the wave's first diagonal, kv_len, or a bad page.
+    const int kv0 = j * kKvStep;
+    const int poff = kPgStep * j - cbase;  // the step's pages: bits poff .. poff + kPgStep - 1
+    const bool pages_ok = ((bad >> poff) & ((1ull << kPgStep) - 1)) == 0;
+    const bool full = kv0 + kKvStep - 1 <= wpos0 && kv0 + kKvStep <= kv_len && pages_ok;
+    // Row maxima on the raw scores (the scale is positive, so it commutes with max), then
+    // x = S * scale - m as one fma.  m is the row's reference maximum: it moves only when a
+    // score exceeds it by more than 8 (a factor of 2^8), so the exponentials stay <= 256 and the
+    // accumulators are rescaled only on those steps.
+    constexpr int NX = 16 * kSub;
+    float x[NX];
+    float pm = -INFINITY;
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < NX; ++i) {
+        x[i] = S[i >> 4][i & 15];
+        pm = fmaxf(pm, x[i]);
+      }
+    } else {
+      bool pg_ok[kPgStep];
+#pragma unroll
+      for (int p = 0; p < kPgStep; ++p) pg_ok[p] = ((bad >> (poff + p)) & 1ull) == 0;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) {
+        const int mm = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * hl + (i & 3);
+        const int tk_i = kv0 + mm;
+        x[i] = (row_ok && pg_ok[mm >> 4] && tk_i <= qpos && tk_i < kv_len) ? S[i >> 4][i & 15] : -INFINITY;
+        pm = fmaxf(pm, x[i]);
+      }
+    }
+    const float smax = halves_max(pm) * scale2;
+    float alpha = 1.f;
+    if (smax > m + 8.f) {  // also the first finite score of the row (m = -inf)
+      alpha = fast_exp2(m - smax);
+      m = smax;
+    }
+    const float nm = m == -INFINITY ? 0.f : -m;
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      x[i] = fast_exp2(fmaf(x[i], scale2, nm));
+      ps += x[i];
+    }
+    l = l * alpha + ps;  // this half's tokens; the halves are summed once at the end
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+    }
+    // P^T chunks: values 8c .. 8c + 7 of this lane, rounded to the KV dtype.
+#pragma unroll
+    for (int cc = 0; cc < 2 * kSub; ++cc)
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        pc[cc][w] = pack2<DT>(x[8 * cc + 2 * w], x[8 * cc + 2 * w + 1]);
+  };
+  // O^T += V^T P^T of a step whose P^T is in pc.
+  auto pv_step = [&](const uint16_t *tk, const u32x4 (&pc)[2 * kSub]) {
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int cc = 0; cc < 2 * kSub; ++cc) {
+        const uint16_t *rd = tk + vtr_off + 16 * cc * kRowPV + 32 * dt;
+        const ps4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)rd);
+        const ps4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 8 * kRowPV));
+        u32x4 va;
+        va[0] = (uint32_t)(uint16_t)v0[0] | ((uint32_t)(uint16_t)v0[1] << 16);
+        va[1] = (uint32_t)(uint16_t)v0[2] | ((uint32_t)(uint16_t)v0[3] << 16);
+        va[2] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
+        va[3] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
+        acc[dt] = MF::run(va, pc[cc], acc[dt]);
+      }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // Waves 0-3 (one per SIMD) run each step whole; waves 4-7, the SIMDs' second waves, run half
+  // a step behind: P.V of the previous step first, then S and the softmax of this one.  So on
+  // each SIMD one wave's softmax runs while the other wave's MFMAs do (P.V of one under the
+  // other's softmax, S of one under the other's softmax), not both softmaxes at once.  A step's
+  // tiles stay in LDS for one more step (three buffers): the late waves read step j - 1 after
+  // the barrier of step j.
+  const bool late = wave >= kPW / 2;
+  u32x4 pcar[2 * kSub];
+  for (int j = 0; j <= nsteps; ++j) {
+    __syncthreads();  // step j is in tiles[j % 3]; tiles[(j + 1) % 3] is free
+    if (j < nsteps && kPgStep * j >= cbase + 64) {  // the id window moves on
       cbase += 64;
       ids = ids_next;
       bad = bad_of(ids, cbase);
       ids_next = cbase + 64 < npages ? load_ids(cbase + 64) : -1;
     }
-    if (j < wsteps) {
-      const uint16_t *tk = &tiles[j & 1][0];
-      f32x16 S[kSub];
-#pragma unroll
-      for (int sb = 0; sb < kSub; ++sb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) S[sb][i] = 0.f;
-      // K fragments one ks ahead of the MFMAs that use them.
-      auto kfrag = [&](int sb, int ks) { return *reinterpret_cast<const u32x4 *>(tk + (32 * sb + n) * kRowP + 16 * ks + 8 * hl); };
-      u32x4 kc[kSub];
-#pragma unroll
-      for (int sb = 0; sb < kSub; ++sb) kc[sb] = kfrag(sb, 0);
-      // Raised wave priority over each MFMA run: of the SIMD's two waves, the one with MFMAs
-      // to issue goes first, which pushes the other into its softmax meanwhile (~1 %).
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        u32x4 kn[kSub];
-        if (ks < 7) {
-#pragma unroll
-          for (int sb = 0; sb < kSub; ++sb) kn[sb] = kfrag(sb, ks + 1);
-        }
-#pragma unroll
-        for (int sb = 0; sb < kSub; ++sb) S[sb] = MF::run(kc[sb], qf[ks], S[sb]);
-        if (ks < 7) {
-#pragma unroll
-          for (int sb = 0; sb < kSub; ++sb) kc[sb] = kn[sb];
-        }
-      }
-      __builtin_amdgcn_s_setprio(0);
-      // Masks only where the step crosses the wave's first diagonal, kv_len, or a bad page.
-      const int kv0 = j * kKvStep;
-      const int poff = kPgStep * j - cbase;  // the step's pages: bits poff .. poff + kPgStep - 1
-      const bool pages_ok = ((bad >> poff) & ((1ull << kPgStep) - 1)) == 0;
-      const bool full = kv0 + kKvStep - 1 <= wpos0 && kv0 + kKvStep <= kv_len && pages_ok;
-      // Row maxima on the raw scores (the scale is positive, so it commutes with max), then
-      // x = S * scale - m as one fma.  m is the row's reference maximum: it moves only when a
-      // score exceeds it by more than 8 (a factor of 2^8), so the exponentials stay <= 256 and the
-      // accumulators are rescaled only on those steps.
-      constexpr int NX = 16 * kSub;
-      float x[NX];
-      float pm = -INFINITY;
-      if (full) {
-#pragma unroll
-        for (int i = 0; i < NX; ++i) {
-          x[i] = S[i >> 4][i & 15];
-          pm = fmaxf(pm, x[i]);
-        }
-      } else {
-        bool pg_ok[kPgStep];
-#pragma unroll
-        for (int p = 0; p < kPgStep; ++p) pg_ok[p] = ((bad >> (poff + p)) & 1ull) == 0;
-#pragma unroll
-        for (int i = 0; i < NX; ++i) {
-          const int mm = 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * hl + (i & 3);
-          const int tk_i = kv0 + mm;
-          x[i] = (row_ok && pg_ok[mm >> 4] && tk_i <= qpos && tk_i < kv_len) ? S[i >> 4][i & 15] : -INFINITY;
-          pm = fmaxf(pm, x[i]);
-        }
-      }
-      const float smax = halves_max(pm) * scale2;
-      float alpha = 1.f;
-      if (smax > m + 8.f) {  // also the first finite score of the row (m = -inf)
-        alpha = fast_exp2(m - smax);
-        m = smax;
-      }
-      const float nm = m == -INFINITY ? 0.f : -m;
-      float ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < NX; ++i) {
-        x[i] = fast_exp2(fmaf(x[i], scale2, nm));
-        ps += x[i];
-      }
-      l = l * alpha + ps;  // this half's tokens; the halves are summed once at the end
-      if (__ballot(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
-      }
-      // P^T chunks: values 8c .. 8c + 7 of this lane, rounded to the KV dtype.
+    if (late) {
+      if (j >= 1 && j - 1 < wsteps) pv_step(&tiles[(j - 1) % kBufs][0], pcar);
+      if (j < wsteps) score_step(j, &tiles[j % kBufs][0], pcar);
+    } else if (j < wsteps) {
       u32x4 pc[2 * kSub];
-#pragma unroll
-      for (int cc = 0; cc < 2 * kSub; ++cc)
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          pc[cc][w] = pack2<DT>(x[8 * cc + 2 * w], x[8 * cc + 2 * w + 1]);
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int cc = 0; cc < 2 * kSub; ++cc) {
-          const uint16_t *rd = tk + vtr_off + 16 * cc * kRowPV + 32 * dt;
-          const ps4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)rd);
-          const ps4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ps4_t *)(rd + 8 * kRowPV));
-          u32x4 va;
-          va[0] = (uint32_t)(uint16_t)v0[0] | ((uint32_t)(uint16_t)v0[1] << 16);
-          va[1] = (uint32_t)(uint16_t)v0[2] | ((uint32_t)(uint16_t)v0[3] << 16);
-          va[2] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
-          va[3] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
-          acc[dt] = MF::run(va, pc[cc], acc[dt]);
-        }
-      __builtin_amdgcn_s_setprio(0);
+      score_step(j, &tiles[j % kBufs][0], pc);
+      pv_step(&tiles[j % kBufs][0], pc);
     }
     if (j + 1 < nsteps) {
       stage(j + 1);

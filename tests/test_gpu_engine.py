@@ -335,6 +335,13 @@ def test_debug_parity_checks_run_after_eager_and_replayed_steps():
     eng2.sync_host_lens()
     eng2.decode_steps(2, use_graph=False)
     assert int(eng2.use_subset_flag) == 1
+    # in debug mode the decode-budget guard checks its host copy of cachelens against the device
+    with torch.inference_mode():
+        eng2.cachelens[0] += 1
+    with pytest.raises(RuntimeError, match="host copy of cachelens"):
+        eng2.decode_steps(1, use_graph=False)
+    eng2.sync_host_lens()
+    eng2.decode_steps(1, use_graph=False)
 
 
 def test_replay_failure_falls_back_to_eager():

@@ -646,18 +646,20 @@ def test_multi_planner_step_matches_oracle(B, on_chip):
     assert torch.equal(sel.paged_subset_kv_indices[:int(taken[1][0][-1])].cpu(), taken[1][1])
 
 
-@pytest.mark.parametrize("ratio", [1.0, 1e9])
-def test_multi_planner_graph_replays_match_eager(ratio):
+@pytest.mark.parametrize("B,ratio", [(4, 1.0), (4, 1e9), (128, 1.0)])
+def test_multi_planner_graph_replays_match_eager(B, ratio):
     """Two planner layers inside one captured step: 12 graph replays, with eager work between
     them, equal 12 eager steps from the same state bit for bit -- tokens, the subset CSR the
     step leaves, and every layer's cache (the appended K/V).  With the gate off (ratio 1e9) the
     planners select nothing, the subset CSR is the full CSR and the subset layers attend every
-    page, as the reference's unplanned step does (backend.py:560-580, 2104-2109)."""
-    eng = make_engine(graph=True, B=4, k=6, L=2, full_layers=(0, 1, 3), n_layer=6, ratio=ratio)
+    page, as the reference's unplanned step does (backend.py:560-580, 2104-2109).  B = 128 (256
+    (row, kv head) blocks) runs both planners with their logits on chip."""
+    eng = make_engine(graph=True, B=B, k=6, L=2, full_layers=(0, 1, 3), n_layer=6, ratio=ratio)
     assert eng.layer_roles == MULTI_ROLES
-    eng.prepare_synthetic_decode([15, 16, 31, 200], decode_budget=40, seed=32)
+    assert eng._plan_on_chip() == (B == 128)
+    lens = [15, 16, 31, 200] if B == 4 else [10 + (53 * i) % 300 for i in range(B)]
+    eng.prepare_synthetic_decode(lens, decode_budget=40, seed=32)
     snap = _snapshot(eng)
-    B = eng.batch_size
     sel = eng.page_selector
 
     def subset_csr():
@@ -838,3 +840,102 @@ def test_per_row_budgets_through_the_engine():
         assert torch.equal(x, y)
     eng.set_subset_budgets(None)
     assert not eng._per_row_budgets and eng._decode_graph is None
+
+
+def test_speed_recipe_shape_three_planners_match_oracle():
+    """The reference's speed recipe (run_reasoni_speed_compare.sh:16-28) at a 2048-token context:
+    DeepSeek-R1-Distill-Qwen-1.5B shape (28 layers, 12 q / 2 kv heads, qkv bias), B = 64, subset
+    64 pages, L = 8, full layers 0 1 2 14 22, so layers 2, 14 and 22 are planners (model.py:177-
+    196).  One eager step, sampled rows: each planner's selection equals the oracle chain from its
+    own layer's rotated q and cache, bit for bit; the first subset layer after each planner (3,
+    15, 23) and the last layer attend that planner's selection.  Then the same step replayed from
+    a captured graph, from the same state, equals the eager step: tokens, the subset CSR it
+    leaves, the appended K/V of every layer's new token."""
+    import math
+    from delta_amd import ops
+    from delta_amd.backend import LMBackend
+    B, ctx, k, L = 64, 2048, 64, 8
+    scale = 1 / math.sqrt(128)
+    eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=True)
+    eng.load_model("random:DeepSeek-R1-Distill-Qwen-1.5B", seed=0)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = [0, 1, 2, 14, 22]
+    cfg.subset_cache_size = k
+    cfg.compression_ratio = 1.0
+    cfg.L = L
+    eng.setup_caches(max_batch_size=B, max_seq_length=ctx + 64)
+    eng.prepare_synthetic_decode(ctx, decode_budget=32, seed=0)
+    planners = [i for i, r in enumerate(eng.layer_roles) if r == "plan"]
+    assert planners == [2, 14, 22]
+    watch = (2, 3, 14, 15, 22, 23, 27)
+    for i in watch:
+        eng.model.layers[i].attention.record = []
+    taken = _spy_planner_selections(eng)
+    lens0, tok0 = eng.cachelens.clone(), eng.static_tokens.clone()
+    eager_tok = eng.decode_steps(1, use_graph=False).clone()
+    torch.cuda.synchronize()
+    assert len(taken) == 3 and int(eng.use_subset_flag) == 1
+    rec = {i: eng.model.layers[i].attention.record[0] for i in watch}
+    for i in watch:
+        eng.model.layers[i].attention.record = None
+    eng.attn_plan = type(eng).attn_plan.__get__(eng)
+    sel = eng.page_selector
+    full_ip = sel.paged_kv_indptr[:B + 1].cpu()
+    full_ind = sel.paged_kv_indices[:int(full_ip[-1])].cpu()
+    last = sel.paged_kv_last_page_len[:B].cpu()
+
+    def row_kv(layer, pages):
+        cache = eng.model.layers[layer].attention.kv_cache.kv_cache
+        kv = cache[pages.to(DEV).long()].cpu()
+        n = pages.numel()
+        return kv, torch.tensor([0, n], dtype=torch.int32), torch.arange(n, dtype=torch.int32)
+
+    for t, layer in enumerate(planners):
+        sp, si = taken[t]
+        assert (sp[1:] - sp[:-1]).eq(k).all()
+        for b in (0, 31, 63):
+            pages = full_ind[int(full_ip[b]):int(full_ip[b + 1])]
+            n = pages.numel()
+            q = rec[layer][0][b:b + 1].cpu()
+            kv, ip1, ind1 = row_kv(layer, pages)
+            x = O.dump_logits(q, kv, ip1, ind1, last[b:b + 1], scale, n * 16)
+            s_ref = O.legacy_softmax_page_scores(x, 1, n, compute_dtype=torch.float64).float()
+            want_i, _ = O.select_pages(s_ref, torch.tensor([n], dtype=torch.int32), pages[None, :], k, L)
+            got = si[int(sp[b]):int(sp[b + 1])]
+            assert got.tolist() == want_i.tolist(), f"planner {layer} row {b}: selection differs from the oracle"
+            o_ref, _ = O.paged_decode_attention(q, kv, ip1, ind1, last[b:b + 1], scale)
+            assert_close(rec[layer][1][b:b + 1], o_ref, f"planner {layer} row {b} attention")
+            for sub in {2: (3,), 14: (15,), 22: (23, 27)}[layer]:
+                qs, os_ = rec[sub]
+                kv, ip1, ind1 = row_kv(sub, got)
+                o_ref, _ = O.paged_decode_attention(qs[b:b + 1].cpu(), kv, ip1, ind1, last[b:b + 1], scale)
+                assert_close(os_[b:b + 1], o_ref, f"layer {sub} row {b} over planner {layer}'s selection")
+    assert not torch.equal(taken[0][1], taken[1][1]) and not torch.equal(taken[1][1], taken[2][1])
+
+    pos = lens0.cpu()
+    slot_pages = torch.tensor([int(full_ind[int(full_ip[b]) + int(pos[b]) // 16]) for b in range(B)])
+
+    def slots():
+        return [eng.model.layers[i].attention.kv_cache.kv_cache[slot_pages.to(DEV).long(), :,
+                                                                 (pos % 16).to(DEV).long()].clone()
+                for i in range(len(eng.model.layers))]
+
+    eager_slots = slots()
+    sub_ip = sel.paged_subset_kv_indptr[:B + 1].clone()
+    sub_ind = sel.paged_subset_kv_indices[:int(sub_ip[-1])].clone()
+    with torch.inference_mode():
+        eng.cachelens.copy_(lens0)
+        eng.static_tokens.copy_(tok0)
+    eng.sync_host_lens()
+    replay_tok = eng.decode_steps(1, use_graph=True).clone()
+    torch.cuda.synchronize()
+    assert eng._decode_graph_failed is None and eng._decode_graph_stats["replays"] == 1
+    assert torch.equal(replay_tok, eager_tok)
+    assert torch.equal(sel.paged_subset_kv_indptr[:B + 1], sub_ip)
+    assert torch.equal(sel.paged_subset_kv_indices[:int(sub_ip[-1])], sub_ind)
+    for i, (a, b_) in enumerate(zip(slots(), eager_slots)):
+        assert torch.equal(a, b_), f"layer {i}: appended K/V differs"
+    ops.set_active_backend(None)
+    del eng
+    torch.cuda.empty_cache()

@@ -17,6 +17,9 @@ Also measured, in the same process:
     page indices, + the logits for the scorers);
   * the decode step of BASELINE config 4 end to end (Qwen2.5-7B shape, batch 4,
     64 k context), selective and full cache;
+  * the decode step of BASELINE config 5 end to end (Qwen2.5-14B shape, 128 ragged rows of
+    1 k-32 k tokens, per-row budgets; the layers share 8 KV caches since the full KV exceeds
+    HBM), selective and full cache;
   * the reference's own speed recipe end to end (DeepSeek-R1-Distill-Qwen-1.5B shape,
     batch 64, full layers 0 1 2 14 22: three planner layers per step), selective and
     full cache at 2 k, 8 k and 16 k context;
@@ -100,6 +103,49 @@ def engine_config4(torch, warmup: int, steps: int) -> dict:
     return {"workload": "config4: Qwen2.5-7B-shaped decode step, B=4, 65536-token context, 4096-token budget "
                         "(256 pages, compression ratio 16, L=8), full layers [0,1], K outlier channels, "
                         "one hipGraph per step",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 2),
+            "full_cache_ms_per_step": round(ms_full, 4), "full_cache_tokens_per_s": round(B / ms_full * 1e3, 2),
+            "speedup_vs_full_cache": round(ms_full / ms, 3)}
+
+
+def engine_config5(torch, warmup: int, steps: int, kv_pool: int = 8) -> dict:
+    """BASELINE config 5 end to end: a random-init Qwen2.5-14B-shaped model (48 layers, 40 q / 8 kv
+    heads, qkv bias, bf16), batch 128 with context lengths uniform in [1024, 32768] (the
+    configuration's seeded lengths), per-row budgets of max(512, len/8) tokens
+    (``LMBackend.set_subset_budgets``), L = 8, layers 0-1 full, one hipGraph per step; selective
+    and full-cache decode.  The full KV (~425 GB) exceeds one GPU's HBM, so the 48 layers share
+    ``kv_pool`` physical caches round robin (``setup_caches(kv_cache_pool=...)``): every layer
+    still reads and appends its own pages at the real shape."""
+    import random
+    from delta_amd.backend import LMBackend
+    from delta_amd import ops
+    B = 128
+    rng = random.Random(0)
+    lens = [rng.randint(1024, 32768) for _ in range(B)]          # as workloads.config_case(5)
+    budgets = [max(1, max(512, n // 8) // 16) for n in lens]
+    extra = 2 * (warmup + steps) + 16
+    eng = LMBackend(dtype=torch.bfloat16, device="cuda:0", cuda_graph_decode=True)
+    eng.load_model("random:Qwen2.5-14b", seed=0)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = [0, 1]
+    cfg.subset_cache_size = max(budgets)
+    cfg.compression_ratio = 1.0
+    cfg.L = 8
+    eng.setup_caches(max_batch_size=B, max_seq_length=max(lens) + extra + 16, kv_cache_pool=kv_pool)
+    eng.prepare_synthetic_decode(lens, decode_budget=extra, seed=0)
+    eng.set_subset_budgets(budgets)
+    ms = time_steps(torch, eng, warmup, steps)
+    eng.enable_selective_cache = False
+    eng._decode_graph = None
+    ms_full = time_steps(torch, eng, warmup, steps)
+    ops.set_active_backend(None)
+    del eng
+    torch.cuda.empty_cache()
+    return {"workload": f"config5: Qwen2.5-14B-shaped decode step, B=128, contexts U[1024, 32768] "
+                        f"({sum(lens)} cached tokens), per-row budgets max(512, len/8) tokens "
+                        f"({sum(budgets)} pages), L=8, full layers [0,1], one hipGraph per step; the 48 "
+                        f"layers share {kv_pool} KV caches round robin (the full KV exceeds HBM)",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 2),
             "full_cache_ms_per_step": round(ms_full, 4), "full_cache_tokens_per_s": round(B / ms_full * 1e3, 2),
             "speedup_vs_full_cache": round(ms_full / ms, 3)}
@@ -622,6 +668,10 @@ def main():
                     help="skip the end-to-end decode step at BASELINE config 4")
     ap.add_argument("--engine-config4-only", action="store_true",
                     help="only the config-4 decode step (selective and full cache; for kernel traces)")
+    ap.add_argument("--no-engine-config5", action="store_true",
+                    help="skip the end-to-end decode step at BASELINE config 5")
+    ap.add_argument("--engine-config5-only", action="store_true",
+                    help="only the config-5 decode step (selective and full cache)")
     ap.add_argument("--no-engine-recipe", action="store_true",
                     help="skip the reference speed recipe's decode step (DeepSeek-R1-Distill-Qwen-1.5B shape)")
     ap.add_argument("--engine-recipe-only", action="store_true",
@@ -657,6 +707,13 @@ def main():
         log(f"  selective {eng4['ms_per_step']:.3f} ms/step ({eng4['tokens_per_s']} tokens/s), full cache "
             f"{eng4['full_cache_ms_per_step']:.3f} ms/step: {eng4['speedup_vs_full_cache']}x")
         print(json.dumps({"engine_config4": eng4}), flush=True)
+        return
+    if args.engine_config5_only:
+        log("engine at config 5 (Qwen2.5-14B shape, B=128 ragged, per-row budgets)")
+        eng5 = engine_config5(torch, args.warmup, args.steps)
+        log(f"  selective {eng5['ms_per_step']:.3f} ms/step, full cache {eng5['full_cache_ms_per_step']:.3f} ms/step: "
+            f"{eng5['speedup_vs_full_cache']}x")
+        print(json.dumps({"engine_config5": eng5}), flush=True)
         return
     if args.engine_recipe_only:
         log("engine at the reference speed recipe (DeepSeek-R1-Distill-Qwen-1.5B shape, B=64)")
@@ -739,6 +796,17 @@ def main():
             eng4 = {"error": repr(exc)}
             log(f"  failed: {exc!r}")
         torch.cuda.empty_cache()
+    eng5 = None
+    if not args.no_engine_config5:
+        log("engine at config 5 (Qwen2.5-14B shape, B=128 ragged, per-row budgets)")
+        try:
+            eng5 = engine_config5(torch, args.warmup, args.steps)
+            log(f"  selective {eng5['ms_per_step']:.3f} ms/step ({eng5['tokens_per_s']} tokens/s), full cache "
+                f"{eng5['full_cache_ms_per_step']:.3f} ms/step: {eng5['speedup_vs_full_cache']}x")
+        except Exception as exc:  # reported in the line, never fatal for the headline number
+            eng5 = {"error": repr(exc)}
+            log(f"  failed: {exc!r}")
+        torch.cuda.empty_cache()
     recipe = None
     if not args.no_engine_recipe:
         log("engine at the reference speed recipe (DeepSeek-R1-Distill-Qwen-1.5B shape, B=64)")
@@ -782,6 +850,7 @@ def main():
         "prefill": prefill,
         "kernels_other_configs": others,
         "engine_config4": eng4,
+        "engine_config5": eng5,
         "engine_recipe": recipe,
     }
     print(json.dumps(line), flush=True)

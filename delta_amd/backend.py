@@ -185,7 +185,13 @@ class LMBackend:
         self.enable_cuda_graph_decode = True
 
     @torch.inference_mode()
-    def setup_caches(self, max_batch_size: int = 1, max_seq_length: int = 2048):
+    def setup_caches(self, max_batch_size: int = 1, max_seq_length: int = 2048,
+                     kv_cache_pool: Optional[int] = None):
+        """Allocate the paged caches, page tables, planner buffers and workspaces (backend.py:247-593).
+        ``kv_cache_pool`` = n shares n physical KV caches among the layers round robin (layer i
+        uses cache i % n): a benchmark aid for shapes whose KV exceeds HBM (
+        ~425 GB), where every layer still reads and appends its own pages at the real shape but
+        the layers of one cache share its values, so the outputs are not a model's."""
         if self.model is None:
             raise RuntimeError("load_model() first")
         cfg = self.model.config
@@ -250,7 +256,7 @@ class LMBackend:
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
         self._pinned_tokens = torch.zeros(B, dtype=torch.long).pin_memory()
         with torch.device(dev):
-            self.model.setup_caches(num_pages=self.num_pages, page_size=PAGE_SIZE)
+            self.model.setup_caches(num_pages=self.num_pages, page_size=PAGE_SIZE, kv_cache_pool=kv_cache_pool)
         self.layer_roles = list(self.model.layer_roles)
         ops.set_active_backend(self)
         self._decode_graph = None
@@ -613,8 +619,12 @@ class LMBackend:
             g2 = torch.Generator()
             g2.manual_seed(seed + 2)
             outl = torch.randperm(self.model.config.head_dim, generator=g2)[:k_outlier_channels].to(self.device)
+        seen = set()
         for layer in self.model.layers:
             cache = layer.attention.kv_cache.kv_cache
+            if cache.data_ptr() in seen:  # a shared cache (kv_cache_pool) is filled once
+                continue
+            seen.add(cache.data_ptr())
             cache.normal_(0.0, fill_std, generator=gen)
             if outl is not None:
                 cache[:, 0, :, :, outl] *= k_outlier_scale

@@ -129,20 +129,32 @@ class Transformer(nn.Module):
         self.layer_roles: List[str] = []
         self.fused = True
 
-    def setup_caches(self, num_pages: int, page_size: int):
-        """Allocate per-layer caches and bind each layer's attention op (model.py:146-196)."""
+    def setup_caches(self, num_pages: int, page_size: int, kv_cache_pool: Optional[int] = None):
+        """Allocate per-layer caches and bind each layer's attention op (model.py:146-196).
+
+        ``kv_cache_pool`` = n (benchmarks of shapes whose KV exceeds HBM only): n physical caches,
+        layer i uses cache i % n.  Every layer still reads and appends its own pages at the real
+        shape; the values are shared between the layers of a cache, so the outputs are not a
+        model's."""
         cfg = self.config
         head_dim = cfg.dim // cfg.n_head
         dtype = self.output.weight.dtype if self.output.weight.dtype == torch.float16 else torch.bfloat16
         full = set(cfg.full_cache_layers or [])
         self.layer_roles = []
+        pool = None
+        if kv_cache_pool is not None:
+            n = int(kv_cache_pool)
+            if n < 1:
+                raise ValueError("kv_cache_pool must be >= 1")
+            pool = [KVCache(num_pages, page_size, cfg.n_local_heads, head_dim, dtype) for _ in range(min(n, cfg.n_layer))]
         for i, b in enumerate(self.layers):
             if full:
                 use_full = i in full
                 next_full = (i + 1) in full if (i + 1) < cfg.n_layer else True
             else:
                 use_full = next_full = True
-            b.attention.kv_cache = KVCache(num_pages, page_size, cfg.n_local_heads, head_dim, dtype)
+            b.attention.kv_cache = (pool[i % len(pool)] if pool is not None
+                                    else KVCache(num_pages, page_size, cfg.n_local_heads, head_dim, dtype))
             if use_full:
                 if next_full:
                     b.attention.attn_decode = torch.ops.mylib.target_decode

@@ -939,3 +939,28 @@ def test_speed_recipe_shape_three_planners_match_oracle():
     ops.set_active_backend(None)
     del eng
     torch.cuda.empty_cache()
+
+
+def test_kv_cache_pool_shares_caches_round_robin():
+    """setup_caches(kv_cache_pool=n) (a benchmark aid for shapes whose KV exceeds HBM): layer i
+    uses physical cache i % n, prepare_synthetic_decode fills each physical cache once, and a
+    step over the shared caches replays from its graph bit for bit like the eager step."""
+    from delta_amd.backend import LMBackend
+    eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=True)
+    eng.load_model("random:tiny-test", seed=1, n_layer=6)
+    cfg = eng.model.config
+    cfg.enable_selective_cache = True
+    cfg.full_cache_layers = [0, 1]
+    cfg.subset_cache_size = 6
+    cfg.L = 2
+    eng.setup_caches(max_batch_size=3, max_seq_length=512, kv_cache_pool=2)
+    ptrs = [l.attention.kv_cache.kv_cache.data_ptr() for l in eng.model.layers]
+    assert len(set(ptrs)) == 2 and all(ptrs[i] == ptrs[i % 2] for i in range(6))
+    eng.prepare_synthetic_decode([100, 257, 400], decode_budget=16, seed=3)
+    snap = _snapshot(eng)
+    eager = [eng.decode_steps(1, use_graph=False).clone() for _ in range(4)]
+    _restore(eng, snap)
+    replay = [eng.decode_steps(1, use_graph=True).clone() for _ in range(4)]
+    assert all(torch.equal(a, b) for a, b in zip(eager, replay))
+    with pytest.raises(ValueError, match="kv_cache_pool"):
+        eng.setup_caches(max_batch_size=3, max_seq_length=512, kv_cache_pool=0)

@@ -676,6 +676,8 @@ def main():
                     help="skip the reference speed recipe's decode step (DeepSeek-R1-Distill-Qwen-1.5B shape)")
     ap.add_argument("--engine-recipe-only", action="store_true",
                     help="only the reference speed recipe's decode step, selective and full cache")
+    ap.add_argument("--recipe-contexts", default=",".join(str(c) for c in RECIPE_CONTEXTS),
+                    help="contexts the speed recipe's decode step is measured at (comma separated)")
     ap.add_argument("--kernel-reps", type=int, default=60)
     ap.add_argument("--configs-only", action="store_true",
                     help="only the kernel-level measurements at BASELINE configs 2, 4 and 5 (for rocprofv3 runs)")
@@ -717,7 +719,8 @@ def main():
         return
     if args.engine_recipe_only:
         log("engine at the reference speed recipe (DeepSeek-R1-Distill-Qwen-1.5B shape, B=64)")
-        print(json.dumps({"engine_recipe": engine_recipe(torch, args.warmup, args.steps)}), flush=True)
+        ctxs = tuple(int(x) for x in args.recipe_contexts.split(","))
+        print(json.dumps({"engine_recipe": engine_recipe(torch, args.warmup, args.steps, ctxs)}), flush=True)
         return
     if args.configs_only:
         out = {}

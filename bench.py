@@ -232,7 +232,9 @@ def graph_timed(torch, calls, n_warm: int, replays: int = 3, passes: int = 3) ->
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # under inference mode (as the engine captures): the CUDA generator's state, which the capture
+    # updates in place, may have been created there
+    with torch.inference_mode(), torch.cuda.graph(g):
         for f in calls:
             f()
     g.replay()

@@ -107,7 +107,9 @@ def test_noalloc_entry_point_in_a_captured_graph():
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # captured under inference mode, as the engine captures its step: an earlier test may have
+    # created the CUDA generator's state there, which capture_begin then updates in place
+    with torch.inference_mode(), torch.cuda.graph(g):
         _lib.call("delta_paged_decode_noalloc", *args, torch.cuda.current_stream().cuda_stream)
     for i in range(2):
         out.fill_(3.0)

@@ -111,8 +111,9 @@ def engine_config4(torch, warmup: int, steps: int) -> dict:
 def engine_config5(torch, warmup: int, steps: int, kv_pool: int = 8) -> dict:
     """BASELINE config 5 end to end: a random-init Qwen2.5-14B-shaped model (48 layers, 40 q / 8 kv
     heads, qkv bias, bf16), batch 128 with context lengths uniform in [1024, 32768] (the
-    configuration's seeded lengths), per-row budgets of max(512, len/8) tokens
-    (``LMBackend.set_subset_budgets``), L = 8, layers 0-1 full, one hipGraph per step; selective
+    configuration's seeded lengths), per-row budgets of max(512, len/8) tokens recomputed from
+    each row's length at every step (``LMBackend.set_subset_budget_rule``), L = 8, layers 0-1
+    full, one hipGraph per step; selective
     and full-cache decode.  The full KV (~425 GB) exceeds one GPU's HBM, so the 48 layers share
     ``kv_pool`` physical caches round robin (``setup_caches(kv_cache_pool=...)``): every layer
     still reads and appends its own pages at the real shape."""
@@ -122,19 +123,19 @@ def engine_config5(torch, warmup: int, steps: int, kv_pool: int = 8) -> dict:
     B = 128
     rng = random.Random(0)
     lens = [rng.randint(1024, 32768) for _ in range(B)]          # as workloads.config_case(5)
-    budgets = [max(1, max(512, n // 8) // 16) for n in lens]
     extra = 2 * (warmup + steps) + 16
+    budgets = [max(1, max(512, (n + 1) // 8) // 16) for n in lens]  # at the first step (kv_len = n + 1)
     eng = LMBackend(dtype=torch.bfloat16, device="cuda:0", cuda_graph_decode=True)
     eng.load_model("random:Qwen2.5-14b", seed=0)
     cfg = eng.model.config
     cfg.enable_selective_cache = True
     cfg.full_cache_layers = [0, 1]
-    cfg.subset_cache_size = max(budgets)
+    cfg.subset_cache_size = max(512, (max(lens) + extra + 1) // 8) // 16  # the rule's largest budget
     cfg.compression_ratio = 1.0
     cfg.L = 8
     eng.setup_caches(max_batch_size=B, max_seq_length=max(lens) + extra + 16, kv_cache_pool=kv_pool)
     eng.prepare_synthetic_decode(lens, decode_budget=extra, seed=0)
-    eng.set_subset_budgets(budgets)
+    eng.set_subset_budget_rule(512, 8)
     ms = time_steps(torch, eng, warmup, steps)
     eng.enable_selective_cache = False
     eng._decode_graph = None
@@ -143,8 +144,8 @@ def engine_config5(torch, warmup: int, steps: int, kv_pool: int = 8) -> dict:
     del eng
     torch.cuda.empty_cache()
     return {"workload": f"config5: Qwen2.5-14B-shaped decode step, B=128, contexts U[1024, 32768] "
-                        f"({sum(lens)} cached tokens), per-row budgets max(512, len/8) tokens "
-                        f"({sum(budgets)} pages), L=8, full layers [0,1], one hipGraph per step; the 48 "
+                        f"({sum(lens)} cached tokens), per-row budgets max(512, len/8) tokens on the device "
+                        f"({sum(budgets)} pages at the first step), L=8, full layers [0,1], one hipGraph per step; the 48 "
                         f"layers share {kv_pool} KV caches round robin (the full KV exceeds HBM)",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 2),
             "full_cache_ms_per_step": round(ms_full, 4), "full_cache_tokens_per_s": round(B / ms_full * 1e3, 2),

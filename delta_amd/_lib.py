@@ -12,7 +12,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_delta_hip.so"
 
 DELTA_BF16 = 0
 DELTA_FP16 = 1
-ABI_VERSION = 201  # delta_abi_version() of the library these signatures describe
+ABI_VERSION = 202  # delta_abi_version() of the library these signatures describe
 
 _P = c_void_p
 
@@ -27,6 +27,14 @@ class DecodeAppendC(ctypes.Structure):
 
 
 _AP = ctypes.POINTER(DecodeAppendC)
+
+
+class BudgetRuleC(ctypes.Structure):
+    """``delta_budget_rule_t``: per-row budgets max(min_tokens, kv_len / divisor) tokens."""
+    _fields_ = [("min_tokens", c_int), ("divisor", c_int), ("out", c_void_p)]
+
+
+_BR = ctypes.POINTER(BudgetRuleC)
 # name -> (restype, argtypes); one entry per function declared in include/delta_hip.h
 SIGNATURES = {
     "delta_last_error": (ctypes.c_char_p, []),
@@ -80,7 +88,7 @@ SIGNATURES = {
     "delta_pack_page_indices": (c_int, [
         _P, c_int, _P, _P, _P, _P, _P, c_int64, _P, c_int, c_int, c_int, c_int, _P]),
     "delta_decode_page_info": (c_int, [
-        _P, _P, _P, c_int, c_int, c_int, _P, c_double, c_int, _P, _P, _P, _P, _P, _P, _P, _P]),
+        _P, _P, _P, c_int, c_int, c_int, _P, _BR, c_double, c_int, _P, _P, _P, _P, _P, _P, _P, _P]),
     "delta_append_kv": (c_int, [
         _P, c_int64, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P, _P, c_int, c_int, c_int,
         c_int, c_int, _P]),

@@ -237,6 +237,9 @@ class LMBackend:
         # launches when switched on, so a captured step takes new values on every replay.
         self.k_per_row = torch.full((B,), self.k_eff, **i32)
         self._per_row_budgets = False
+        # Or a length rule (``set_subset_budget_rule``): the metadata launch derives each row's
+        # budget from its length at every step and writes it into k_per_row for the selection.
+        self._budget_rule = None
         self.use_subset_flag = torch.zeros(1, **i32)
         self.qo_indptr = torch.arange(B + 1, **i32)
         self.static_tokens = torch.zeros((1, B), dtype=torch.long, device=dev)
@@ -272,10 +275,11 @@ class LMBackend:
         or eager; switching the per-row budgets on or off captures the step again."""
         if self.cachelens is None:
             raise RuntimeError("setup_caches() first")
-        if pages is None:
+        if pages is None:  # also ends a budget rule
             if self._per_row_budgets:
                 self._decode_graph = None
             self._per_row_budgets = False
+            self._budget_rule = None
             return
         vals = [int(x) for x in (pages.tolist() if isinstance(pages, torch.Tensor) else pages)]
         if len(vals) != self.batch_size:
@@ -286,13 +290,46 @@ class LMBackend:
                              f"got {bad[0]}")
         with torch.inference_mode():
             self.k_per_row.copy_(torch.tensor(vals, dtype=torch.int32))
-        if not self._per_row_budgets:
+        if not self._per_row_budgets or self._budget_rule is not None:
             self._decode_graph = None
+        self._budget_rule = None
+        self._per_row_budgets = True
+
+    def set_subset_budget_rule(self, min_tokens: Optional[int] = 512, divisor: int = 8) -> None:
+        """Per-row budgets from each row's length, recomputed on the device at every decode step:
+        row b selects ``max(min_tokens, kv_len_b // divisor)`` tokens in whole 16-token pages,
+        clamped to [1, subset_cache_size], where ``kv_len_b`` is its length after the step's
+        token.  The defaults are BASELINE config 5's ``max(512, len/8)``-token budget.  An
+        extension like ``set_subset_budgets`` (the reference has one global k), but a captured
+        step keeps applying the rule as the rows grow.  ``min_tokens=None`` goes back to the
+        global ``subset_cache_size``; setting fixed budgets replaces the rule."""
+        if self.cachelens is None:
+            raise RuntimeError("setup_caches() first")
+        if min_tokens is None:
+            if self._budget_rule is not None:
+                self._decode_graph = None
+            self._budget_rule = None
+            self._per_row_budgets = False
+            return
+        if int(divisor) < 1 or int(min_tokens) < 0:
+            raise ValueError(f"budget rule needs divisor >= 1 and min_tokens >= 0, got {divisor}, {min_tokens}")
+        rule = (int(min_tokens), int(divisor))
+        if rule != self._budget_rule:  # the rule's constants are baked into the captured launch
+            self._decode_graph = None
+        self._budget_rule = rule
         self._per_row_budgets = True
 
     def _row_budgets(self):
-        """The per-row budget tensor when per-row budgets are on, else None (global k)."""
+        """The per-row budget tensor when per-row budgets (fixed or by rule) are on, else None
+        (global k).  Under a rule the step's metadata launch has just written it."""
         return self.k_per_row if self._per_row_budgets else None
+
+    def _page_info_budgets(self) -> dict:
+        """Budget arguments of the step's metadata launch: the rule with k_per_row as its output,
+        or the fixed per-row budgets, or neither."""
+        if self._budget_rule is not None:
+            return dict(budget_rule=(*self._budget_rule, self.k_per_row))
+        return dict(k_per_row=self._row_budgets())
 
     # ----------------------------------------------------------- op bodies
     def rope_params(self) -> dict:
@@ -409,6 +446,11 @@ class LMBackend:
         counts = [(n + 1) // PAGE_SIZE + 1 for n in lens]
         last = [(n + 1) % PAGE_SIZE for n in lens]
         ks = self.k_per_row.tolist() if self._per_row_budgets else [k] * B
+        if self._budget_rule is not None:  # the rule's budgets for the step's lengths
+            mt, dv = self._budget_rule
+            want = [min(max(max(mt, (n + 1) // dv) // PAGE_SIZE, 1), k) for n in lens]
+            if ks != want:
+                raise RuntimeError("DELTA fast decode page-info mismatch in k_per_row (budget rule)")
         full_tot = sum(c for c, a in zip(counts, act) if a)
         sub_tot = sum(min(c, kb) for c, kb, a in zip(counts, ks, act) if a)
         use = bool(self.enable_selective_cache and sub_tot > 0 and full_tot / sub_tot > self.compression_ratio)
@@ -478,7 +520,7 @@ class LMBackend:
             self.cachelens, self.slot_block_table, B, self.k_eff, self.compression_ratio, self.enable_selective_cache,
             sel.paged_kv_indptr, sel.paged_kv_indices, sel.paged_kv_last_page_len, row_block_table=sel._block_table,
             subset_indices=sel.paged_subset_kv_indices, subset_indptr=sel.paged_subset_kv_indptr,
-            use_subset=self.use_subset_flag, active=self.active, k_per_row=self._row_budgets()))
+            use_subset=self.use_subset_flag, active=self.active, **self._page_info_budgets()))
         self._step = self._decode_csr()
         try:
             tokens = self.model(self.static_tokens, self.cachelens, self.qo_indptr, sel.paged_kv_indices,
@@ -883,7 +925,8 @@ class LMBackend:
                         "delta_dump_buffer_dtype": self.delta_dump_buffer_dtype,
                         "delta_page_score_impl": self.delta_page_score_impl,
                         "planner_logits_on_chip": self._plan_on_chip() if self.enable_selective_cache else False,
-                        "per_row_budgets": self._per_row_budgets}
+                        "per_row_budgets": self._per_row_budgets,
+                        "subset_budget_rule": list(self._budget_rule) if self._budget_rule else None}
                 path.write_text(json.dumps({"meta": meta, "steps": self._step_records}, indent=2))
                 print(f"  Step timings saved to: {path}")
         print("=" * 60)

@@ -30,4 +30,4 @@ int check_launch(const char *what) {
 
 extern "C" DELTA_EXPORT const char *delta_last_error(void) { return delta::g_error; }
 
-extern "C" DELTA_EXPORT int delta_abi_version(void) { return 201; }
+extern "C" DELTA_EXPORT int delta_abi_version(void) { return 202; }

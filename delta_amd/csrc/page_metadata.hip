@@ -17,7 +17,9 @@
 // rows only (backend.py:2047-2067, 2104-2109).  With per-row budgets
 // (k_per_row, an extension: the reference has one global subset_cache_size),
 // row b's subset count is min(pages_b, k_per_row[b]) in the gate's totals and
-// in the default subset CSR, as the selector counts it.
+// in the default subset CSR, as the selector counts it.  A budget rule (max(min_tokens,
+// kv_len / divisor) tokens per row, config 5's shape) derives each row's budget from its current
+// length on the device and writes it out for the selector of the same step.
 #include "delta_common.h"
 
 namespace delta {
@@ -51,6 +53,8 @@ struct PageInfoArgs {
   const int32_t *slot_bt;
   int batch, pages_per_slot, k;
   const int32_t *k_per_row;  // [batch] or null (every row takes k)
+  int rule_min_tokens, rule_divisor;  // budget rule (rule_divisor > 0): see row_budget
+  int32_t *rule_out;                  // [batch]: each row's budget under the rule
   double compression_ratio;
   int selective;
   int32_t *kv_indptr, *kv_indices, *last_page_len, *row_bt, *subset_indices, *subset_indptr, *use_subset;
@@ -69,8 +73,19 @@ __device__ __forceinline__ void row_pages(const PageInfoArgs &a, int b, int *np,
   *last = lp;
 }
 
-// Row b's subset budget in pages (the selector's row_budget: clamped to [0, pages_per_slot]).
+// Row b's subset budget in pages.  With the budget rule: max(min_tokens, kv_len / divisor)
+// tokens after the decode token, in whole pages, clamped to [1, k]; else k_per_row[b] or k, clamped
+// to [0, pages_per_slot] as the selector's row_budget clamps it.
 __device__ __forceinline__ int row_budget(const PageInfoArgs &a, int b) {
+  if (a.rule_divisor > 0) {
+    int64_t kv_len = (int64_t)a.cachelens[b] + 1;
+    kv_len = kv_len < 1 ? 1 : kv_len;
+    const int64_t share = kv_len / a.rule_divisor;
+    const int64_t tokens = share > a.rule_min_tokens ? share : a.rule_min_tokens;
+    int64_t kb = tokens / kPageSize;
+    kb = kb > a.k ? a.k : kb;
+    return kb < 1 ? 1 : (int)kb;
+  }
   int kb = a.k_per_row ? a.k_per_row[b] : a.k;
   kb = kb < 0 ? 0 : kb;
   return kb > a.pages_per_slot ? a.pages_per_slot : kb;
@@ -120,6 +135,7 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
   const bool gate = a.selective && sub_tot > 0 && ((double)full_tot / (double)sub_tot) > a.compression_ratio;
   const int kb = row_budget(a, b);
   const int sc = gate ? (np < kb ? np : kb) : np;
+  if (a.rule_out && tid == 0) a.rule_out[b] = kb;  // the selector reads this step's budgets
   const long long sb = gate ? sub_before : full_before;
   if (tid == 0) {
     a.kv_indptr[b + 1] = (int32_t)(full_before + np);
@@ -170,7 +186,8 @@ extern "C" DELTA_EXPORT int delta_pack_page_indices(const int32_t *slot_block_ta
 
 extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, const int32_t *active,
                                                    const int32_t *slot_block_table, int batch, int pages_per_slot,
-                                                   int k, const int32_t *k_per_row, double compression_ratio,
+                                                   int k, const int32_t *k_per_row,
+                                                   const delta_budget_rule_t *budget_rule, double compression_ratio,
                                                    int selective, int32_t *kv_indptr, int32_t *kv_indices,
                                                    int32_t *kv_last_page_len, int32_t *row_block_table,
                                                    int32_t *subset_indices, int32_t *subset_indptr,
@@ -183,6 +200,10 @@ extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, con
   if (pages_per_slot <= 0) return set_error(DELTA_ERR_INVALID, "delta_decode_page_info: pages_per_slot <= 0");
   if ((subset_indices == nullptr) != (subset_indptr == nullptr))
     return set_error(DELTA_ERR_INVALID, "delta_decode_page_info: subset_indices and subset_indptr go together");
+  if (budget_rule && (k_per_row || budget_rule->divisor <= 0 || budget_rule->min_tokens < 0 || !budget_rule->out))
+    return set_error(DELTA_ERR_INVALID,
+                     "delta_decode_page_info: a budget rule needs divisor > 0, min_tokens >= 0, an output array, "
+                     "and no k_per_row");
   PageInfoArgs a;
   a.cachelens = cachelens;
   a.active = active;
@@ -191,6 +212,9 @@ extern "C" DELTA_EXPORT int delta_decode_page_info(const int32_t *cachelens, con
   a.pages_per_slot = pages_per_slot;
   a.k = k < 0 ? 0 : k;
   a.k_per_row = k_per_row;
+  a.rule_min_tokens = budget_rule ? budget_rule->min_tokens : 0;
+  a.rule_divisor = budget_rule ? budget_rule->divisor : 0;
+  a.rule_out = budget_rule ? budget_rule->out : nullptr;
   a.compression_ratio = compression_ratio;
   a.selective = selective;
   a.kv_indptr = kv_indptr;

@@ -461,14 +461,18 @@ def decode_page_info(cachelens: torch.Tensor, slot_block_table: torch.Tensor, ba
                      subset_indptr: Optional[torch.Tensor] = None,
                      use_subset: Optional[torch.Tensor] = None,
                      active: Optional[torch.Tensor] = None,
-                     k_per_row: Optional[torch.Tensor] = None) -> None:
+                     k_per_row: Optional[torch.Tensor] = None,
+                     budget_rule: Optional[tuple] = None) -> None:
     """Device-side decode page info for rows 0..batch-1 (``delta_decode_page_info``).
 
     ``active`` (int32 [batch], optional) marks the rows the ``use_subset`` gate counts; idle
     rows still get their CSR entries.  ``k_per_row`` (int32 [batch], optional) gives each row
-    its own subset budget in place of ``k``."""
+    its own subset budget in place of ``k``.  ``budget_rule`` = ``(min_tokens, divisor, out)``
+    derives each row's budget from its length instead, ``max(min_tokens, kv_len // divisor) // 16``
+    pages clamped to [1, k], and writes them to ``out`` (int32 [batch]) for ``select_pages``."""
+    rule_out = budget_rule[2] if budget_rule is not None else None
     dev = _check_cuda(cachelens, slot_block_table, kv_indptr, kv_indices, kv_last_page_len,
-                      row_block_table, subset_indices, subset_indptr, use_subset, active, k_per_row)
+                      row_block_table, subset_indices, subset_indptr, use_subset, active, k_per_row, rule_out)
     pps = slot_block_table.shape[1]
     _check_i32("cachelens", cachelens, batch)
     if active is not None:
@@ -488,9 +492,16 @@ def decode_page_info(cachelens: torch.Tensor, slot_block_table: torch.Tensor, ba
         _check_i32("use_subset", use_subset, 1)
     if k_per_row is not None:
         _check_i32("k_per_row", k_per_row, batch)
+    rule = None
+    if budget_rule is not None:
+        if k_per_row is not None:
+            raise ValueError("budget_rule and k_per_row are exclusive")
+        min_tokens, divisor, out = budget_rule
+        _check_i32("budget_rule out", out, batch)
+        rule = ctypes.byref(_lib.BudgetRuleC(int(min_tokens), int(divisor), out.data_ptr()))
     _lib.call("delta_decode_page_info",
               cachelens.data_ptr(), _ptr(active), slot_block_table.data_ptr(), int(batch), int(pps), int(k),
-              _ptr(k_per_row), float(compression_ratio), int(bool(selective)), kv_indptr.data_ptr(),
+              _ptr(k_per_row), rule, float(compression_ratio), int(bool(selective)), kv_indptr.data_ptr(),
               kv_indices.data_ptr(), kv_last_page_len.data_ptr(), _ptr(row_block_table),
               _ptr(subset_indices), _ptr(subset_indptr), _ptr(use_subset), _stream(dev))
 

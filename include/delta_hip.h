@@ -356,10 +356,22 @@ int delta_pack_page_indices(const int32_t *slot_block_table, int num_slots,
  * k_per_row (int32 [batch], optional; an extension, the reference has one
  * global k) gives row b the budget k_per_row[b] in place of k, clamped to
  * [0, pages_per_slot] as delta_select_pages clamps it: the gate's subset total
- * and the default subset CSR then count min(pages, k_per_row[b]) for row b. */
+ * and the default subset CSR then count min(pages, k_per_row[b]) for row b.
+ * budget_rule (optional, exclusive with k_per_row; also an extension) derives
+ * row b's budget from its length after the decode token, kv_len = cachelens[b]
+ * + 1: max(min_tokens, kv_len / divisor) tokens, in whole pages (/ 16),
+ * clamped to [1, k]; the budgets are written to budget_rule->out [batch] for
+ * delta_select_pages (k_per_row) in the same step. */
+typedef struct {
+  int min_tokens;  /* budget floor in tokens (config 5: 512) */
+  int divisor;     /* the row's share: kv_len / divisor tokens (config 5: 8) */
+  int32_t *out;    /* [batch] device array: each row's budget in pages */
+} delta_budget_rule_t;
+
 int delta_decode_page_info(const int32_t *cachelens, const int32_t *active,
                            const int32_t *slot_block_table, int batch, int pages_per_slot, int k,
-                           const int32_t *k_per_row, double compression_ratio,
+                           const int32_t *k_per_row, const delta_budget_rule_t *budget_rule,
+                           double compression_ratio,
                            int selective, int32_t *kv_indptr, int32_t *kv_indices,
                            int32_t *kv_last_page_len, int32_t *row_block_table,
                            int32_t *subset_indices, int32_t *subset_indptr,

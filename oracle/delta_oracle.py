@@ -368,6 +368,20 @@ def decode_page_info(cachelens: torch.Tensor, pages_per_row_alloc: int, k,
     return page_count, last, subset_count, subset_start
 
 
+def budget_rule_pages(cachelens: torch.Tensor, min_tokens: int, divisor: int, k_cap: int,
+                      page_size: int = PAGE_SIZE) -> torch.Tensor:
+    """Per-row subset budgets in pages under a length rule (an extension, no reference code).
+
+    Config 5's "per-sequence budget of max(512, len/8) tokens" read
+    at each decode step: ``len`` is the row's length after the decode token, ``kv_len =
+    cachelens + 1`` (backend.py:2047-2067's plan(1, 16)); the budget is ``max(min_tokens,
+    kv_len // divisor)`` tokens in whole pages (``// page_size``), clamped to ``[1, k_cap]``.
+    """
+    kv_len = cachelens.to(torch.int64) + 1
+    tokens = torch.clamp(kv_len // int(divisor), min=int(min_tokens))
+    return torch.clamp(tokens // page_size, min=1, max=int(k_cap)).to(torch.int32)
+
+
 def use_subset_decision(full_total: int, subset_total: int, compression_ratio: float,
                         enable_selective_cache: bool = True) -> bool:
     """``use_subset`` gate (backend.py:2104-2109): full/subset page ratio above threshold."""

@@ -49,7 +49,7 @@ def test_no_undeclared_exports(lib):
 
 
 def test_queries_without_gpu(lib):
-    assert lib.delta_abi_version() == 201
+    assert lib.delta_abi_version() == 202
     assert lib.delta_last_error() == b""
     # split heuristic: deterministic, >= 1; the larger of the attention and the dump plans.
     # Page-major splits are sized for 16-wave blocks (Hkv heads x R waves): up to 4096 waves in
@@ -91,6 +91,12 @@ def test_argument_errors_reported_without_launch(lib):
                   1, 8, 8, 64, 0, 1.0, 1, None, 0, None)
     with pytest.raises(_lib.DeltaHipError, match="k out of range"):
         _lib.call("delta_select_pages", 8, 4, 8, 8, 4, 1, 4, 5, None, 1, 1e-7, 0, None, 8, 4, 8, None)
+    # a budget rule needs divisor > 0, an output array and no fixed per-row budgets
+    import ctypes
+    for rule, kpr in (((512, 0, 8), None), ((512, 8, None), None), ((-1, 8, 8), None), ((512, 8, 8), 8)):
+        with pytest.raises(_lib.DeltaHipError, match="budget rule needs"):
+            _lib.call("delta_decode_page_info", 8, None, 8, 4, 16, 8, kpr, ctypes.byref(_lib.BudgetRuleC(*rule)),
+                      1.0, 1, 8, 8, 8, None, 8, 8, 8, None)
 
 
 def test_gemm_rows32_plan_and_errors_without_launch(lib):

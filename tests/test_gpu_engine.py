@@ -842,6 +842,86 @@ def test_per_row_budgets_through_the_engine():
     assert not eng._per_row_budgets and eng._decode_graph is None
 
 
+def test_budget_rule_through_the_engine():
+    """set_subset_budget_rule (an extension): each row's budget, max(min_tokens, kv_len //
+    divisor) tokens in pages, is recomputed on the device at every step.  With min 32 tokens,
+    divisor 2 and k = 8, rows of 30, 94, 125, 160, 190 and 470 cached tokens start at 2, 2, 3, 5,
+    5 and 8 pages; rows 1 and 4 cross to 3 and 6 pages at step 1 and row 2 to 4 at step 2.  The
+    first eager step's selections are checked row by row against the oracle chain; then 10
+    graph replays equal 10 eager steps bit for bit, the budgets after each step equal
+    O.budget_rule_pages of the step's lengths, and the debug page-info check (which rebuilds
+    the budgets on the host) passes on every step."""
+    B, k = 6, 8
+    eng = make_engine(graph=True, B=B, k=k, L=2, full_layers=(0, 1, 3), n_layer=6, ratio=1.0)
+    lens = [30, 94, 125, 160, 190, 470]
+    eng.prepare_synthetic_decode(lens, decode_budget=24, seed=43)
+    for bad in ((32, 0), (-1, 2)):
+        with pytest.raises(ValueError, match="budget rule needs"):
+            eng.set_subset_budget_rule(*bad)
+    eng.set_subset_budget_rule(32, 2)
+    assert eng._per_row_budgets and eng._budget_rule == (32, 2)
+    for layer in eng.model.layers:
+        layer.attention.record = []
+    taken = _spy_planner_selections(eng)
+    cl0 = eng.cachelens.cpu()
+    budgets = O.budget_rule_pages(cl0, 32, 2, k).tolist()
+    assert budgets == [2, 2, 3, 5, 5, 8]
+    eng.decode_steps(1, use_graph=False)
+    torch.cuda.synchronize()
+    assert eng.k_per_row.cpu().tolist() == budgets
+    assert int(eng.use_subset_flag) == int(O.decode_step_gate(cl0.tolist(), [1] * B, budgets, 1.0))
+    ip, ind, last, _ = _csr(eng)
+    counts = ip[1:] - ip[:-1]
+    rec = [l.attention.record[0] for l in eng.model.layers]
+    caches = [l.attention.kv_cache.kv_cache.cpu() for l in eng.model.layers]
+    for t, li in enumerate((1, 3)):
+        got_p, got_i = taken[t]
+        assert (got_p[1:] - got_p[:-1]).tolist() == [min(int(c), kb) for c, kb in zip(counts, budgets)]
+        q = rec[li][0].cpu()
+        bt = O.block_table_from_csr(ip, ind, int(counts.max()))
+        x = O.dump_logits(q, caches[li], ip, ind, last, SCALE, int(counts.max()) * 16)
+        s = O.legacy_softmax_page_scores(x, B, int(counts.max()), compute_dtype=torch.float64).float()
+        for b in range(B):
+            wi, _ = O.select_pages(s[b:b + 1], counts[b:b + 1], bt[b:b + 1], budgets[b], eng.L)
+            assert got_i[int(got_p[b]):int(got_p[b + 1])].tolist() == wi.tolist(), f"planner {li} row {b}"
+    eng.attn_plan = type(eng).attn_plan.__get__(eng)  # drop the spy
+    for layer in eng.model.layers:
+        layer.attention.record = None
+    snap = _snapshot(eng)
+    sel = eng.page_selector
+    eng.enable_delta_debug_fast_decode_page_info_parity = True
+
+    def run(use_graph):
+        outs, seen = [], []
+        for _ in range(10):
+            before = eng.cachelens.cpu()
+            tok = eng.decode_steps(1, use_graph=use_graph).clone()
+            p = sel.paged_subset_kv_indptr[:B + 1].clone()
+            outs.append((tok, p, sel.paged_subset_kv_indices[:int(p[-1])].clone()))
+            got = eng.k_per_row.cpu().tolist()
+            assert got == O.budget_rule_pages(before, 32, 2, k).tolist()
+            seen.append(got)
+        return outs, seen, [l.attention.kv_cache.kv_cache.clone() for l in eng.model.layers]
+
+    eager, seen, eager_caches = run(False)
+    assert seen[0] == [2, 3, 3, 5, 6, 8] and seen[1] == [2, 3, 4, 5, 6, 8]  # rows 1, 4, then 2 grew
+    _restore(eng, snap)
+    replay, seen_r, replay_caches = run(True)
+    assert seen_r == seen
+    assert eng._decode_graph_stats["captures"] == 1 and eng._decode_graph_stats["replays"] == 10
+    for i, (a, b) in enumerate(zip(eager, replay)):
+        assert all(torch.equal(x, y) for x, y in zip(a, b)), f"step {i}: replay differs from eager"
+        counts_i = (a[1][1:] - a[1][:-1]).tolist()
+        assert all(c <= kb for c, kb in zip(counts_i, seen[i]))
+    for x, y in zip(eager_caches, replay_caches):
+        assert torch.equal(x, y)
+    eng.set_subset_budgets([1] * B)  # fixed budgets replace the rule (and the captured step)
+    assert eng._budget_rule is None and eng._decode_graph is None
+    eng.set_subset_budget_rule(32, 2)
+    eng.set_subset_budget_rule(None)
+    assert not eng._per_row_budgets and eng._budget_rule is None and eng._decode_graph is None
+
+
 def test_speed_recipe_shape_three_planners_match_oracle():
     """The reference's speed recipe (run_reasoni_speed_compare.sh:16-28) at a 2048-token context:
     DeepSeek-R1-Distill-Qwen-1.5B shape (28 layers, 12 q / 2 kv heads, qkv bias), B = 64, subset

@@ -481,6 +481,53 @@ def test_decode_page_info_per_row_budgets():
             assert sub_i[sp[b]:sp[b + 1]].cpu().tolist() == slot_bt[b, start[b]:int(pc[b])].tolist(), (ratio, b)
 
 
+@pytest.mark.parametrize("min_tokens,divisor,k", [(512, 8, 256), (64, 8, 20), (0, 1, 1000)])
+def test_decode_page_info_budget_rule(min_tokens, divisor, k):
+    """budget_rule (an extension): every row's budget comes from its length on the device,
+    written out equal to O.budget_rule_pages, and the gate's totals and the default subset CSR
+    use it as they use fixed per-row budgets.  300 rows (more than one 256-thread pass of the
+    totals loop) of ragged lengths in [0, 8000], a few idle; the gate is checked on and off."""
+    gen = torch.Generator().manual_seed(12)
+    B = 300
+    cachelens = torch.randint(0, 8001, (B,), generator=gen, dtype=torch.int32)
+    cachelens[:4] = torch.tensor([0, 15, 4223, 8000], dtype=torch.int32)
+    pps = 8001 // 16 + 1
+    active = (torch.rand(B, generator=gen) > 0.1).to(torch.int32)
+    slot_bt = torch.randint(0, 1 << 20, (B, pps), generator=gen, dtype=torch.int32)
+    want_k = O.budget_rule_pages(cachelens, min_tokens, divisor, k)
+    pc, lp, sc, ss = O.decode_page_info(cachelens, pps, want_k)
+    ip = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    ind = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    last = torch.zeros(B, dtype=torch.int32, device=DEV)
+    sub_i = torch.zeros(B * pps, dtype=torch.int32, device=DEV)
+    sub_p = torch.zeros(B + 1, dtype=torch.int32, device=DEV)
+    flag = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    full_tot = int(pc[active.bool()].sum())
+    sub_tot = int(sc[active.bool()].sum())
+    for ratio in (1.0, full_tot / sub_tot - 1e-6, full_tot / sub_tot + 1e-6):
+        out = torch.full((B,), -7, dtype=torch.int32, device=DEV)
+        K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, k, ratio, True, ip, ind, last, None, sub_i,
+                           sub_p, flag, active=active.to(DEV), budget_rule=(min_tokens, divisor, out))
+        torch.cuda.synchronize()
+        assert out.cpu().tolist() == want_k.tolist()
+        want = O.decode_step_gate(cachelens.tolist(), active.tolist(), want_k.tolist(), ratio)
+        assert int(flag) == int(want), ratio
+        cnt = sc.tolist() if want else pc.tolist()
+        start = ss.tolist() if want else [0] * B
+        sp = [0] + torch.cumsum(torch.tensor(cnt), 0).tolist()
+        assert sub_p.cpu().tolist() == sp, ratio
+        got = sub_i.cpu()
+        for b in range(B):
+            assert got[sp[b]:sp[b + 1]].tolist() == slot_bt[b, start[b]:int(pc[b])].tolist(), (ratio, b)
+    out = torch.zeros(B, dtype=torch.int32, device=DEV)
+    with pytest.raises(K._lib.DeltaHipError, match="budget rule needs"):
+        K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, k, 1.0, True, ip, ind, last, None, sub_i,
+                           sub_p, flag, budget_rule=(min_tokens, 0, out))
+    with pytest.raises(ValueError, match="exclusive"):
+        K.decode_page_info(cachelens.to(DEV), slot_bt.to(DEV), B, k, 1.0, True, ip, ind, last, None, sub_i,
+                           sub_p, flag, k_per_row=out, budget_rule=(min_tokens, divisor, out))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_append_kv(dtype):
     c = make_case(batch=3, hq=8, hkv=4, kv_lens=[17, 32, 50], seed=9, dtype=dtype, trailing_empty_page=True)

@@ -101,6 +101,23 @@ def test_per_row_budgets_in_page_info_and_gate():
     assert O.decode_step_gate(cl.tolist(), act, [5] * 4, 2.0) == O.decode_step_gate(cl.tolist(), act, 5, 2.0)
 
 
+def test_budget_rule_pages_hand_counted():
+    """Config 5's max(512, len/8)-token budget, len = cachelens + 1 after the decode token.
+    Hand-counted: 1024 and 4096 tokens sit on the 512-token floor (32 pages); 4223 tokens give
+    527 tokens (32 pages) and 4224 give 528 (33 pages), the first step the share passes a page;
+    32768 tokens give 4096 tokens (256 pages), 100 under a cap of 100; one token with no floor
+    gives 0 tokens, raised to the 1-page minimum."""
+    cl = torch.tensor([1023, 4095, 4222, 4223, 32767], dtype=torch.int32)
+    assert O.budget_rule_pages(cl, 512, 8, 2048).tolist() == [32, 32, 32, 33, 256]
+    assert O.budget_rule_pages(cl, 512, 8, 100).tolist() == [32, 32, 32, 33, 100]
+    assert O.budget_rule_pages(torch.tensor([0, 15, 16]), 0, 8, 64).tolist() == [1, 1, 1]
+    assert O.budget_rule_pages(torch.tensor([0, 255, 256]), 0, 1, 64).tolist() == [1, 16, 16]
+    # fed to decode_page_info as per-row budgets: 4224 tokens hold 265 pages, 33 of them selected
+    pc, _, sc, ss = O.decode_page_info(cl, 2049, k=O.budget_rule_pages(cl, 512, 8, 2048))
+    assert pc.tolist() == [65, 257, 264, 265, 2049] and sc.tolist() == [32, 32, 32, 33, 256]
+    assert ss.tolist() == [33, 225, 232, 232, 1793]
+
+
 # ---------------------------------------------------------------- dump logits
 
 def test_dump_logits_bruteforce():

@@ -13,11 +13,13 @@
 // key's bin is taken) finds the k-th largest key T and
 // how many keys equal to T are taken (r); one ordered pass then marks
 // key > T, or key == T among the first r such pages, and compacts the marked
-// pages in ascending j with ballot prefix sums -- the output is sorted by
-// construction, no sort pass.  Rows of up to 4096 pages keep their keys in
-// registers for all passes; longer rows recompute them from the fp32 scores in
-// every pass (they stay in L2), so any row length works.  When every key equal
-// to T is taken (the usual case), the compaction needs no rank among them.
+// pages in ascending j -- the output is sorted by construction, no sort pass.
+// Rows of up to 1024 (256 threads) or 8192 pages (1024 threads) keep their keys in registers,
+// each thread a contiguous run of up to 4 or 8 pages loaded at the kernel's start, so
+// the compaction is one block prefix sum of the threads' counts (two when keys equal to T must
+// be ranked).  Longer rows recompute the keys from the fp32 scores in every pass (they stay in
+// L2) and compact 1024 pages at a time with ballot prefix sums, so any row length works.  When
+// every key equal to T is taken (the usual case), the compaction needs no rank among them.
 #include <float.h>
 
 #include "delta_common.h"
@@ -26,11 +28,15 @@ namespace delta {
 namespace {
 
 // Block sizes: 1024 threads for rows of more than 1024 pages (few key loads per thread), 256
-// for shorter rows (their barriers wait on 4 waves, not 16).
+// for shorter rows (their barriers wait on 4 waves, not 16).  Keys held in registers per
+// thread: 4 (rows of up to 1024 pages) and 8 (up to 8192 pages: a 128 k-token context).
 constexpr int kSelThreadsLong = 1024;
 constexpr int kSelThreadsShort = 256;
+constexpr int kKeysLong = 8;
+constexpr int kKeysShort = 4;
 constexpr int kBins = 256;         // radix digit bins, handled by the first 4 waves
-constexpr int kKeysPerThread = 4;  // keys held in registers: rows of up to 4096 pages
+constexpr int kHistCopies = 8;     // pass-1 histogram copies
+constexpr int kCopyStride = kBins + 1;
 constexpr uint32_t kKeyPosInf = 0xFF800000u;  // order_key(+inf)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -106,6 +112,29 @@ __device__ int block_sum(int v, int *scratch) {
   return s;
 }
 
+// Exclusive block prefix of an int in thread order over NW waves; *total gets the block total.
+template <int NW>
+__device__ int block_prefix_int(int v, int *scratch, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(inc, off);
+    if (lane >= off) inc += y;
+  }
+  if (lane == 63) scratch[wave] = inc;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int x = scratch[w];
+    before += w < wave ? x : 0;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + inc - v;
+}
+
 // Exclusive block prefix of a 0/1 flag in thread order over NW waves; *total gets the block total.
 template <int NW>
 __device__ int block_prefix(bool flag, int *scratch, int *total) {
@@ -126,18 +155,35 @@ __device__ int block_prefix(bool flag, int *scratch, int *total) {
   return before + wpre;
 }
 
-template <int kSelThreads>
+template <int kSelThreads, int kKeys>
 __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
   constexpr int kSelWaves = kSelThreads / 64;
   static_assert(kSelThreads >= kBins, "the bins are handled by the first kBins threads");
   __shared__ int s_scratch[kSelWaves];
-  __shared__ uint32_t s_hist[kBins];
+  __shared__ uint32_t s_hist[2][kBins];                    // passes 2-4 alternate between the two
+  __shared__ uint32_t s_hcopy[kHistCopies * kCopyStride];  // pass 1: one histogram per (lane & 7)
   __shared__ int s_digit, s_remaining, s_eq;
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  const bool subset = a.use_subset == nullptr || a.use_subset[0] != 0;
+  const float *srow = a.scores + (int64_t)b * a.score_stride;
+  const int32_t *bt = a.block_table + (int64_t)b * a.bt_stride;
+  // When max_pages fits kKeys * kSelThreads, every row keeps its keys in registers, thread t
+  // holding the contiguous run j0 = t * kpt .. j0 + kpt - 1 with kpt = ceil(max_pages /
+  // kSelThreads) <= kKeys (so every wave holds keys).  The scores are loaded first, up to
+  // max_pages (inside the scores' row), so the loads overlap the row bookkeeping below.
+  const bool cached = a.max_pages <= kKeys * kSelThreads;
+  const int kpt = (a.max_pages + kSelThreads - 1) / kSelThreads;
+  const int j0 = tid * kpt;
+  float sv[kKeys];
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kKeys; ++i) sv[i] = i < kpt && j0 + i < a.max_pages ? srow[j0 + i] : 0.f;
+  }
+  for (int x = tid; x < kHistCopies * kCopyStride; x += kSelThreads) s_hcopy[x] = 0;
+  if (tid < kBins) s_hist[1][tid] = 0;  // pass 2's bins; pass 3's are cleared during pass 2
 
+  const bool subset = a.use_subset == nullptr || a.use_subset[0] != 0;
   // Output offset of this row: sum of the counts of the rows before it.
   int before = 0;
   if (subset && a.fixed_count) {
@@ -155,7 +201,6 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
 
   const int tp = row_pages(a, b);
   const int kb = row_budget(a, b);
-  const int32_t *bt = a.block_table + (int64_t)b * a.bt_stride;
   int32_t *out = a.out_indices + before;
   // Never write past the caller's buffer (the indptr above still says what was meant).
   const int64_t room = a.out_len - (int64_t)before;
@@ -170,45 +215,53 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
   }
 
   const int last_start = tp - a.L > 0 ? tp - a.L : 0;
-  auto key_of = [&](int j) -> uint32_t {
+  auto key_of = [&](int j, float s) -> uint32_t {
     if (j >= last_start) return kKeyPosInf;
-    return order_key(prepare(a.scores[(int64_t)b * a.score_stride + j], j, a.bias_scale));
+    return order_key(prepare(s, j, a.bias_scale));
   };
-
-  // Rows of up to kKeysPerThread * 1024 pages keep their keys in registers across the five
-  // passes below; longer rows recompute them from the scores (L2) in every pass.
-  const bool cached = tp <= kKeysPerThread * kSelThreads;
-  uint32_t kc[kKeysPerThread];
+  uint32_t kc[kKeys];
   if (cached) {
 #pragma unroll
-    for (int i = 0; i < kKeysPerThread; ++i) {
-      const int j = tid + i * kSelThreads;
-      kc[i] = j < tp ? key_of(j) : 0u;
-    }
+    for (int i = 0; i < kKeys; ++i) kc[i] = i < kpt && j0 + i < tp ? key_of(j0 + i, sv[i]) : 0u;
   }
+  __syncthreads();  // the histograms are clear
 
-  // Radix select of the kb-th largest key.
+  // Radix select of the kb-th largest key, 8 bits a pass from the top.  Pass 1 counts into
+  // eight lane-indexed copies (one word apart, so one bin's copies sit in different banks): its
+  // digits are the keys' sign and exponent, which few values share, and same-address LDS atomics
+  // of one wave serialise.  Later passes count into one histogram and clear the other for the
+  // pass after, so a pass needs three barriers.
   uint32_t prefix = 0, pmask = 0;
   int remaining = kb;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    if (tid < kBins) s_hist[tid] = 0;
-    __syncthreads();
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    uint32_t *hist = s_hist[pass & 1];
+    uint32_t *bins = pass == 0 ? s_hcopy + (tid & (kHistCopies - 1)) * kCopyStride : hist;
     if (cached) {
 #pragma unroll
-      for (int i = 0; i < kKeysPerThread; ++i) {
+      for (int i = 0; i < kKeys; ++i) {
         const uint32_t key = kc[i];
-        if (tid + i * kSelThreads < tp && (key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+        if (i < kpt && j0 + i < tp && (key & pmask) == prefix) atomicAdd(&bins[(key >> shift) & 255u], 1u);
       }
     } else {
       for (int j = tid; j < tp; j += kSelThreads) {
-        const uint32_t key = key_of(j);
-        if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+        const uint32_t key = key_of(j, srow[j]);
+        if ((key & pmask) == prefix) atomicAdd(&bins[(key >> shift) & 255u], 1u);
       }
     }
+    if (pass > 0 && tid < kBins) s_hist[(pass + 1) & 1][tid] = 0;  // read last in the previous pass
     __syncthreads();
     // Suffix sums over the 256 bins (thread d < 256 holds bin d): suf[d] = #keys with digit >= d.
     const int lane = tid & 63, wave = tid >> 6;
-    const int hd = tid < kBins ? (int)s_hist[tid] : 0;
+    int hd = 0;
+    if (tid < kBins) {
+      if (pass == 0) {
+#pragma unroll
+        for (int c = 0; c < kHistCopies; ++c) hd += (int)s_hcopy[c * kCopyStride + tid];
+      } else {
+        hd = (int)hist[tid];
+      }
+    }
     int suf = hd;
     for (int off = 1; off < 64; off <<= 1) {
       const int y = __shfl_down(suf, off);
@@ -223,22 +276,58 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
       s_eq = hd;  // after the last digit: the number of keys equal to T
     }
     __syncthreads();
+    // s_digit / s_remaining / s_eq are next written after two barriers of the next pass.
     prefix |= (uint32_t)s_digit << shift;
     pmask |= 0xFFu << shift;
     remaining = s_remaining;
-    const bool bin_taken = remaining == s_eq;
-    __syncthreads();
     // Every key of the k-th key's bin is taken: the selection is exactly the keys whose digits so
     // far are >= the prefix, i.e. key >= T with T = prefix (lower bits zero) -- no further pass.
-    if (bin_taken) break;
+    if (remaining == s_eq) break;
   }
   const uint32_t T = prefix;
   const int take_eq = remaining;  // how many keys == T are selected (smallest j first)
   const bool all_eq = take_eq >= s_eq;  // every key equal to T is taken: no rank among them
 
-  // Ordered compaction (block-uniform trip counts: the prefixes hold barriers).
+  if (cached) {
+    // Ordered compaction of the thread's contiguous run: the pages it takes go to its prefix of
+    // the block's counts, in ascending j.  Keys equal to T are taken from the smallest j on:
+    // the thread takes those of its own that rank below take_eq among the block's.
+    int n_gt = 0, n_eq = 0;
+#pragma unroll
+    for (int i = 0; i < kKeys; ++i) {
+      const bool in = i < kpt && j0 + i < tp;
+      n_gt += in && kc[i] > T;
+      n_eq += in && kc[i] == T;
+    }
+    int eq_take = n_eq;
+    if (!all_eq) {
+      int eq_tot;
+      const int eq_before = block_prefix_int<kSelWaves>(n_eq, s_scratch, &eq_tot);
+      const int left = take_eq - eq_before;
+      eq_take = left <= 0 ? 0 : (left < n_eq ? left : n_eq);
+    }
+    int sel_tot;
+    int pos = block_prefix_int<kSelWaves>(n_gt + eq_take, s_scratch, &sel_tot);
+#pragma unroll
+    for (int i = 0; i < kKeys; ++i) {
+      const bool in = i < kpt && j0 + i < tp;
+      const bool eq = in && kc[i] == T;
+      const bool sel = (in && kc[i] > T) || (eq && eq_take > 0);
+      eq_take -= eq ? 1 : 0;
+      if (sel) {
+        if (pos < lim) out[pos] = bt[j0 + i];
+        ++pos;
+      }
+    }
+    return;
+  }
+
+  // Ordered compaction of longer rows, 1024 pages at a time (block-uniform trip counts: the
+  // prefixes hold barriers).
   int eq_seen = 0, written = 0;
-  auto compact = [&](int j, uint32_t key) {
+  for (int base = 0; base < tp; base += kSelThreads) {
+    const int j = base + tid;
+    const uint32_t key = j < tp ? key_of(j, srow[j]) : 0u;
     const bool in = j < tp;
     bool sel;
     if (all_eq) {
@@ -254,16 +343,6 @@ __global__ void __launch_bounds__(kSelThreads) select_pages_kernel(SelArgs a) {
     const int pos = written + block_prefix<kSelWaves>(sel, s_scratch, &sel_tot);
     if (sel && pos < lim) out[pos] = bt[j];
     written += sel_tot;
-  };
-  if (cached) {
-#pragma unroll
-    for (int i = 0; i < kKeysPerThread; ++i)
-      if (i * kSelThreads < tp) compact(tid + i * kSelThreads, kc[i]);
-  } else {
-    for (int base = 0; base < tp; base += kSelThreads) {
-      const int j = base + tid;
-      compact(j, j < tp ? key_of(j) : 0u);
-    }
   }
 }
 
@@ -306,11 +385,11 @@ extern "C" DELTA_EXPORT int delta_select_pages(const float *scores, int64_t scor
   a.out_indices = out_indices;
   a.out_len = out_indices_len;
   a.out_indptr = out_indptr;
-  if (max_pages <= kKeysPerThread * kSelThreadsShort)
-    hipLaunchKernelGGL(select_pages_kernel<kSelThreadsShort>, dim3(batch), dim3(kSelThreadsShort), 0,
+  if (max_pages <= kKeysShort * kSelThreadsShort)
+    hipLaunchKernelGGL((select_pages_kernel<kSelThreadsShort, kKeysShort>), dim3(batch), dim3(kSelThreadsShort), 0,
                        (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(select_pages_kernel<kSelThreadsLong>, dim3(batch), dim3(kSelThreadsLong), 0,
+    hipLaunchKernelGGL((select_pages_kernel<kSelThreadsLong, kKeysLong>), dim3(batch), dim3(kSelThreadsLong), 0,
                        (hipStream_t)stream, a);
   return check_launch(who);
 }

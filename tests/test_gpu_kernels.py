@@ -160,8 +160,9 @@ def test_selection_bit_exact_on_gpu_scores(name):
 
 
 # Row lengths for each selection launch: 256-thread blocks (<= 1024 pages), 1024-thread blocks
-# with the keys in registers (<= 4096) and with the keys re-read every pass (longer).
-@pytest.mark.parametrize("n", [300, 2500, 5000])
+# with the keys in registers (<= 8192; 4097 is config 4's row after its decode token) and with
+# the keys re-read every pass (longer).
+@pytest.mark.parametrize("n", [300, 2500, 4097, 5000, 9000])
 def test_selection_adversarial_scores(n):
     gen = torch.Generator().manual_seed(5)
     B = 6

@@ -176,11 +176,23 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   const int wpos0 = kv_len - qn + tok0;
 
   const int64_t row_elems = (int64_t)a.hkv * kHeadDim;
-  const int64_t page_elems = 2 * kPageSize * row_elems;
+  const int64_t page_bytes = 2 * kPageSize * row_elems * 2;
   // Cooperative step load: 2 * kKvStep * 16 chunks of 16 bytes (K, then V; rows x 16 chunks) over
-  // kPW * 64 threads.
+  // kPW * 64 threads.  Thread t stages chunk c16 = t % 16 of step rows t / 16 and t / 16 + 32 of
+  // K and of V; the 64 lanes of a wave cover four rows of one page, so the page of each of its
+  // loads is wave-uniform (page wave / 4 of the step for rows < 32, wave / 4 + 2 above): its id
+  // and base address are scalars and the lanes' offsets are fixed for the whole sweep.
   constexpr int kChunks = 2 * kKvStep * (kHeadDim / 8);
   constexpr int kPer = kChunks / (kPW * 64);
+  static_assert(kPer == 4 && kKvStep == 64 && kPW * 64 == 2 * kKvStep * 4, "staging layout");
+  const int wq = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));  // wave / 4
+  const int srow = (int)(threadIdx.x >> 4), c16 = (int)(threadIdx.x & 15);  // srow in [0, 32)
+  const uint32_t goff_k = (uint32_t)(((srow & 15) * row_elems + (int64_t)h * kHeadDim + 8 * c16) * 2);
+  const uint32_t goff_v = goff_k + (uint32_t)(kPageSize * row_elems * 2);
+  int lds_off[kPer];  // elements: K rows srow, srow + 32, then the padded V rows
+#pragma unroll
+  for (int r = 0; r < kPer; ++r)
+    lds_off[r] = (r < 2 ? (srow + 32 * r) * kRowP : kTile + (srow + 32 * (r - 2)) * kRowPV) + 8 * c16;
 
   // Page ids, 64 per register (lane i: page cbase + i), the next 64 a chunk ahead.
   const int npages = (nsteps * kKvStep + kPageSize - 1) / kPageSize;
@@ -200,31 +212,30 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   auto id_of = [&](int pg) -> int {  // pg in [cbase, cbase + 128)
     return pg - cbase < 64 ? __builtin_amdgcn_readlane(ids, pg - cbase) : __builtin_amdgcn_readlane(ids_next, pg - cbase - 64);
   };
-  u32x4 ring[kPer];
+  u32x4 ring[kPer];  // K rows srow, srow + 32, V rows srow, srow + 32
   auto fetch = [&](int j) {  // global loads of step j into the ring
-    int pids[kPgStep];
 #pragma unroll
-    for (int p = 0; p < kPgStep; ++p) pids[p] = kPgStep * j + p < npages ? id_of(kPgStep * j + p) : -1;
-#pragma unroll
-    for (int r = 0; r < kPer; ++r) {
-      const int ci = threadIdx.x + r * kPW * 64;
-      const int which = ci / (kKvStep * 16), row = (ci >> 4) % kKvStep, c16 = ci & 15;
-      int pid = pids[0];
-#pragma unroll
-      for (int p = 1; p < kPgStep; ++p)
-        if ((row >> 4) == p) pid = pids[p];
-      ring[r] = pid >= 0 ? ld128(a.kv + (int64_t)pid * page_elems + (int64_t)(which * kPageSize + (row & 15)) * row_elems +
-                                 (int64_t)h * kHeadDim + 8 * c16)
-                         : u32x4{0u, 0u, 0u, 0u};
+    for (int half = 0; half < 2; ++half) {
+      const int pg = kPgStep * j + wq + 2 * half;
+      const int pid = pg < npages ? id_of(pg) : -1;
+      if (pid >= 0) {
+        const char *pb = reinterpret_cast<const char *>(a.kv) + (int64_t)pid * page_bytes;
+        ring[half] = ld128(pb + goff_k);
+        ring[2 + half] = ld128(pb + goff_v);
+      } else {
+        ring[half] = u32x4{0u, 0u, 0u, 0u};
+        ring[2 + half] = u32x4{0u, 0u, 0u, 0u};
+      }
     }
   };
   auto stage = [&](int j) {  // the ring (step j) into tiles[j % kBufs]; V rows past kv_len as zeros
+    uint16_t *tb = &tiles[j % kBufs][0];
+    const bool v_whole = (j + 1) * kKvStep <= kv_len;
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-      const int ci = threadIdx.x + r * kPW * 64;
-      const int which = ci / (kKvStep * 16), row = (ci >> 4) % kKvStep, c16 = ci & 15;
-      const bool keep = which == 0 || j * kKvStep + row < kv_len;
-      st128(&tiles[j % kBufs][(which ? kTile + row * kRowPV : row * kRowP) + 8 * c16], keep ? ring[r] : u32x4{0u, 0u, 0u, 0u});
+      u32x4 v = ring[r];
+      if (r >= 2 && !v_whole && j * kKvStep + srow + 32 * (r - 2) >= kv_len) v = u32x4{0u, 0u, 0u, 0u};
+      st128(tb + lds_off[r], v);
     }
   };
   if (nsteps > 0) {

@@ -202,6 +202,39 @@ def test_selection_fixed_and_use_subset():
     assert idx[:int(indptr[-1])].cpu().tolist() == full.tolist()
 
 
+@pytest.mark.parametrize("n", [1500, 4097, 8192, 9000])
+def test_selection_long_rows_fixed_per_row_and_gate_off(n):
+    """The 1024-thread launch (each thread a contiguous run of ceil(n / 1024) keys, up to 8192
+    pages; longer rows re-read their scores every pass): the fixed path, per-row budgets over
+    ragged rows (each against the oracle's single-row selection with its own k) and the gate
+    off (every row's pages in order)."""
+    gen = torch.Generator().manual_seed(16)
+    B, k, L = 5, 96, 8
+    s = torch.rand(B, n, generator=gen) * 1e-3
+    s[1, ::7] = s[1, 3]  # ties
+    counts = torch.tensor([n, n, n - 5, n // 2, 200])
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(counts, 0)
+    bt = torch.randperm(B * n, generator=gen).reshape(B, n).to(torch.int32)
+    sd, ipd, btd = s.to(DEV), indptr.to(DEV), bt.to(DEV)
+    idx, ip = K.select_pages(sd, ipd, btd, k, L, fixed_count=True)
+    wi, wp = O.select_pages(s, counts, bt, k, L, fixed_count=True)
+    assert ip.cpu().tolist() == wp.tolist() and idx.cpu().tolist() == wi.tolist()
+    kpr = torch.tensor([1, k, 37, k // 2, 200], dtype=torch.int32)  # row 4 (200 pages) takes them all
+    idx, ip = K.select_pages(sd, ipd, btd, 200, L, k_per_row=kpr.to(DEV))
+    got_p = ip.cpu()
+    for b in range(B):
+        kb = int(kpr[b])
+        wi, wp = O.select_pages(s[b:b + 1], counts[b:b + 1], bt[b:b + 1], kb, L)
+        assert int(got_p[b + 1] - got_p[b]) == int(wp[-1]), b
+        assert idx[int(got_p[b]):int(got_p[b + 1])].cpu().tolist() == wi.tolist(), b
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    idx, ip = K.select_pages(sd, ipd, btd, k, L, use_subset=flag)
+    assert ip.cpu().tolist() == indptr.tolist()
+    full = torch.cat([bt[b, :int(counts[b])] for b in range(B)])
+    assert idx[:int(indptr[-1])].cpu().tolist() == full.tolist()
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_selective_step_end_to_end(name):
     """Planner score -> selection -> sparse attention, against the oracle's own chain."""

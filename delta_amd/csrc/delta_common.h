@@ -33,6 +33,11 @@ __device__ __forceinline__ u32x4 ld128(const void *p) {
   return *reinterpret_cast<const u32x4 *>(p);
 }
 __device__ __forceinline__ void st128(void *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
+
+// Buffer resources for raw buffer stores: linear addressing (stride 0), 32-bit data format in the
+// fourth word; cache-policy operand sc1 (agent scope) as the compiler encodes it for gfx950.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kCpolSc1 = 16;
 // Streaming 16-byte load (nontemporal hint): for data read exactly once, such as the K/V
 // pages of a decode step.  On MI355X a page gather issued this way sustains ~6.6 TB/s against
 // ~5.8 TB/s for plain loads of the same addresses.

@@ -313,7 +313,19 @@ __device__ __forceinline__ float rows4_sum(float v) {
 // of LDS tiles, which leaves the LDS to the logits: lane (c, j) loads V[tok(i)][8j, 8j + 8)
 // for its four k slots and MFMA n takes element n of each (two v_perm_b32), so
 // D = O[g = 4c + r][d = 8 lane%16 + n].
-template <int DT, int G, bool WITH_V, bool WITH_DUMP, bool ROPE, bool TOKMAX = false>
+// Store of a split partial.  AGENT (the subset launches): agent-scope (sc1) stores, which
+// measured 2-3 % faster on the small split subset launches at configs 2 and 4 (15.9 -> 15.6 and
+// 12.6 -> 12.2 us with their merge launch, interleaved A/B) but slower on the larger split
+// full-attention launches (config 4 88.1 -> 90.9 us), which keep plain stores.
+template <bool AGENT>
+__device__ __forceinline__ void part_store(float *p, float v) {
+  if constexpr (AGENT)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+
+template <int DT, int G, bool WITH_V, bool WITH_DUMP, bool ROPE, bool TOKMAX = false, bool AGENT_PARTS = false>
 __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *smem) {
   // No FMA contraction: every instantiation (with or without the dump) rounds the softmax
   // arguments identically, so P -- rounded to the KV dtype for the P.V MFMA -- is the same.
@@ -841,13 +853,13 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
         if (g < G) {
           const int64_t pidx = ((int64_t)pslot * a.hkv + h) * G + g;
 #pragma unroll
-          for (int n = 0; n < 8; ++n) a.part_acc[pidx * kHeadDim + 16 * n + t] = acc[n][r];
+          for (int n = 0; n < 8; ++n) part_store<AGENT_PARTS>(&a.part_acc[pidx * kHeadDim + 16 * n + t], acc[n][r]);
         }
       }
       if (c == 0 && t < G) {
         const int64_t pidx = ((int64_t)pslot * a.hkv + h) * G + t;
-        a.part_ml[pidx * 2 + 0] = m;
-        a.part_ml[pidx * 2 + 1] = l;
+        part_store<AGENT_PARTS>(&a.part_ml[pidx * 2 + 0], m);
+        part_store<AGENT_PARTS>(&a.part_ml[pidx * 2 + 1], l);
       }
       return;
     }
@@ -931,10 +943,10 @@ __device__ __forceinline__ void decode_split_body(const DecodeArgs &a, float *sm
       if (TOKMAX) smem[tokmax_lds_header<G>() - 16 + g] = L > 0.f ? M + log2f(L) : -INFINITY;
     } else {
       const int64_t pidx = ((int64_t)pslot * a.hkv + hh) * G + g;
-      if (WITH_V) a.part_acc[pidx * kHeadDim + dd] = A;
+      if (WITH_V) part_store<AGENT_PARTS>(&a.part_acc[pidx * kHeadDim + dd], A);
       if (dd == 0) {
-        a.part_ml[pidx * 2 + 0] = M;
-        a.part_ml[pidx * 2 + 1] = L;
+        part_store<AGENT_PARTS>(&a.part_ml[pidx * 2 + 0], M);
+        part_store<AGENT_PARTS>(&a.part_ml[pidx * 2 + 1], L);
       }
     }
   }
@@ -957,7 +969,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_full_kernel(Decod
 template <int DT, int G, bool ROPE>
 __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_subset_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
-  decode_split_body<DT, G, true, false, ROPE>(a, smem);
+  decode_split_body<DT, G, true, false, ROPE, false, true>(a, smem);
 }
 template <int DT, int G, bool ROPE>
 __global__ void __launch_bounds__(kMaxWaves * 64) paged_decode_plan_kernel(DecodeArgs a) {

@@ -134,7 +134,10 @@ __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) 
   const int tile = (int)gridDim.y - 1 - (int)blockIdx.y;  // heaviest tiles first
   const int btok0 = tile * BT;
   if (btok0 >= qn) return;  // whole block
-  const int tok0 = btok0 + wave * TW;
+  // The wave's first query token, read as a scalar: the compiler cannot see that wave (from the
+  // thread index) is uniform, and with tok0 scalar the wave's step count and its diagonal test
+  // (full / masked step) become scalar branches (8192-token prompt 594 -> 569-585 us).
+  const int tok0 = __builtin_amdgcn_readfirstlane(btok0 + wave * TW);
 
   // Row's pages and length (indptr entries clamped as in the decode kernels).
   const int64_t ilen = a.kv_indices_len;

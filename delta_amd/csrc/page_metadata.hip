@@ -149,14 +149,28 @@ __global__ void __launch_bounds__(256) decode_page_info_kernel(PageInfoArgs a) {
   }
   const int32_t *src = a.slot_bt + (int64_t)b * a.pages_per_slot;
   const int sub_start = np - sc;
-  for (int c = tid; c < a.pages_per_slot; c += 256) {
-    if (c < np) {
-      const int32_t v = src[c];
-      a.kv_indices[full_before + c] = v;
-      if (a.row_bt) a.row_bt[(int64_t)b * a.pages_per_slot + c] = v;
-      if (a.subset_indices && c >= sub_start) a.subset_indices[sb + c - sub_start] = v;
-    } else if (a.row_bt) {
-      a.row_bt[(int64_t)b * a.pages_per_slot + c] = 0;  // no stale ids past the row (backend.py:2080-2086)
+  // Eight 256-page batches' ids are loaded before any of their stores: the stores may alias the
+  // source as far as the compiler knows, so a load-store loop waits one memory round trip per
+  // batch (a 4097-page row: 17 round trips, ~9 us).
+  constexpr int kCopyUnroll = 8;
+  for (int c0 = tid; c0 < a.pages_per_slot; c0 += 256 * kCopyUnroll) {
+    int32_t v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int c = c0 + 256 * u;
+      v[u] = c < np ? src[c] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int c = c0 + 256 * u;
+      if (c >= a.pages_per_slot) break;
+      if (c < np) {
+        a.kv_indices[full_before + c] = v[u];
+        if (a.row_bt) a.row_bt[(int64_t)b * a.pages_per_slot + c] = v[u];
+        if (a.subset_indices && c >= sub_start) a.subset_indices[sb + c - sub_start] = v[u];
+      } else if (a.row_bt) {
+        a.row_bt[(int64_t)b * a.pages_per_slot + c] = 0;  // no stale ids past the row (backend.py:2080-2086)
+      }
     }
   }
 }

@@ -202,6 +202,43 @@ def test_selection_fixed_and_use_subset():
     assert idx[:int(indptr[-1])].cpu().tolist() == full.tolist()
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_selection_random_shapes(seed):
+    """Seeded random selections against the oracle, bit for bit: row counts over both launch
+    sizes and the register-held / re-read paths (max pages 3 .. 9500), ragged rows, random k, L
+    and position bias, quantised scores (ties) with NaN / +-inf sprinkled in, and per-row
+    budgets on every other seed (each row against the oracle's single-row selection)."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    ri = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    B = ri(1, 24)
+    n = [ri(3, 300), ri(300, 1024), ri(1025, 4096), ri(4097, 8192), ri(8193, 9500)][seed % 5]
+    counts = torch.randint(1, n + 1, (B,), generator=g)
+    counts[0] = n
+    s = torch.round(torch.rand(B, n, generator=g) * ri(4, 4096)) / 1024.0
+    s[torch.rand(B, n, generator=g) < 0.01] = float("nan")
+    s[torch.rand(B, n, generator=g) < 0.005] = float("inf")
+    s[torch.rand(B, n, generator=g) < 0.01] = float("-inf")
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(counts, 0)
+    bt = torch.randperm(B * n, generator=g).reshape(B, n).to(torch.int32)
+    k, L = ri(1, min(n, 300)), ri(0, 10)
+    bias = [0.0, 1e-7, 1e-3][seed % 3]
+    sd, ipd, btd = s.to(DEV), indptr.to(DEV), bt.to(DEV)
+    if seed % 2 == 0:
+        idx, ip = K.select_pages(sd, ipd, btd, k, L, pos_bias_scale=bias)
+        wi, wp = O.select_pages(s, counts, bt, k, L, bias)
+        assert ip.cpu().tolist() == wp.tolist()
+        assert idx[:int(wp[-1])].cpu().tolist() == wi.tolist()
+    else:
+        kpr = torch.randint(1, k + 1, (B,), generator=g).to(torch.int32)
+        idx, ip = K.select_pages(sd, ipd, btd, k, L, pos_bias_scale=bias, k_per_row=kpr.to(DEV))
+        got_p = ip.cpu()
+        for b in range(B):
+            wi, wp = O.select_pages(s[b:b + 1], counts[b:b + 1], bt[b:b + 1], int(kpr[b]), L, bias)
+            assert int(got_p[b + 1] - got_p[b]) == int(wp[-1]), b
+            assert idx[int(got_p[b]):int(got_p[b + 1])].cpu().tolist() == wi.tolist(), b
+
+
 @pytest.mark.parametrize("n", [1500, 4097, 8192, 9000])
 def test_selection_long_rows_fixed_per_row_and_gate_off(n):
     """The 1024-thread launch (each thread a contiguous run of ceil(n / 1024) keys, up to 8192

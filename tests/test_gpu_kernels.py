@@ -780,6 +780,34 @@ def test_paged_prefill_matches_oracle(hq, hkv, dtype):
     assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_paged_prefill_random_shapes(seed):
+    """Seeded random prefill shapes against the oracle: group sizes 1-8, 1-8 kv heads, 1-6 rows
+    of 1-700 cached tokens with prompts of 1..kv_len tokens (chunked prefill: the prompt's first
+    token sits past the row's start), trailing empty pages and both dtypes; o and lse."""
+    g = torch.Generator().manual_seed(2000 + seed)
+    ri = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    G, hkv = ri(1, 8), [1, 2, 4, 8][ri(0, 3)]
+    hq = G * hkv
+    B = ri(1, 6)
+    kv_lens = [ri(1, 700) for _ in range(B)]
+    qo = [ri(1, n) for n in kv_lens]
+    dtype = [torch.bfloat16, torch.float16][seed % 2]
+    c = make_case(batch=B, hq=hq, hkv=hkv, kv_lens=kv_lens, seed=50 + seed, page_order="randperm", k=4, L=2,
+                  dtype=dtype, trailing_empty_page=bool(seed % 3 == 0))
+    q = torch.randn(sum(qo), hq, 128, generator=g).to(dtype)
+    qo_indptr = torch.tensor([0] + list(torch.cumsum(torch.tensor(qo), 0)), dtype=torch.int32)
+    gc = gpu(c)
+    lse = torch.empty(sum(qo), hq, device=DEV)
+    o = K.paged_prefill(q.to(DEV), gc.kv_cache, qo_indptr.to(DEV), gc.kv_indptr, gc.kv_indices,
+                        gc.kv_last_page_len, max_qo_len=max(qo), lse=lse)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = O.paged_prefill_attention(q, qo_indptr, c.kv_cache, c.kv_indptr, c.kv_indices,
+                                               c.kv_last_page_len, c.sm_scale)
+    assert_attn_close(o, o_ref, f"random prefill seed {seed}: G={G} hkv={hkv} kv={kv_lens} qo={qo}")
+    assert torch.allclose(lse.cpu(), lse_ref, atol=1e-3, rtol=1e-4)
+
+
 @pytest.mark.parametrize("sign", [1.0, -1.0])
 def test_paged_prefill_long_rows_growing_scores(sign):
     """Prompts of 1100 and 300 tokens (more than 64 pages: the page-id window moves), K scaled

@@ -78,21 +78,23 @@ __global__ void __launch_bounds__(256) dump_lse_kernel(const float *dump, int64_
 // One token per thread; the max over q heads of exp2(logit log2e - lse log2e), then the 16-lane
 // page sum.  Two loads per lane bring the first NH heads' lse values (lane i: head i) and the
 // row bounds (lanes 0-2); then each pass requests the logits of NH heads as independent loads,
-// so a block waits two memory round trips for hq <= NH.  Heads past hq - 1 repeat head hq - 1,
-// which leaves the max unchanged.  Blocks wholly past the row's kv_len load no logits.
+// so a block waits two memory round trips for hq <= NH.  NH is hq rounded up to a multiple of 8
+// (at most 64, then several passes); heads past hq - 1 repeat head hq - 1, which leaves the max
+// unchanged.  Blocks wholly past the row's kv_len load no logits.
 template <int NH>
 __global__ void __launch_bounds__(kScoreThreads)
     legacy_softmax_score_kernel(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
                                 const int32_t *kv_indptr, const int32_t *last, float *scores,
                                 int64_t score_stride, int hq, int max_pages) {
-  static_assert(NH == 32 || NH == 64, "lse of head h0 + i sits in lane i");
+  static_assert(NH % 8 == 0 && NH >= 8 && NH <= 64, "lse of head h0 + i sits in lane i");
   const int b = blockIdx.y;
   const int tok = blockIdx.x * kScoreThreads + threadIdx.x;
   const int lane = threadIdx.x & 63;
   const int32_t *bsrc = lane == 0 ? kv_indptr + b : lane == 1 ? kv_indptr + b + 1 : last + b;
   const int bw = *bsrc;
   const float *lse_b = lse + (int64_t)b * hq;
-  float lv = lse_b[min(lane & (NH - 1), hq - 1)];
+  const int lh = lane < NH ? lane : NH - 1;  // lane i < NH holds head h0 + i's lse
+  float lv = lse_b[min(lh, hq - 1)];
   asm volatile("" ::"v"(bw), "v"(lv));  // both loads in flight together
   int np = __builtin_amdgcn_readlane(bw, 1) - __builtin_amdgcn_readlane(bw, 0);
   np = np < 0 ? 0 : np;
@@ -103,7 +105,7 @@ __global__ void __launch_bounds__(kScoreThreads)
   float best = 0.f;
   if ((int)blockIdx.x * kScoreThreads < n) {
     for (int h0 = 0; h0 < hq; h0 += NH) {
-      if (h0 > 0) lv = lse_b[min(h0 + (lane & (NH - 1)), hq - 1)];
+      if (h0 > 0) lv = lse_b[min(h0 + lh, hq - 1)];
       if (tok < n) {
         float x[NH];
 #pragma unroll
@@ -156,13 +158,23 @@ int launch_scores(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
                   const int32_t *kv_indptr, const int32_t *last, float *scores, int64_t score_stride,
                   int batch, int hq, int max_pages, hipStream_t stream, const char *who) {
   dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
-  // Heads per pass: every head in one pass up to 64 (32 when that covers them).
-  if (hq <= 32)
-    hipLaunchKernelGGL(legacy_softmax_score_kernel<32>, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse,
-                       kv_indptr, last, scores, score_stride, hq, max_pages);
-  else
-    hipLaunchKernelGGL(legacy_softmax_score_kernel<64>, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse,
-                       kv_indptr, last, scores, score_stride, hq, max_pages);
+  // Heads per pass: hq rounded up to a multiple of 8, every head in one pass up to 64 (each
+  // repeated head would cost a load and an exponential per token).
+  const int nh = hq >= 64 ? 64 : ((hq + 7) / 8) * 8;
+  auto launch = [&](auto k) {
+    hipLaunchKernelGGL(k, grid, dim3(kScoreThreads), 0, stream, dump, sdb, sdh, lse, kv_indptr, last, scores,
+                       score_stride, hq, max_pages);
+  };
+  switch (nh) {
+    case 8: launch(legacy_softmax_score_kernel<8>); break;
+    case 16: launch(legacy_softmax_score_kernel<16>); break;
+    case 24: launch(legacy_softmax_score_kernel<24>); break;
+    case 32: launch(legacy_softmax_score_kernel<32>); break;
+    case 40: launch(legacy_softmax_score_kernel<40>); break;
+    case 48: launch(legacy_softmax_score_kernel<48>); break;
+    case 56: launch(legacy_softmax_score_kernel<56>); break;
+    default: launch(legacy_softmax_score_kernel<64>); break;
+  }
   return check_launch(who);
 }
 

@@ -131,6 +131,32 @@ def test_page_scores(name):
         assert rel.max().item() < 1e-4, f"{name}/{what}: rel err {rel.max().item()}"
 
 
+@pytest.mark.parametrize("hq", [4, 12, 20, 24, 40, 44, 48, 56, 64, 72, 96])
+def test_page_scores_from_logits_head_counts(hq):
+    """The score kernel's head passes (hq rounded up to a multiple of 8 up to 64 heads, several
+    passes above) on synthetic logits: rows of 1, 333 and 640 tokens (-inf past kv_len), with the
+    planner's lse and with the two-pass normaliser, within 1e-4 of the fp64 oracle."""
+    gen = torch.Generator().manual_seed(hq)
+    kv_lens = [1, 333, 640]
+    B = len(kv_lens)
+    pages = [n // 16 + (n % 16 > 0) for n in kv_lens]
+    mp = max(pages)
+    indptr = torch.zeros(B + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(pages), 0)
+    last = torch.tensor([n - 16 * (p - 1) for n, p in zip(kv_lens, pages)], dtype=torch.int32)
+    x = torch.randn(B, hq, mp * 16, generator=gen) * 3
+    for b, n in enumerate(kv_lens):
+        x[b, :, n:] = float("-inf")
+    lse = torch.logsumexp(x.double(), dim=-1).float()
+    ref = O.legacy_softmax_page_scores(x, B, mp, compute_dtype=torch.float64).double()
+    xd = x.to(DEV)
+    for what, kw in (("planner lse", dict(lse=lse.to(DEV))), ("two-pass", {})):
+        s = K.page_scores_from_logits(xd, indptr.to(DEV), last.to(DEV), mp, **kw).cpu().double()
+        rel = (s - ref).abs() / ref.abs().clamp_min(1e-30)
+        rel[ref == 0] = s[ref == 0].abs()
+        assert rel.max().item() < 1e-4, f"hq={hq} {what}: rel err {rel.max().item()}"
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_selection_bit_exact_on_gpu_scores(name):
     c = CASES[name]()

@@ -8,14 +8,15 @@
 //   tie order unspecified; this build fixes it), positions emitted in
 //   ascending j (132-134) as physical ids from the row's block table (147-150).
 //
-// Algorithm per row (one block of 256 or 1024 threads): fp32 keys map to order-preserving uint32
+// Algorithm per row (one block of 256, 512 or 1024 threads): fp32 keys map to order-preserving uint32
 // (+0/-0 folded); an 8-bit radix select (up to 4 passes; it stops once every key of the k-th
 // key's bin is taken) finds the k-th largest key T and
 // how many keys equal to T are taken (r); one ordered pass then marks
 // key > T, or key == T among the first r such pages, and compacts the marked
 // pages in ascending j -- the output is sorted by construction, no sort pass.
-// Rows of up to 1024 (256 threads) or 8192 pages (1024 threads) keep their keys in registers,
-// each thread a contiguous run of up to 4 or 8 pages loaded at the kernel's start, so
+// Rows of up to 1024 (256 threads), 4096 (512 threads) or 8192 pages (1024 threads) keep their
+// keys in registers, each thread a contiguous run of up to 4 or 8 pages loaded at the kernel's
+// start, so
 // the compaction is one block prefix sum of the threads' counts (two when keys equal to T must
 // be ranked).  Longer rows recompute the keys from the fp32 scores in every pass (they stay in
 // L2) and compact 1024 pages at a time with ballot prefix sums, so any row length works.  When
@@ -27,10 +28,13 @@
 namespace delta {
 namespace {
 
-// Block sizes: 1024 threads for rows of more than 1024 pages (few key loads per thread), 256
-// for shorter rows (their barriers wait on 4 waves, not 16).  Keys held in registers per
-// thread: 4 (rows of up to 1024 pages) and 8 (up to 8192 pages: a 128 k-token context).
+// Block sizes by the launch's longest row: 256 threads x 4 keys up to 1024 pages, 512 x 4 up to
+// 2048, 512 x 8 up to 4096, 1024 x 8 up to 8192 (a 128 k-token context) and past it (keys
+// re-read every pass).  Fewer waves wait at each of a pass's barriers; against 1024-thread
+// blocks, 512 x 4 took 64 rows of 1125 pages 9.0 -> 7.0 us and config 5 (2046 pages) 10.0 -> 7.8
+// us, 512 x 8 16 rows of 3000 pages 10.4 -> 9.2 us and 4096-page rows the same 10.3 us.
 constexpr int kSelThreadsLong = 1024;
+constexpr int kSelThreadsMid = 512;
 constexpr int kSelThreadsShort = 256;
 constexpr int kKeysLong = 8;
 constexpr int kKeysShort = 4;
@@ -387,6 +391,12 @@ extern "C" DELTA_EXPORT int delta_select_pages(const float *scores, int64_t scor
   a.out_indptr = out_indptr;
   if (max_pages <= kKeysShort * kSelThreadsShort)
     hipLaunchKernelGGL((select_pages_kernel<kSelThreadsShort, kKeysShort>), dim3(batch), dim3(kSelThreadsShort), 0,
+                       (hipStream_t)stream, a);
+  else if (max_pages <= kKeysShort * kSelThreadsMid)
+    hipLaunchKernelGGL((select_pages_kernel<kSelThreadsMid, kKeysShort>), dim3(batch), dim3(kSelThreadsMid), 0,
+                       (hipStream_t)stream, a);
+  else if (max_pages <= kKeysLong * kSelThreadsMid)
+    hipLaunchKernelGGL((select_pages_kernel<kSelThreadsMid, kKeysLong>), dim3(batch), dim3(kSelThreadsMid), 0,
                        (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL((select_pages_kernel<kSelThreadsLong, kKeysLong>), dim3(batch), dim3(kSelThreadsLong), 0,

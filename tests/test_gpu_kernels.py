@@ -185,10 +185,11 @@ def test_selection_bit_exact_on_gpu_scores(name):
     assert idx[:int(want_p[-1])].cpu().tolist() == want_i.tolist()
 
 
-# Row lengths for each selection launch: 256-thread blocks (<= 1024 pages), 1024-thread blocks
-# with the keys in registers (<= 8192; 4097 is config 4's row after its decode token) and with
-# the keys re-read every pass (longer).
-@pytest.mark.parametrize("n", [300, 2500, 4097, 5000, 9000])
+# Row lengths for each selection launch: 256-thread blocks (<= 1024 pages), 512-thread blocks
+# with 4 or 8 keys per thread (<= 2048, <= 4096), 1024-thread blocks with the keys in registers
+# (<= 8192; 4097 is config 4's row after its decode token) and with the keys re-read every pass
+# (longer).
+@pytest.mark.parametrize("n", [300, 1500, 2500, 4097, 5000, 9000])
 def test_selection_adversarial_scores(n):
     gen = torch.Generator().manual_seed(5)
     B = 6
@@ -265,12 +266,12 @@ def test_selection_random_shapes(seed):
             assert idx[int(got_p[b]):int(got_p[b + 1])].cpu().tolist() == wi.tolist(), b
 
 
-@pytest.mark.parametrize("n", [1500, 4097, 8192, 9000])
+@pytest.mark.parametrize("n", [1500, 3000, 4097, 8192, 9000])
 def test_selection_long_rows_fixed_per_row_and_gate_off(n):
-    """The 1024-thread launch (each thread a contiguous run of ceil(n / 1024) keys, up to 8192
-    pages; longer rows re-read their scores every pass): the fixed path, per-row budgets over
-    ragged rows (each against the oracle's single-row selection with its own k) and the gate
-    off (every row's pages in order)."""
+    """The 512- and 1024-thread launches (each thread a contiguous run of ceil(n / threads)
+    keys, up to 8192 pages; longer rows re-read their scores every pass): the fixed path,
+    per-row budgets over ragged rows (each against the oracle's single-row selection with its
+    own k) and the gate off (every row's pages in order)."""
     gen = torch.Generator().manual_seed(16)
     B, k, L = 5, 96, 8
     s = torch.rand(B, n, generator=gen) * 1e-3

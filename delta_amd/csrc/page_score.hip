@@ -124,8 +124,10 @@ __global__ void __launch_bounds__(kScoreThreads)
 // Page scores from the LDS scorer's per-(kv head, token) maxima tm [batch][hkv][sh]: one token per
 // thread, the max over the hkv values (the max over all q heads of the token's probability),
 // then the same 16-lane page sum as legacy_softmax_score_kernel.  One load brings the row bounds
-// (lanes 0-2); then the kMaxWaves kv heads' maxima are requested together (heads past hkv - 1
+// (lanes 0-2); then KH kv heads' maxima (hkv rounded up to a power of two, at most kMaxWaves)
+// are requested together (heads past hkv - 1
 // repeat head hkv - 1, which leaves the max unchanged).
+template <int KH>
 __global__ void __launch_bounds__(kScoreThreads)
     tokmax_score_kernel(const float *tm, int64_t sb, int64_t sh, int hkv, const int32_t *kv_indptr,
                         const int32_t *last, float *scores, int64_t score_stride, int max_pages) {
@@ -143,15 +145,31 @@ __global__ void __launch_bounds__(kScoreThreads)
   const float *col = tm + (int64_t)b * sb + tok;
   float best = 0.f;
   if (tok < n) {
-    float v[kMaxWaves];
+    float v[KH];
 #pragma unroll
-    for (int kh = 0; kh < kMaxWaves; ++kh) v[kh] = __builtin_nontemporal_load(col + min(kh, hkv - 1) * sh);
+    for (int kh = 0; kh < KH; ++kh) v[kh] = __builtin_nontemporal_load(col + min(kh, hkv - 1) * sh);
 #pragma unroll
-    for (int kh = 0; kh < kMaxWaves; ++kh) best = fmaxf(best, v[kh]);
+    for (int kh = 0; kh < KH; ++kh) best = fmaxf(best, v[kh]);
   }
   const float page_sum = row16_sum(best);
   const int page = tok >> 4;
   if ((threadIdx.x & 15) == 0 && page < max_pages) scores[(int64_t)b * score_stride + page] = page_sum;
+}
+
+// The page-sum launch over per-(kv head, token) maxima, KH = hkv rounded up to a power of two.
+void launch_tokmax_scores(const float *tm, int64_t sb, int64_t sh, int hkv, const int32_t *kv_indptr,
+                          const int32_t *last, float *scores, int64_t score_stride, int batch, int max_pages,
+                          hipStream_t stream) {
+  dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
+  auto launch = [&](auto k) {
+    hipLaunchKernelGGL(k, grid, dim3(kScoreThreads), 0, stream, tm, sb, sh, hkv, kv_indptr, last, scores,
+                       score_stride, max_pages);
+  };
+  if (hkv <= 1) launch(tokmax_score_kernel<1>);
+  else if (hkv <= 2) launch(tokmax_score_kernel<2>);
+  else if (hkv <= 4) launch(tokmax_score_kernel<4>);
+  else if (hkv <= 8) launch(tokmax_score_kernel<8>);
+  else launch(tokmax_score_kernel<kMaxWaves>);
 }
 
 int launch_scores(const float *dump, int64_t sdb, int64_t sdh, const float *lse,
@@ -276,9 +294,8 @@ extern "C" DELTA_EXPORT int delta_page_score(const void *q, int64_t q_stride_b, 
                         kv_last_page_len, nullptr, 0, 0, nullptr, tm, sb, sh, batch, num_qo_heads, num_kv_heads,
                         head_dim, dtype, sm_scale, max_pages, /*kScoreTokmax*/ 4, nullptr, 0, st, who, nullptr);
     if (rc) return rc;
-    dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
-    hipLaunchKernelGGL(tokmax_score_kernel, grid, dim3(kScoreThreads), 0, st, tm, sb, sh, num_kv_heads, kv_indptr,
-                       kv_last_page_len, scores, score_stride, max_pages);
+    launch_tokmax_scores(tm, sb, sh, num_kv_heads, kv_indptr, kv_last_page_len, scores, score_stride, batch,
+                         max_pages, st);
     return check_launch(who);
   }
   const int ns = decode_num_splits(batch, num_kv_heads, max_pages);
@@ -327,9 +344,8 @@ int run_decode_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h, con
                       num_kv_heads, head_dim, dtype, sm_scale, max_pages, /*kAttnTokmax*/ 5, nullptr, 0, st, who,
                       ap);
   if (rc) return rc;
-  dim3 grid((unsigned)ceil_div((int64_t)max_pages * kPageSize, kScoreThreads), batch);
-  hipLaunchKernelGGL(tokmax_score_kernel, grid, dim3(kScoreThreads), 0, st, tm, sb, sh, num_kv_heads, kv_indptr,
-                     kv_last_page_len, scores, score_stride, max_pages);
+  launch_tokmax_scores(tm, sb, sh, num_kv_heads, kv_indptr, kv_last_page_len, scores, score_stride, batch, max_pages,
+                       st);
   return check_launch(who);
 }
 }  // namespace

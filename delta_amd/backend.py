@@ -26,7 +26,6 @@ Out of scope on this build (raise): tensor parallelism, ``torch.compile``
 from __future__ import annotations
 
 import json
-import math
 import os
 import time
 from collections import defaultdict

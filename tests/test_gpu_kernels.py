@@ -4,7 +4,6 @@ Tolerances (north star): selected page sets bit-exact; page scores within 1e-4
 relative (fp32); attention outputs within 2e-2 absolute with cosine > 0.999
 (bf16/fp16).  Logits dump within 1e-4 * (1 + |x|) (fp32 accumulation order).
 """
-import math
 
 import pytest
 import torch

@@ -117,7 +117,6 @@ __device__ __forceinline__ float halves_sum(float v) {
 template <int DT, int G>
 __global__ void __launch_bounds__(kPW * 64) paged_prefill_kernel(PrefillArgs a) {
 #pragma clang fp contract(off)
-  using E = Elem<DT>;
   using MF = Mfma32<DT>;
   constexpr int TW = 32 / G;                  // query tokens per wave
   constexpr int BT = kPW * TW;                // query tokens per block

@@ -774,9 +774,14 @@ def main():
         log(f"  {k}: {v['us']} us, {v['GB_s']} GB/s ({100 * v['frac']:.1f}% of peak)")
     dom = kern["paged_decode_subset_kernel<ROPE>"]  # the launch each selective layer of a step makes
     log("prefill kernel")
-    prefill = prefill_roofline(torch)
-    log(f"  paged_prefill_kernel: {prefill['us']} us, {prefill['TFLOP_s']} TFLOP/s "
-        f"({100 * prefill['frac']:.1f}% of bf16 MFMA peak)")
+    try:
+        prefill = prefill_roofline(torch)
+        log(f"  paged_prefill_kernel: {prefill['us']} us, {prefill['TFLOP_s']} TFLOP/s "
+            f"({100 * prefill['frac']:.1f}% of bf16 MFMA peak)")
+    except Exception as exc:  # reported in the line, never fatal for the headline number
+        prefill = {"error": repr(exc)}
+        log(f"  failed: {exc!r}")
+    torch.cuda.empty_cache()
     others = None
     if not args.no_other_configs:
         others = {}
@@ -825,8 +830,12 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
-        cpu = cpu_baseline(torch)
-        log(f"  cpu: {cpu['value']} tokens/s on {cpu['cores']} cores")
+        try:
+            cpu = cpu_baseline(torch)
+            log(f"  cpu: {cpu['value']} tokens/s on {cpu['cores']} cores")
+        except Exception as exc:  # reported in the line, never fatal for the headline number
+            cpu = {"error": repr(exc)}
+            log(f"  failed: {exc!r}")
 
     line = {
         "metric": METRIC,

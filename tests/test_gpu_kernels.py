@@ -130,6 +130,30 @@ def test_page_scores(name):
         assert rel.max().item() < 1e-4, f"{name}/{what}: rel err {rel.max().item()}"
 
 
+@pytest.mark.parametrize("name", ["cfg2_fp16_small", "cfg3_bf16_small", "long_row_b1"])
+def test_planner_dump_at_unaligned_address(name):
+    """The planner's dump stores (16-byte buffer stores) into a dump view at a 4-byte offset
+    with odd row strides, as the C ABI allows: the dump, lse and o equal those of an aligned
+    dump, and nothing is written outside the view."""
+    c = CASES[name]()
+    g = gpu(c)
+    B, hq = c.q.shape[:2]
+    mp = c.max_pages
+    dump_a = torch.full((B, hq, mp * 16), float("-inf"), device=DEV)
+    lse_a = torch.empty(B, hq, device=DEV)
+    o_a = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                         lse=lse_a, logits_dump=dump_a)
+    base = torch.full((B, hq, mp * 16 + 1), 7.0, device=DEV)
+    dump_u = base[:, :, 1:]
+    dump_u.fill_(float("-inf"))
+    lse_u = torch.empty(B, hq, device=DEV)
+    o_u = K.paged_decode(g.q, g.kv_cache, g.kv_indptr, g.kv_indices, g.kv_last_page_len, max_pages_per_row=mp,
+                         lse=lse_u, logits_dump=dump_u)
+    torch.cuda.synchronize()
+    assert torch.equal(dump_u, dump_a) and torch.equal(lse_u, lse_a) and torch.equal(o_u, o_a)
+    assert bool((base[:, :, 0] == 7.0).all())
+
+
 @pytest.mark.parametrize("hq", [4, 12, 20, 24, 40, 44, 48, 56, 64, 72, 96])
 def test_page_scores_from_logits_head_counts(hq):
     """The score kernel's head passes (hq rounded up to a multiple of 8 up to 64 heads, several

@@ -91,6 +91,11 @@ def test_argument_errors_reported_without_launch(lib):
                   1, 8, 8, 64, 0, 1.0, 1, None, 0, None)
     with pytest.raises(_lib.DeltaHipError, match="k out of range"):
         _lib.call("delta_select_pages", 8, 4, 8, 8, 4, 1, 4, 5, None, 1, 1e-7, 0, None, 8, 4, 8, None)
+    # the dump writer's offsets must stay below 2^31 bytes: max_pages * 16 <= 2^28 floats
+    # (aligned stand-in addresses; rejected before any launch)
+    with pytest.raises(_lib.DeltaHipError, match="max_pages \\* 16 <= 2\\^28"):
+        _lib.call("delta_paged_decode", 256, 1024, 128, 256, 100, 256, 256, 100, 256, 256, 1024, 128, None,
+                  256, 1 << 30, 1 << 28, 1, 8, 8, 128, 0, 1.0, (1 << 24) + 1, None, 0, None)
     # a budget rule needs divisor > 0, an output array and no fixed per-row budgets
     import ctypes
     for rule, kpr in (((512, 0, 8), None), ((512, 8, None), None), ((-1, 8, 8), None), ((512, 8, 8), 8)):

@@ -16,9 +16,9 @@ DEV = "cuda:0"
 
 
 def make_engine(selective=True, graph=False, B=3, max_len=512, full_layers=(0, 1), k=6, L=2, ratio=1.0,
-                n_layer=None, **backend_kw):
+                n_layer=None, dtype=torch.bfloat16, **backend_kw):
     from delta_amd.backend import LMBackend
-    eng = LMBackend(dtype=torch.bfloat16, device=DEV, cuda_graph_decode=graph, **backend_kw)
+    eng = LMBackend(dtype=dtype, device=DEV, cuda_graph_decode=graph, **backend_kw)
     eng.load_model("random:tiny-test", seed=1, **({} if n_layer is None else {"n_layer": n_layer}))
     cfg = eng.model.config
     cfg.enable_selective_cache = selective
@@ -46,9 +46,10 @@ def _csr(eng):
             sel.paged_subset_kv_indptr[:B + 1].cpu())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("lens", [[100, 257, 400], [300, 300, 300]])
-def test_decode_step_layers_match_oracle(lens):
-    eng = make_engine()
+def test_decode_step_layers_match_oracle(lens, dtype):
+    eng = make_engine(dtype=dtype)
     eng.prepare_synthetic_decode(lens, decode_budget=16, seed=3)
     for layer in eng.model.layers:
         layer.attention.record = []
@@ -113,9 +114,10 @@ def _restore(eng, snap):
     eng.sync_host_lens()
 
 
-@pytest.mark.parametrize("selective", [True, False])
-def test_graph_replays_match_eager_steps(selective):
-    eng = make_engine(selective=selective, graph=True, B=4)
+@pytest.mark.parametrize("selective,dtype", [(True, torch.bfloat16), (False, torch.bfloat16),
+                                             (True, torch.float16)], ids=["selective", "full", "selective_fp16"])
+def test_graph_replays_match_eager_steps(selective, dtype):
+    eng = make_engine(selective=selective, graph=True, B=4, dtype=dtype)
     eng.prepare_synthetic_decode([15, 16, 31, 200], decode_budget=40, seed=5)  # crosses page boundaries
     snap = _snapshot(eng)
     eager = []

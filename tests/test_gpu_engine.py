@@ -152,7 +152,8 @@ def test_partial_batch_idle_slots_untouched():
         assert all(p == scratch or p in set(owned.tolist()) for p in changed)
 
 
-def test_serving_loop_with_prefill():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_serving_loop_with_prefill(dtype):
     """Three requests through two slots (prefill, decode, a slot reused): every request gets
     its full output, every page returns to the pool, and the token streams are identical with
     the decode steps eager or replayed from the captured graph."""
@@ -160,7 +161,7 @@ def test_serving_loop_with_prefill():
     caps = [90, 80, 100]
     streams = []
     for graph in (False, True):
-        eng = make_engine(B=2, max_len=256, k=4, graph=graph)
+        eng = make_engine(B=2, max_len=256, k=4, graph=graph, dtype=dtype)
         eng.add_requests(prompts, caps, [])
         results = eng.run_scheduler_loop()
         assert len(results) == 3
@@ -199,10 +200,11 @@ def test_prefill_rows_are_causal():
     assert_close(o, ref, "prefill layer 0")
 
 
-def test_two_row_prefill_step_matches_oracle():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_two_row_prefill_step_matches_oracle(dtype):
     """One eager prompt step for two rows of different lengths: layer 0's attention output
     equals the oracle's causal prefill over each row's own pages."""
-    eng = make_engine(B=2, max_len=256)
+    eng = make_engine(B=2, max_len=256, dtype=dtype)
     for layer in eng.model.layers:
         layer.attention.record = []
     prompts = [torch.arange(1, 24), torch.arange(30, 39)]

@@ -141,6 +141,112 @@ def test_append_descriptor_errors_reported_without_launch(lib):
                   None, None, 0, 0, 1, 8, 8, 128, 0, 1.0, 1, None, 0, None)
 
 
+def _rejects(name, args, match):
+    from delta_amd import _lib
+    with pytest.raises(_lib.DeltaHipError, match=match):
+        _lib.call(name, *args)
+
+
+def test_empty_calls_return_before_touching_pointers(lib):
+    from delta_amd import _lib
+    # batch / row count 0: nothing to do, success, even with every pointer null
+    _lib.call("delta_paged_prefill", None, 0, 0, None, 0, None, None, None, 0, None, None, 0, 0, None,
+              0, 32, 8, 128, 0, 1.0, 0, None)
+    _lib.call("delta_append_kv", None, 0, None, 0, None, None, 0, None, 0, None, None, 0, 0, 8, 128, 0, None)
+    _lib.call("delta_rope", None, 0, None, 0, None, 0, None, 0, None, None, 0, 0, 32, 8, 128, 0,
+              1.0, 5e5, 0, 1.0, 4.0, 8192.0, None)
+    _lib.call("delta_pack_page_indices", None, 0, None, None, None, None, None, 0, None, 0, 16, 0, 0, None)
+    _lib.call("delta_page_scores_from_logits", None, 0, 0, None, None, None, None, 0, 0, 32, 16, None, 0, None)
+    _lib.call("delta_page_score", None, 0, 0, None, 0, None, None, 0, None, None, 0, 0, None, 0,
+              0, 32, 8, 128, 0, 1.0, 16, None, 0, None)
+    _lib.call("delta_select_pages", None, 0, None, None, 0, 0, 16, 4, None, 2, 1e-7, 0, None, None, 0, None, None)
+    _lib.call("delta_decode_page_info", None, None, None, 0, 16, 4, None, None, 1.0, 1,
+              None, None, None, None, None, None, None, None)
+
+
+def test_argument_errors_of_every_hot_path_entry_point(lib):
+    """Each entry point's first-line checks (reference behaviour: a RuntimeError naming the bad
+    argument) fire before anything touches the pointers; null pointers only, so the calls are
+    safe wherever they run."""
+    # causal prefill
+    pf = lambda hq, hkv, hd, dt, q=None: (q, 0, 0, None, 16, None, None, None, 0, None, None, 0, 0, None,
+                                           1, hq, hkv, hd, dt, 1.0, 4, None)
+    _rejects("delta_paged_prefill", pf(32, 8, 64, 0), "head_dim must be 128")
+    _rejects("delta_paged_prefill", pf(12, 8, 128, 0), "multiple of num_kv_heads")
+    _rejects("delta_paged_prefill", pf(72, 8, 128, 0), "group size 9 > 8")
+    _rejects("delta_paged_prefill", pf(32, 8, 128, 7), "bad dtype")
+    _rejects("delta_paged_prefill", pf(32, 8, 128, 0), "null pointer")
+    # KV append and RoPE
+    ak = lambda hd, dt: (None, 0, None, 0, None, None, 16, None, 0, None, None, 1, 1, 8, hd, dt, None)
+    _rejects("delta_append_kv", ak(64, 0), "head_dim must be 128")
+    _rejects("delta_append_kv", ak(128, 9), "bad dtype")
+    _rejects("delta_append_kv", ak(128, 1), "null pointer")
+    rp = lambda hd, dt: (None, 0, None, 0, None, 0, None, 0, None, None, 1, 1, 32, 8, hd, dt,
+                         1.0, 5e5, 0, 1.0, 4.0, 8192.0, None)
+    _rejects("delta_rope", rp(96, 0), "head_dim must be 128")
+    _rejects("delta_rope", rp(128, 3), "bad dtype")
+    _rejects("delta_rope", rp(128, 0), "null pointer")
+    # page-index packer (page_metadata.py:42-70)
+    _rejects("delta_pack_page_indices", (None, 4, None, None, None, None, None, 0, None, 2, 16, 8, 1, None),
+             "null pointer")
+    # page scores from a logits dump
+    sl = lambda dump, hq, sstride, dstride_h: (dump, 0, dstride_h, None, None, None, None, sstride, 2, hq, 16,
+                                               None, 0, None)
+    _rejects("delta_page_scores_from_logits", sl(None, 32, 16, 256), "null pointer")
+    # K-only scorer
+    ps = lambda scores, hq, hkv, sstride: (None, 0, 0, None, 16, None, None, 0, None, None, 0, 0, scores,
+                                          sstride, 2, hq, hkv, 128, 0, 1.0, 16, None, 0, None)
+    _rejects("delta_page_score", ps(None, 32, 8, 16), "null output pointer")
+    # selection
+    sp = lambda scores, sstride, bt_stride, mp, k, kpr, L, fixed: (scores, sstride, None, None, bt_stride, 2, mp, k,
+                                                                    kpr, L, 1e-7, fixed, None, None, 0, None, None)
+    _rejects("delta_select_pages", sp(None, 16, 16, 16, 4, None, 2, 0), "null pointer")
+    # decode metadata
+    _rejects("delta_decode_page_info", (None, None, None, 2, 16, 4, None, None, 1.0, 1,
+                                        None, None, None, None, None, None, None, None), "null pointer")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="stand-in addresses: validation-only, run where no GPU is visible")
+def test_argument_errors_past_the_null_checks(lib):
+    """The checks after the null-pointer ones, with non-null 256-byte aligned stand-in addresses
+    that are never dereferenced (each call fails validation before any launch)."""
+    A = 1 << 20  # stand-in address
+    _rejects("delta_paged_prefill", (A + 8, 1024, 128, A, 16, A, A, A, 16, A, A, 4096, 128, None,
+                                     1, 32, 8, 128, 0, 1.0, 4, None), "16-byte aligned")
+    _rejects("delta_paged_prefill", (A, 4096, 128, A, 16, A, A, A, 16, A, A + 2, 4096, 128, None,
+                                     1, 32, 8, 128, 0, 1.0, 4, None), "o 8-byte aligned")
+    _rejects("delta_paged_prefill", (A, 4096, 128, A, 0, A, A, A, 16, A, A, 4096, 128, None,
+                                     1, 32, 8, 128, 0, 1.0, 4, None), "empty cache")
+    _rejects("delta_append_kv", (A + 4, 1024, A, 1024, A, A, 16, A, 16, A, A, 1, 1, 8, 128, 0, None),
+             "16-byte aligned")
+    _rejects("delta_rope", (A, 4096, A, 1024, A, 4096, A, 1024, A, A, 1, 1, 32, 8, 128, 0,
+                            0.0, 5e5, 0, 1.0, 4.0, 8192.0, None), "bad rope params")
+    _rejects("delta_rope", (A, 4096, A, 1024, A, 4096, A, 1024, A, A, 1, 1, 32, 8, 128, 0,
+                            8.0, 5e5, 1, 4.0, 1.0, 8192.0, None), "llama3.1 frequency factors")
+    _rejects("delta_pack_page_indices", (A, 4, A, A, A, A, A, 64, None, 2, 16, 8, 1, None), "null row block table")
+    sl = lambda hq, sstride, dstride_h: (A, 32 * 256, dstride_h, None, A, A, A, sstride, 2, hq, 16, None, 0, None)
+    _rejects("delta_page_scores_from_logits", sl(0, 16, 256), r"num_qo_heads must be in \[1, 256\]")
+    _rejects("delta_page_scores_from_logits", sl(32, 8, 256), "score_stride < max_pages")
+    _rejects("delta_page_scores_from_logits", sl(32, 16, 255), "dump rows shorter than max_pages\\*16")
+    ps = lambda hq, hkv, sstride, dump=None, dstride_h=0, ws=None, wsb=0: (
+        A, 4096, 128, A, 16, A, A, 16, A, dump, 0, dstride_h, A, sstride, 2, hq, hkv, 128, 0, 1.0, 16, ws, wsb, None)
+    _rejects("delta_page_score", ps(300, 10, 16), "too many heads")
+    _rejects("delta_page_score", ps(12, 8, 16), "multiple of num_kv_heads")
+    _rejects("delta_page_score", ps(32, 8, 8), "score_stride < max_pages")
+    _rejects("delta_page_score", ps(32, 8, 16, dump=A, dstride_h=100), "dump rows shorter")
+    _rejects("delta_page_score", ps(32, 8, 16), "needs a logits dump buffer")  # 2 x 8 (row, kv head) pairs
+    _rejects("delta_page_score", ps(32, 8, 16, dump=A, dstride_h=256), "workspace of .* bytes needed")
+    sp = lambda sstride, bt_stride, mp, k, kpr, L, fixed: (A, sstride, A, A, bt_stride, 2, mp, k, kpr, L, 1e-7,
+                                                           fixed, None, A, 64, A, None)
+    _rejects("delta_select_pages", sp(16, 16, 0, 4, None, 2, 0), "max_pages must be positive")
+    _rejects("delta_select_pages", sp(8, 16, 16, 4, None, 2, 0), "row strides must be >= max_pages")
+    _rejects("delta_select_pages", sp(16, 16, 16, 4, A, 2, 1), "fixed_count needs a global k")
+    _rejects("delta_select_pages", sp(16, 16, 16, 4, None, -1, 0), "L must be >= 0")
+    pi = lambda pps, si, sip: (A, None, A, 2, pps, 4, None, None, 1.0, 1, A, A, A, None, si, sip, None, None)
+    _rejects("delta_decode_page_info", pi(0, None, None), "pages_per_slot <= 0")
+    _rejects("delta_decode_page_info", pi(16, A, None), "go together")
+
+
 def test_wrappers_reject_cpu_tensors():
     from delta_amd import kernels
     q = torch.zeros(1, 8, 128, dtype=torch.bfloat16)
